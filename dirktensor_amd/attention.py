@@ -1,0 +1,283 @@
+"""Python mirror of the reference's attention interfaces, on the HIP path.
+
+    flash_attention_forward(Q, K, V, scale, causal=True) -> FlashAttentionResult
+        FlashAttention.h:15-21 (returns output, softmax_m, softmax_l,
+        FlashAttention.h:6-10)
+    flash_attention_backward(...)
+        FlashAttention.h:33-43 -- raises: the GPU path is forward-only
+    OlmoAttention(folder, index) / OlmoAttention.from_weights(...)
+        OlmoAttention.h:10-42; forward(x) -> out
+    qk_norm_rope(q_proj, k_proj, q_norm_w, k_norm_w)
+        RMSNorm::forward (RMSNorm.cpp:15-22) for q_norm/k_norm + apply_rope
+        (OlmoAttention.cpp:111-146), fused
+
+Tensors may be torch tensors on a ROCm device (the call is stream-ordered on
+torch's current stream; fp32 selects the exact mode, bf16 the MFMA mode) or
+numpy arrays in host memory (copied in, computed and copied out
+synchronously, like the reference's value semantics). Everything runs in
+libdirktensor_amd.so; nothing here computes attention itself.
+"""
+
+from __future__ import annotations
+
+import ctypes
+from dataclasses import dataclass
+from typing import Optional
+
+import numpy as np
+
+from . import _capi as C
+
+try:  # torch is plumbing for device memory and streams only
+    import torch
+except Exception:  # pragma: no cover - torch is installed in every supported environment
+    torch = None
+
+
+class Context:
+    """Owns a dt_ctx (device binding, RoPE tables, rocBLAS handle, staging buffers)."""
+
+    def __init__(self, device: int = 0):
+        h = ctypes.c_void_p()
+        C.call("dt_ctx_create", int(device), ctypes.byref(h))
+        self.handle = h
+        self.device = int(device)
+
+    def close(self) -> None:
+        if self.handle:
+            C.lib().dt_ctx_destroy(self.handle)
+            self.handle = ctypes.c_void_p()
+
+    def __del__(self):  # pragma: no cover - interpreter teardown order
+        try:
+            self.close()
+        except Exception:
+            pass
+
+    def rope_table_init(self, theta: float, max_seq_len: int) -> None:
+        C.call("dt_rope_table_init", self.handle, float(theta), int(max_seq_len))
+
+
+_default_ctx: dict = {}
+
+
+def default_context(device: int = 0) -> Context:
+    ctx = _default_ctx.get(device)
+    if ctx is None:
+        ctx = Context(device)
+        _default_ctx[device] = ctx
+    return ctx
+
+
+@dataclass
+class FlashAttentionResult:
+    """FlashAttention.h:6-10: output [B,T,H,D], softmax_m and softmax_l [B,T,H]."""
+
+    output: object
+    softmax_m: object
+    softmax_l: object
+
+
+def _is_torch(x) -> bool:
+    return torch is not None and isinstance(x, torch.Tensor)
+
+
+def _mode_of(x, mode: Optional[str]) -> int:
+    if mode is not None:
+        if mode in ("fp32", "fp32_exact", "exact"):
+            return C.DT_FP32_EXACT
+        if mode == "bf16":
+            return C.DT_BF16
+        raise ValueError(f"unknown mode {mode!r}")
+    if _is_torch(x):
+        if x.dtype == torch.float32:
+            return C.DT_FP32_EXACT
+        if x.dtype == torch.bfloat16:
+            return C.DT_BF16
+        raise TypeError(f"unsupported dtype {x.dtype}: use float32 (exact mode) or bfloat16 (MFMA mode)")
+    if x.dtype == np.float32:
+        return C.DT_FP32_EXACT
+    if x.dtype == np.uint16:  # bf16 bit patterns
+        return C.DT_BF16
+    raise TypeError(f"unsupported numpy dtype {x.dtype}: float32, or uint16 holding bf16 bits")
+
+
+def _stream_of(t) -> ctypes.c_void_p:
+    return ctypes.c_void_p(torch.cuda.current_stream(t.device).cuda_stream)
+
+
+def _seq_lens_arg(seq_lens, B: int):
+    if seq_lens is None:
+        return None, None
+    arr = np.ascontiguousarray(np.asarray(seq_lens.cpu() if _is_torch(seq_lens) else seq_lens, dtype=np.int32))
+    if arr.shape != (B,):
+        raise ValueError(f"seq_lens must have shape ({B},), got {arr.shape}")
+    return arr, arr.ctypes.data_as(ctypes.c_void_p)
+
+
+def flash_attention_forward(Q, K, V, scale: float, causal: bool = True, *, seq_lens=None,
+                            mode: Optional[str] = None, ctx: Optional[Context] = None) -> FlashAttentionResult:
+    """Causal flash attention forward (FlashAttention.cpp:24-182) on the GPU.
+
+    Q, K, V: [B, T, H, 128], all torch device tensors or all numpy host arrays.
+    ``seq_lens`` (optional, B ints in [1, T]) masks keys at t >= seq_lens[b]
+    and returns rows t >= seq_lens[b] as the reference's empty row
+    (output 0, m = -inf, l = 0). Raises DTError on invalid arguments.
+    """
+    if Q.shape != K.shape or Q.shape != V.shape or len(Q.shape) != 4:
+        raise ValueError(f"Q, K, V must share one [B,T,H,D] shape, got {tuple(Q.shape)}, {tuple(K.shape)}, "
+                         f"{tuple(V.shape)}")
+    B, T, H, D = (int(s) for s in Q.shape)
+    dtype = _mode_of(Q, mode)
+    lens_arr, lens_p = _seq_lens_arg(seq_lens, B)
+    if _is_torch(Q):
+        if not (_is_torch(K) and _is_torch(V)):
+            raise TypeError("Q, K, V must all be torch tensors or all numpy arrays")
+        if not (Q.is_cuda and K.is_cuda and V.is_cuda):
+            raise ValueError("torch inputs must be on a ROCm device; use numpy arrays for host memory")
+        if Q.dtype != K.dtype or Q.dtype != V.dtype:
+            raise TypeError("Q, K, V must share one dtype")
+        ctx = ctx or default_context(Q.device.index or 0)
+        Q, K, V = Q.contiguous(), K.contiguous(), V.contiguous()
+        O = torch.empty_like(Q)
+        m = torch.empty((B, T, H), dtype=torch.float32, device=Q.device)
+        l = torch.empty((B, T, H), dtype=torch.float32, device=Q.device)
+        C.call("dt_flash_attn_fwd", ctx.handle, Q.data_ptr(), K.data_ptr(), V.data_ptr(), O.data_ptr(),
+               m.data_ptr(), l.data_ptr(), B, T, H, D, float(scale), int(bool(causal)), lens_p, dtype,
+               C.DT_MEM_DEVICE, _stream_of(Q))
+        return FlashAttentionResult(O, m, l)
+    ctx = ctx or default_context(0)
+    np_dt = np.float32 if dtype == C.DT_FP32_EXACT else np.uint16
+    Qh, Kh, Vh = (np.ascontiguousarray(x, dtype=np_dt) for x in (Q, K, V))
+    O = np.empty_like(Qh)
+    m = np.empty((B, T, H), dtype=np.float32)
+    l = np.empty((B, T, H), dtype=np.float32)
+    C.call("dt_flash_attn_fwd", ctx.handle, Qh.ctypes.data, Kh.ctypes.data, Vh.ctypes.data, O.ctypes.data,
+           m.ctypes.data, l.ctypes.data, B, T, H, D, float(scale), int(bool(causal)), lens_p, dtype,
+           C.DT_MEM_HOST, None)
+    return FlashAttentionResult(O, m, l)
+
+
+def flash_attention_backward(d_output, output, softmax_m, softmax_l, Q, K, V, scale: float, causal: bool = True):
+    """FlashAttention.h:33-43. The GPU path is forward-only: this raises DTError (NOT_IMPLEMENTED)."""
+    ctx = default_context(0)
+    C.call("dt_flash_attn_bwd", ctx.handle, None, None, None, None, None, None, None, None, None, None,
+           0, 0, 0, 0, float(scale), int(bool(causal)), C.DT_FP32_EXACT, C.DT_MEM_DEVICE, None)
+
+
+def qk_norm_rope(q_proj, k_proj, q_norm_w, k_norm_w, *, n_heads: int = C.N_HEADS, out_dtype: str = "fp32",
+                 return_rms: bool = False, ctx: Optional[Context] = None):
+    """Fused q/k RMSNorm over all d_model features + rotate-half RoPE at position t.
+
+    q_proj, k_proj: [B, T, d_model] fp32; returns q, k as [B, T, H, 128]
+    (fp32, or bf16 when out_dtype == "bf16"), plus the two [B, T] rms arrays
+    when ``return_rms``.
+    """
+    B, T, dm = (int(s) for s in q_proj.shape)
+    H = n_heads
+    od = C.DT_BF16 if out_dtype == "bf16" else C.DT_FP32_EXACT
+    if _is_torch(q_proj):
+        ctx = ctx or default_context(q_proj.device.index or 0)
+        q_in, k_in = q_proj.contiguous(), k_proj.contiguous()
+        tdt = torch.bfloat16 if od == C.DT_BF16 else torch.float32
+        q_out = torch.empty((B, T, H, dm // H), dtype=tdt, device=q_in.device)
+        k_out = torch.empty_like(q_out)
+        q_rms = torch.empty((B, T), dtype=torch.float32, device=q_in.device)
+        k_rms = torch.empty_like(q_rms)
+        C.call("dt_qk_norm_rope_fwd", ctx.handle, q_in.data_ptr(), k_in.data_ptr(), q_norm_w.contiguous().data_ptr(),
+               k_norm_w.contiguous().data_ptr(), q_out.data_ptr(), k_out.data_ptr(), q_rms.data_ptr(),
+               k_rms.data_ptr(), B, T, H, dm // H, dm, dm, od, C.DT_MEM_DEVICE, _stream_of(q_in))
+    else:
+        ctx = ctx or default_context(0)
+        q_in = np.ascontiguousarray(q_proj, dtype=np.float32)
+        k_in = np.ascontiguousarray(k_proj, dtype=np.float32)
+        qw = np.ascontiguousarray(q_norm_w, dtype=np.float32)
+        kw = np.ascontiguousarray(k_norm_w, dtype=np.float32)
+        ndt = np.uint16 if od == C.DT_BF16 else np.float32
+        q_out = np.empty((B, T, H, dm // H), dtype=ndt)
+        k_out = np.empty_like(q_out)
+        q_rms = np.empty((B, T), dtype=np.float32)
+        k_rms = np.empty_like(q_rms)
+        C.call("dt_qk_norm_rope_fwd", ctx.handle, q_in.ctypes.data, k_in.ctypes.data, qw.ctypes.data,
+               kw.ctypes.data, q_out.ctypes.data, k_out.ctypes.data, q_rms.ctypes.data, k_rms.ctypes.data,
+               B, T, H, dm // H, dm, dm, od, C.DT_MEM_HOST, None)
+    if return_rms:
+        return q_out, k_out, q_rms, k_rms
+    return q_out, k_out
+
+
+class OlmoAttention:
+    """OlmoAttention (OlmoAttention.h:10-42) on the HIP path.
+
+    ``OlmoAttention(folder, index)`` loads the reference's per-layer .npy files
+    (OlmoAttention.cpp:39-53); ``OlmoAttention.from_weights`` takes arrays
+    (fp32, [out, in] like torch Linear). ``forward(x)`` maps [B, T, d_model]
+    fp32 to [B, T, d_model] fp32 (OlmoAttention.cpp:56-108). backward, step and
+    zero_grad raise: the GPU path is forward-only.
+    """
+
+    def __init__(self, folder: Optional[str] = None, index: int = 0, *, ctx: Optional[Context] = None,
+                 _handle: Optional[ctypes.c_void_p] = None):
+        self.ctx = ctx or default_context(0)
+        if _handle is not None:
+            self.handle = _handle
+            return
+        if folder is None:
+            raise ValueError("OlmoAttention needs a weights folder (or use OlmoAttention.from_weights)")
+        h = ctypes.c_void_p()
+        C.call("dt_attn_layer_load", self.ctx.handle, str(folder).encode(), int(index), ctypes.byref(h))
+        self.handle = h
+
+    @classmethod
+    def from_weights(cls, wq, wk, wv, wo, q_norm, k_norm, *, ctx: Optional[Context] = None) -> "OlmoAttention":
+        ctx = ctx or default_context(0)
+        dm = int(wq.shape[0])
+        h = ctypes.c_void_p()
+        if _is_torch(wq):
+            ws = [w.contiguous().float() for w in (wq, wk, wv, wo, q_norm, k_norm)]
+            C.call("dt_attn_layer_create", ctx.handle, *[w.data_ptr() for w in ws], dm, dm // C.HEAD_DIM,
+                   C.DT_MEM_DEVICE, ctypes.byref(h))
+            torch.cuda.synchronize(ws[0].device)
+        else:
+            ws = [np.ascontiguousarray(w, dtype=np.float32) for w in (wq, wk, wv, wo, q_norm, k_norm)]
+            C.call("dt_attn_layer_create", ctx.handle, *[w.ctypes.data for w in ws], dm, dm // C.HEAD_DIM,
+                   C.DT_MEM_HOST, ctypes.byref(h))
+        return cls(ctx=ctx, _handle=h)
+
+    def close(self) -> None:
+        if getattr(self, "handle", None):
+            C.lib().dt_attn_layer_destroy(self.handle)
+            self.handle = None
+
+    def __del__(self):  # pragma: no cover
+        try:
+            self.close()
+        except Exception:
+            pass
+
+    def forward(self, x, *, seq_lens=None, mode: str = "fp32"):
+        B, T, dm = (int(s) for s in x.shape)
+        dtype = _mode_of(x, mode)
+        lens_arr, lens_p = _seq_lens_arg(seq_lens, B)
+        if _is_torch(x):
+            xi = x.contiguous().float()
+            out = torch.empty_like(xi)
+            C.call("dt_attn_layer_fwd", self.handle, xi.data_ptr(), out.data_ptr(), B, T, lens_p, dtype,
+                   C.DT_MEM_DEVICE, _stream_of(xi))
+            return out
+        xi = np.ascontiguousarray(x, dtype=np.float32)
+        out = np.empty_like(xi)
+        C.call("dt_attn_layer_fwd", self.handle, xi.ctypes.data, out.ctypes.data, B, T, lens_p, dtype,
+               C.DT_MEM_HOST, None)
+        return out
+
+    __call__ = forward
+
+    def backward(self, d_output):
+        C.call("dt_attn_layer_bwd", self.handle, None, None, 0, 0, C.DT_MEM_DEVICE, None)
+
+    def step(self, lr: float):
+        raise NotImplementedError("OlmoAttention.step: the GPU path is forward-only (no gradients are kept)")
+
+    def zero_grad(self):
+        raise NotImplementedError("OlmoAttention.zero_grad: the GPU path is forward-only (no gradients are kept)")

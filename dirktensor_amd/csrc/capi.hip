@@ -1,0 +1,538 @@
+// C ABI of the attention path: argument validation, context, host-memory
+// staging and the OlmoAttention layer orchestration (projections on rocBLAS,
+// norm + RoPE and the attention core on this library's kernels).
+//
+// Every entry point validates all arguments before its first HIP call, so an
+// invalid call returns a status without touching the device (the reference's
+// shape checks are compiled-out asserts, CMakeLists.txt:68, and T > 8192 is
+// undefined behaviour there, OlmoAttention.cpp:129).
+
+#include <rocblas/rocblas.h>
+
+#include <cmath>
+#include <cstdarg>
+#include <cstdio>
+#include <cstring>
+#include <string>
+#include <vector>
+
+#include "dt_internal.h"
+
+namespace dt {
+
+static thread_local std::string t_err;
+
+int set_error(int code, const char* fmt, ...) {
+    char buf[1024];
+    va_list ap;
+    va_start(ap, fmt);
+    vsnprintf(buf, sizeof buf, fmt, ap);
+    va_end(ap);
+    t_err = buf;
+    return code;
+}
+
+void clear_error() { t_err.clear(); }
+
+int DeviceBuffer::ensure(size_t need) {
+    if (need <= bytes) return DT_OK;
+    if (ptr) {
+        DT_HIP_TRY(hipFree(ptr));
+        ptr = nullptr;
+        bytes = 0;
+    }
+    size_t sz = (need + 255) & ~size_t(255);
+    DT_HIP_TRY(hipMalloc(&ptr, sz));
+    bytes = sz;
+    return DT_OK;
+}
+
+void DeviceBuffer::release() {
+    if (ptr) (void)hipFree(ptr);
+    ptr = nullptr;
+    bytes = 0;
+}
+
+static bool aligned16(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15) == 0; }
+
+static int check_device_binding(dt_ctx* ctx) {
+    DT_HIP_TRY(hipSetDevice(ctx->device));
+    return DT_OK;
+}
+
+static int rope_upload(dt_ctx* ctx, float theta, int max_seq_len) {
+    // compute_rope_buffers, OlmoAttention.cpp:18-31: fp64 inv_freq and angles, fp32 tables.
+    const int half = DT_HEAD_DIM / 2;
+    std::vector<float> cs((size_t)max_seq_len * half), sn((size_t)max_seq_len * half);
+    std::vector<double> inv(half);
+    for (int i = 0; i < half; ++i) inv[i] = 1.0 / std::pow((double)theta, (double)(2 * i) / (double)DT_HEAD_DIM);
+    for (int p = 0; p < max_seq_len; ++p)
+        for (int i = 0; i < half; ++i) {
+            const double ang = (double)p * inv[i];
+            cs[(size_t)p * half + i] = (float)std::cos(ang);
+            sn[(size_t)p * half + i] = (float)std::sin(ang);
+        }
+    if (ctx->rope_cos) DT_HIP_TRY(hipFree(ctx->rope_cos));
+    if (ctx->rope_sin) DT_HIP_TRY(hipFree(ctx->rope_sin));
+    ctx->rope_cos = ctx->rope_sin = nullptr;
+    ctx->rope_len = 0;
+    DT_HIP_TRY(hipMalloc(&ctx->rope_cos, cs.size() * sizeof(float)));
+    DT_HIP_TRY(hipMalloc(&ctx->rope_sin, sn.size() * sizeof(float)));
+    DT_HIP_TRY(hipMemcpy(ctx->rope_cos, cs.data(), cs.size() * sizeof(float), hipMemcpyHostToDevice));
+    DT_HIP_TRY(hipMemcpy(ctx->rope_sin, sn.data(), sn.size() * sizeof(float), hipMemcpyHostToDevice));
+    ctx->rope_len = max_seq_len;
+    ctx->rope_theta = theta;
+    return DT_OK;
+}
+
+static int validate_seq_lens(const int32_t* seq_lens, int B, int T) {
+    if (!seq_lens) return DT_OK;
+    if (B > kMaxRaggedBatch)
+        return set_error(DT_ERR_UNSUPPORTED, "seq_lens given with B=%d > %d", B, kMaxRaggedBatch);
+    for (int b = 0; b < B; ++b)
+        if (seq_lens[b] < 1 || seq_lens[b] > T)
+            return set_error(DT_ERR_INVALID_ARG, "seq_lens[%d]=%d outside [1, T=%d]", b, seq_lens[b], T);
+    return DT_OK;
+}
+
+static int run_flash(dt_ctx* ctx, const FlashArgs& fa, const int32_t* seq_lens, int dtype, hipStream_t s) {
+    (void)ctx;
+    SeqLens sl;
+    const SeqLens* lp = nullptr;
+    if (seq_lens) {
+        std::memcpy(sl.len, seq_lens, sizeof(int32_t) * fa.B);
+        lp = &sl;
+    }
+    return dtype == DT_BF16 ? launch_flash_fwd_bf16(fa, lp, s) : launch_flash_fwd_f32(fa, lp, s);
+}
+
+// ---------------- rocBLAS helpers ----------------
+static const char* blas_status_str(rocblas_status st) { return rocblas_status_to_string(st); }
+
+static int ensure_blas(dt_ctx* ctx) {
+    if (ctx->blas) return DT_OK;
+    rocblas_handle h = nullptr;
+    rocblas_status st = rocblas_create_handle(&h);
+    if (st != rocblas_status_success) return set_error(DT_ERR_BLAS, "rocblas_create_handle: %s", blas_status_str(st));
+    ctx->blas = h;
+    return DT_OK;
+}
+
+// Row-major C[M][N] = A[M][K] * W[N][K]^T (y = x W^T). In rocBLAS's column-major
+// terms this is C^T (N x M) = W (N x K, i.e. op(T) of the K x N col-major view) * A^T.
+static int gemm_xwt(dt_ctx* ctx, hipStream_t s, int M, int N, int K, const void* A, int lda, const void* W, int ldw,
+                    float* C, int ldc, bool bf16_in) {
+    DT_TRY(ensure_blas(ctx));
+    rocblas_handle h = static_cast<rocblas_handle>(ctx->blas);
+    rocblas_set_stream(h, s);
+    const float one = 1.0f, zero = 0.0f;
+    rocblas_status st;
+    if (!bf16_in) {
+        st = rocblas_sgemm(h, rocblas_operation_transpose, rocblas_operation_none, N, M, K, &one,
+                           static_cast<const float*>(W), ldw, static_cast<const float*>(A), lda, &zero, C, ldc);
+    } else {
+        st = rocblas_gemm_ex(h, rocblas_operation_transpose, rocblas_operation_none, N, M, K, &one, W,
+                             rocblas_datatype_bf16_r, ldw, A, rocblas_datatype_bf16_r, lda, &zero, C,
+                             rocblas_datatype_f32_r, ldc, C, rocblas_datatype_f32_r, ldc, rocblas_datatype_f32_r,
+                             rocblas_gemm_algo_standard, 0, 0);
+    }
+    if (st != rocblas_status_success) return set_error(DT_ERR_BLAS, "rocBLAS GEMM (%d x %d x %d): %s", M, N, K,
+                                                       blas_status_str(st));
+    return DT_OK;
+}
+
+// ---------------- .npy reader (v1/v2/v3, little-endian fp32, C order) ----------------
+static int read_npy_f32(const std::string& path, std::vector<float>& out, std::vector<size_t>& shape) {
+    FILE* f = std::fopen(path.c_str(), "rb");
+    if (!f) return set_error(DT_ERR_IO, "cannot open %s", path.c_str());
+    unsigned char magic[8];
+    if (std::fread(magic, 1, 8, f) != 8 || std::memcmp(magic, "\x93NUMPY", 6) != 0) {
+        std::fclose(f);
+        return set_error(DT_ERR_IO, "%s is not a .npy file (a Git-LFS pointer?)", path.c_str());
+    }
+    uint32_t hlen = 0;
+    if (magic[6] == 1) {
+        unsigned char b[2];
+        if (std::fread(b, 1, 2, f) != 2) { std::fclose(f); return set_error(DT_ERR_IO, "%s: truncated", path.c_str()); }
+        hlen = b[0] | (b[1] << 8);
+    } else {
+        unsigned char b[4];
+        if (std::fread(b, 1, 4, f) != 4) { std::fclose(f); return set_error(DT_ERR_IO, "%s: truncated", path.c_str()); }
+        hlen = b[0] | (b[1] << 8) | (b[2] << 16) | ((uint32_t)b[3] << 24);
+    }
+    std::string hdr(hlen, '\0');
+    if (std::fread(&hdr[0], 1, hlen, f) != hlen) { std::fclose(f); return set_error(DT_ERR_IO, "%s: truncated", path.c_str()); }
+    if (hdr.find("'<f4'") == std::string::npos || hdr.find("'fortran_order': False") == std::string::npos) {
+        std::fclose(f);
+        return set_error(DT_ERR_IO, "%s: need little-endian float32 in C order, header %s", path.c_str(), hdr.c_str());
+    }
+    size_t p = hdr.find("'shape': (");
+    if (p == std::string::npos) { std::fclose(f); return set_error(DT_ERR_IO, "%s: no shape", path.c_str()); }
+    p += 10;
+    shape.clear();
+    size_t n = 1;
+    while (p < hdr.size() && hdr[p] != ')') {
+        while (p < hdr.size() && (hdr[p] == ' ' || hdr[p] == ',')) ++p;
+        if (p < hdr.size() && hdr[p] == ')') break;
+        size_t v = 0;
+        bool any = false;
+        while (p < hdr.size() && hdr[p] >= '0' && hdr[p] <= '9') { v = v * 10 + (hdr[p] - '0'); ++p; any = true; }
+        if (!any) { std::fclose(f); return set_error(DT_ERR_IO, "%s: bad shape", path.c_str()); }
+        shape.push_back(v);
+        n *= v;
+    }
+    out.resize(n);
+    if (std::fread(out.data(), sizeof(float), n, f) != n) {
+        std::fclose(f);
+        return set_error(DT_ERR_IO, "%s: truncated data", path.c_str());
+    }
+    std::fclose(f);
+    return DT_OK;
+}
+
+}  // namespace dt
+
+// ---------------- layer ----------------
+struct dt_attn_layer {
+    dt_ctx* ctx = nullptr;
+    int d_model = 0, n_heads = 0;
+    float* w_qkv = nullptr;      // [3*d_model][d_model] fp32 (q rows, k rows, v rows)
+    float* w_o = nullptr;        // [d_model][d_model]
+    uint16_t* w_qkv16 = nullptr; // bf16 copies, made on first bf16 forward
+    uint16_t* w_o16 = nullptr;
+    float* q_norm = nullptr;
+    float* k_norm = nullptr;
+    dt::DeviceBuffer qkv32, qkv16, attn, x16;
+};
+
+using namespace dt;
+
+extern "C" {
+
+const char* dt_last_error(void) { return t_err.c_str(); }
+
+int dt_version(void) { return 1; }
+
+int dt_ctx_create(int device, dt_ctx** out) {
+    clear_error();
+    if (!out) return set_error(DT_ERR_INVALID_ARG, "out is NULL");
+    *out = nullptr;
+    if (device < 0) return set_error(DT_ERR_INVALID_ARG, "device %d < 0", device);
+    int count = 0;
+    DT_HIP_TRY(hipGetDeviceCount(&count));
+    if (device >= count) return set_error(DT_ERR_INVALID_ARG, "device %d >= device count %d", device, count);
+    DT_HIP_TRY(hipSetDevice(device));
+    dt_ctx* c = new dt_ctx();
+    c->device = device;
+    int rc = rope_upload(c, DT_ROPE_THETA, DT_MAX_SEQ_LEN);
+    if (rc != DT_OK) {
+        delete c;
+        return rc;
+    }
+    *out = c;
+    return DT_OK;
+}
+
+int dt_ctx_destroy(dt_ctx* ctx) {
+    clear_error();
+    if (!ctx) return DT_OK;
+    (void)hipSetDevice(ctx->device);
+    if (ctx->rope_cos) (void)hipFree(ctx->rope_cos);
+    if (ctx->rope_sin) (void)hipFree(ctx->rope_sin);
+    for (auto& b : ctx->stage) b.release();
+    if (ctx->blas) rocblas_destroy_handle(static_cast<rocblas_handle>(ctx->blas));
+    delete ctx;
+    return DT_OK;
+}
+
+int dt_rope_table_init(dt_ctx* ctx, float theta, int max_seq_len) {
+    clear_error();
+    if (!ctx) return set_error(DT_ERR_INVALID_ARG, "ctx is NULL");
+    if (!(theta > 1.0f) || !std::isfinite(theta)) return set_error(DT_ERR_INVALID_ARG, "theta %g must be > 1", theta);
+    if (max_seq_len < 1 || max_seq_len > (1 << 20))
+        return set_error(DT_ERR_INVALID_ARG, "max_seq_len %d outside [1, 2^20]", max_seq_len);
+    DT_TRY(check_device_binding(ctx));
+    return rope_upload(ctx, theta, max_seq_len);
+}
+
+int dt_flash_attn_fwd(dt_ctx* ctx, const void* q, const void* k, const void* v, void* o, float* m, float* l, int B,
+                      int T, int H, int D, float scale, int causal, const int32_t* seq_lens, int dtype, int mem,
+                      void* stream) {
+    clear_error();
+    if (!q || !k || !v || !o) return set_error(DT_ERR_INVALID_ARG, "q, k, v and o must be non-NULL");
+    if (D != DT_HEAD_DIM) return set_error(DT_ERR_UNSUPPORTED, "head_dim D=%d, kernels are built for D=%d", D, DT_HEAD_DIM);
+    if (B < 1 || H < 1 || T < 1) return set_error(DT_ERR_INVALID_ARG, "B=%d, T=%d, H=%d must be >= 1", B, T, H);
+    if (T > DT_MAX_SEQ_LEN) return set_error(DT_ERR_INVALID_ARG, "T=%d exceeds max_seq_len %d", T, DT_MAX_SEQ_LEN);
+    if (H > 65535 || B > 65535) return set_error(DT_ERR_UNSUPPORTED, "B=%d or H=%d exceeds grid limits", B, H);
+    if (dtype != DT_FP32_EXACT && dtype != DT_BF16) return set_error(DT_ERR_INVALID_ARG, "unknown dtype %d", dtype);
+    if (mem != DT_MEM_DEVICE && mem != DT_MEM_HOST) return set_error(DT_ERR_INVALID_ARG, "unknown mem %d", mem);
+    if (!(scale > 0.0f) || !std::isfinite(scale)) return set_error(DT_ERR_INVALID_ARG, "scale %g must be finite and > 0", scale);
+    if (causal != 0 && causal != 1) return set_error(DT_ERR_INVALID_ARG, "causal must be 0 or 1");
+    if (mem == DT_MEM_DEVICE && (!aligned16(q) || !aligned16(k) || !aligned16(v) || !aligned16(o)))
+        return set_error(DT_ERR_INVALID_ARG, "device q/k/v/o must be 16-byte aligned");
+    DT_TRY(validate_seq_lens(seq_lens, B, T));
+    if (!ctx) return set_error(DT_ERR_INVALID_ARG, "ctx is NULL");
+    DT_TRY(check_device_binding(ctx));
+
+    hipStream_t s = static_cast<hipStream_t>(stream);
+    const int ld = H * D;
+    FlashArgs fa{q, k, v, o, m, l, B, T, H, ld, ld, ld, ld, scale, causal, seq_lens ? 1 : 0};
+    if (mem == DT_MEM_DEVICE) return run_flash(ctx, fa, seq_lens, dtype, s);
+
+    // host memory: stage through context buffers, synchronous like the reference
+    const size_t esz = dtype == DT_BF16 ? 2 : 4;
+    const size_t nel = (size_t)B * T * H * D;
+    const size_t nst = (size_t)B * T * H;
+    for (int i = 0; i < 4; ++i) DT_TRY(ctx->stage[i].ensure(nel * esz));
+    DT_TRY(ctx->stage[4].ensure(nst * sizeof(float)));
+    DT_TRY(ctx->stage[5].ensure(nst * sizeof(float)));
+    DT_HIP_TRY(hipMemcpyAsync(ctx->stage[0].ptr, q, nel * esz, hipMemcpyHostToDevice, s));
+    DT_HIP_TRY(hipMemcpyAsync(ctx->stage[1].ptr, k, nel * esz, hipMemcpyHostToDevice, s));
+    DT_HIP_TRY(hipMemcpyAsync(ctx->stage[2].ptr, v, nel * esz, hipMemcpyHostToDevice, s));
+    FlashArgs fd = fa;
+    fd.q = ctx->stage[0].ptr;
+    fd.k = ctx->stage[1].ptr;
+    fd.v = ctx->stage[2].ptr;
+    fd.o = ctx->stage[3].ptr;
+    fd.m = m ? static_cast<float*>(ctx->stage[4].ptr) : nullptr;
+    fd.l = l ? static_cast<float*>(ctx->stage[5].ptr) : nullptr;
+    DT_TRY(run_flash(ctx, fd, seq_lens, dtype, s));
+    DT_HIP_TRY(hipMemcpyAsync(o, fd.o, nel * esz, hipMemcpyDeviceToHost, s));
+    if (m) DT_HIP_TRY(hipMemcpyAsync(m, fd.m, nst * sizeof(float), hipMemcpyDeviceToHost, s));
+    if (l) DT_HIP_TRY(hipMemcpyAsync(l, fd.l, nst * sizeof(float), hipMemcpyDeviceToHost, s));
+    DT_HIP_TRY(hipStreamSynchronize(s));
+    return DT_OK;
+}
+
+int dt_flash_attn_bwd(dt_ctx*, const void*, const void*, const float*, const float*, const void*, const void*,
+                      const void*, void*, void*, void*, int, int, int, int, float, int, int, int, void*) {
+    clear_error();
+    return set_error(DT_ERR_NOT_IMPLEMENTED,
+                     "flash_attention_backward is not implemented on the GPU path (forward-only prefill)");
+}
+
+int dt_qk_norm_rope_fwd(dt_ctx* ctx, const float* q_in, const float* k_in, const float* q_norm_w,
+                        const float* k_norm_w, void* q_out, void* k_out, float* q_rms, float* k_rms, int B, int T,
+                        int H, int D, int ld_in, int ld_out, int out_dtype, int mem, void* stream) {
+    clear_error();
+    if (!q_in || !k_in || !q_norm_w || !k_norm_w || !q_out || !k_out)
+        return set_error(DT_ERR_INVALID_ARG, "q_in, k_in, norm weights, q_out and k_out must be non-NULL");
+    if (D != DT_HEAD_DIM) return set_error(DT_ERR_UNSUPPORTED, "head_dim D=%d, kernels are built for D=%d", D, DT_HEAD_DIM);
+    if (B < 1 || T < 1 || H < 1 || H > 256) return set_error(DT_ERR_INVALID_ARG, "B=%d, T=%d, H=%d out of range", B, T, H);
+    if ((int64_t)B * T > 0x7fffffff) return set_error(DT_ERR_UNSUPPORTED, "B*T too large");
+    if (ld_in < H * D || ld_out < H * D || (ld_in & 3) || (ld_out & 3))
+        return set_error(DT_ERR_INVALID_ARG, "row strides ld_in=%d / ld_out=%d must be >= H*D=%d and multiples of 4",
+                         ld_in, ld_out, H * D);
+    if (out_dtype != DT_FP32_EXACT && out_dtype != DT_BF16) return set_error(DT_ERR_INVALID_ARG, "unknown dtype %d", out_dtype);
+    if (mem != DT_MEM_DEVICE && mem != DT_MEM_HOST) return set_error(DT_ERR_INVALID_ARG, "unknown mem %d", mem);
+    if (mem == DT_MEM_DEVICE && (!aligned16(q_in) || !aligned16(k_in) || !aligned16(q_out) || !aligned16(k_out) ||
+                                 !aligned16(q_norm_w) || !aligned16(k_norm_w)))
+        return set_error(DT_ERR_INVALID_ARG, "device pointers must be 16-byte aligned");
+    if (T > DT_MAX_SEQ_LEN) return set_error(DT_ERR_INVALID_ARG, "T=%d exceeds max_seq_len %d", T, DT_MAX_SEQ_LEN);
+    if (!ctx) return set_error(DT_ERR_INVALID_ARG, "ctx is NULL");
+    if (T > ctx->rope_len) return set_error(DT_ERR_INVALID_ARG, "T=%d exceeds the RoPE table length %d", T, ctx->rope_len);
+    DT_TRY(check_device_binding(ctx));
+    hipStream_t s = static_cast<hipStream_t>(stream);
+    const int rows = B * T;
+    NormRopeArgs na{q_in, k_in, nullptr, q_norm_w, k_norm_w, q_out, k_out, nullptr, q_rms, k_rms,
+                    ctx->rope_cos, ctx->rope_sin, rows, T, H, ld_in, ld_out, DT_RMS_EPS};
+    if (mem == DT_MEM_DEVICE) return launch_qk_norm_rope(na, out_dtype == DT_BF16, s);
+
+    const size_t esz = out_dtype == DT_BF16 ? 2 : 4;
+    const size_t in_bytes = (size_t)rows * ld_in * 4, out_bytes = (size_t)rows * ld_out * esz;
+    const size_t w_bytes = (size_t)H * D * 4;
+    DT_TRY(ctx->stage[0].ensure(in_bytes));
+    DT_TRY(ctx->stage[1].ensure(in_bytes));
+    DT_TRY(ctx->stage[2].ensure(out_bytes));
+    DT_TRY(ctx->stage[3].ensure(out_bytes));
+    DT_TRY(ctx->stage[4].ensure(2 * w_bytes));
+    DT_TRY(ctx->stage[5].ensure(2 * (size_t)rows * 4));
+    char* wbuf = static_cast<char*>(ctx->stage[4].ptr);
+    float* rbuf = static_cast<float*>(ctx->stage[5].ptr);
+    DT_HIP_TRY(hipMemcpyAsync(ctx->stage[0].ptr, q_in, in_bytes, hipMemcpyHostToDevice, s));
+    DT_HIP_TRY(hipMemcpyAsync(ctx->stage[1].ptr, k_in, in_bytes, hipMemcpyHostToDevice, s));
+    DT_HIP_TRY(hipMemcpyAsync(wbuf, q_norm_w, w_bytes, hipMemcpyHostToDevice, s));
+    DT_HIP_TRY(hipMemcpyAsync(wbuf + w_bytes, k_norm_w, w_bytes, hipMemcpyHostToDevice, s));
+    NormRopeArgs nd = na;
+    nd.q_in = static_cast<const float*>(ctx->stage[0].ptr);
+    nd.k_in = static_cast<const float*>(ctx->stage[1].ptr);
+    nd.q_w = reinterpret_cast<const float*>(wbuf);
+    nd.k_w = reinterpret_cast<const float*>(wbuf + w_bytes);
+    nd.q_out = ctx->stage[2].ptr;
+    nd.k_out = ctx->stage[3].ptr;
+    nd.q_rms = q_rms ? rbuf : nullptr;
+    nd.k_rms = k_rms ? rbuf + rows : nullptr;
+    DT_TRY(launch_qk_norm_rope(nd, out_dtype == DT_BF16, s));
+    DT_HIP_TRY(hipMemcpyAsync(q_out, nd.q_out, out_bytes, hipMemcpyDeviceToHost, s));
+    DT_HIP_TRY(hipMemcpyAsync(k_out, nd.k_out, out_bytes, hipMemcpyDeviceToHost, s));
+    if (q_rms) DT_HIP_TRY(hipMemcpyAsync(q_rms, rbuf, rows * 4, hipMemcpyDeviceToHost, s));
+    if (k_rms) DT_HIP_TRY(hipMemcpyAsync(k_rms, rbuf + rows, rows * 4, hipMemcpyDeviceToHost, s));
+    DT_HIP_TRY(hipStreamSynchronize(s));
+    return DT_OK;
+}
+
+int dt_attn_layer_create(dt_ctx* ctx, const float* wq, const float* wk, const float* wv, const float* wo,
+                         const float* q_norm_w, const float* k_norm_w, int d_model, int n_heads, int mem,
+                         dt_attn_layer** out) {
+    clear_error();
+    if (!out) return set_error(DT_ERR_INVALID_ARG, "out is NULL");
+    *out = nullptr;
+    if (!wq || !wk || !wv || !wo || !q_norm_w || !k_norm_w) return set_error(DT_ERR_INVALID_ARG, "weights must be non-NULL");
+    if (n_heads < 1 || n_heads > 256 || d_model != n_heads * DT_HEAD_DIM)
+        return set_error(DT_ERR_UNSUPPORTED, "d_model=%d must equal n_heads (%d) * %d", d_model, n_heads, DT_HEAD_DIM);
+    if (mem != DT_MEM_DEVICE && mem != DT_MEM_HOST) return set_error(DT_ERR_INVALID_ARG, "unknown mem %d", mem);
+    if (!ctx) return set_error(DT_ERR_INVALID_ARG, "ctx is NULL");
+    DT_TRY(check_device_binding(ctx));
+    dt_attn_layer* L = new dt_attn_layer();
+    L->ctx = ctx;
+    L->d_model = d_model;
+    L->n_heads = n_heads;
+    const size_t wsz = (size_t)d_model * d_model * sizeof(float);
+    const hipMemcpyKind kind = mem == DT_MEM_HOST ? hipMemcpyHostToDevice : hipMemcpyDeviceToDevice;
+    auto fail = [&](int rc) {
+        dt_attn_layer_destroy(L);
+        return rc;
+    };
+    hipError_t e = hipMalloc(&L->w_qkv, 3 * wsz);
+    if (e == hipSuccess) e = hipMalloc(&L->w_o, wsz);
+    if (e == hipSuccess) e = hipMalloc(&L->q_norm, d_model * sizeof(float));
+    if (e == hipSuccess) e = hipMalloc(&L->k_norm, d_model * sizeof(float));
+    if (e == hipSuccess) e = hipMemcpy(L->w_qkv, wq, wsz, kind);
+    if (e == hipSuccess) e = hipMemcpy(reinterpret_cast<char*>(L->w_qkv) + wsz, wk, wsz, kind);
+    if (e == hipSuccess) e = hipMemcpy(reinterpret_cast<char*>(L->w_qkv) + 2 * wsz, wv, wsz, kind);
+    if (e == hipSuccess) e = hipMemcpy(L->w_o, wo, wsz, kind);
+    if (e == hipSuccess) e = hipMemcpy(L->q_norm, q_norm_w, d_model * sizeof(float), kind);
+    if (e == hipSuccess) e = hipMemcpy(L->k_norm, k_norm_w, d_model * sizeof(float), kind);
+    if (e != hipSuccess) return fail(set_error(DT_ERR_HIP, "layer weight upload: %s", hipGetErrorString(e)));
+    *out = L;
+    return DT_OK;
+}
+
+int dt_attn_layer_load(dt_ctx* ctx, const char* folder, unsigned index, dt_attn_layer** out) {
+    clear_error();
+    if (!out) return set_error(DT_ERR_INVALID_ARG, "out is NULL");
+    *out = nullptr;
+    if (!folder) return set_error(DT_ERR_INVALID_ARG, "folder is NULL");
+    // file names of the OlmoAttention(folder, index) constructor, OlmoAttention.cpp:39-53
+    const char* names[6] = {"q_proj.weight", "k_proj.weight", "v_proj.weight",
+                            "o_proj.weight", "q_norm.weight", "k_norm.weight"};
+    std::vector<float> w[6];
+    size_t d = 0;
+    for (int i = 0; i < 6; ++i) {
+        std::string path = std::string(folder) + "/model.layers." + std::to_string(index) + ".self_attn." + names[i] + ".npy";
+        std::vector<size_t> shape;
+        DT_TRY(read_npy_f32(path, w[i], shape));
+        if (i == 0) {
+            if (shape.size() != 2 || shape[0] != shape[1]) return set_error(DT_ERR_IO, "%s: expected a square matrix", path.c_str());
+            d = shape[0];
+        }
+        const bool ok = i < 4 ? (shape.size() == 2 && shape[0] == d && shape[1] == d) : (shape.size() == 1 && shape[0] == d);
+        if (!ok) return set_error(DT_ERR_IO, "%s: unexpected shape", path.c_str());
+    }
+    if (d % DT_HEAD_DIM) return set_error(DT_ERR_UNSUPPORTED, "d_model=%zu is not a multiple of %d", d, DT_HEAD_DIM);
+    if (!ctx) return set_error(DT_ERR_INVALID_ARG, "ctx is NULL");
+    return dt_attn_layer_create(ctx, w[0].data(), w[1].data(), w[2].data(), w[3].data(), w[4].data(), w[5].data(),
+                                (int)d, (int)(d / DT_HEAD_DIM), DT_MEM_HOST, out);
+}
+
+int dt_attn_layer_destroy(dt_attn_layer* L) {
+    clear_error();
+    if (!L) return DT_OK;
+    if (L->ctx) (void)hipSetDevice(L->ctx->device);
+    if (L->w_qkv) (void)hipFree(L->w_qkv);
+    if (L->w_o) (void)hipFree(L->w_o);
+    if (L->w_qkv16) (void)hipFree(L->w_qkv16);
+    if (L->w_o16) (void)hipFree(L->w_o16);
+    if (L->q_norm) (void)hipFree(L->q_norm);
+    if (L->k_norm) (void)hipFree(L->k_norm);
+    L->qkv32.release();
+    L->qkv16.release();
+    L->attn.release();
+    L->x16.release();
+    delete L;
+    return DT_OK;
+}
+
+int dt_attn_layer_fwd(dt_attn_layer* L, const float* x, float* out, int B, int T, const int32_t* seq_lens,
+                      int dtype, int mem, void* stream) {
+    clear_error();
+    if (!x || !out) return set_error(DT_ERR_INVALID_ARG, "x and out must be non-NULL");
+    if (B < 1 || T < 1) return set_error(DT_ERR_INVALID_ARG, "B=%d, T=%d must be >= 1", B, T);
+    if (T > DT_MAX_SEQ_LEN) return set_error(DT_ERR_INVALID_ARG, "T=%d exceeds max_seq_len %d", T, DT_MAX_SEQ_LEN);
+    if ((int64_t)B * T > 0x7fffffff / 8) return set_error(DT_ERR_UNSUPPORTED, "B*T too large");
+    if (dtype != DT_FP32_EXACT && dtype != DT_BF16) return set_error(DT_ERR_INVALID_ARG, "unknown dtype %d", dtype);
+    if (mem != DT_MEM_DEVICE && mem != DT_MEM_HOST) return set_error(DT_ERR_INVALID_ARG, "unknown mem %d", mem);
+    if (mem == DT_MEM_DEVICE && (!aligned16(x) || !aligned16(out)))
+        return set_error(DT_ERR_INVALID_ARG, "device x/out must be 16-byte aligned");
+    DT_TRY(validate_seq_lens(seq_lens, B, T));
+    if (!L) return set_error(DT_ERR_INVALID_ARG, "layer is NULL");
+    dt_ctx* ctx = L->ctx;
+    if (T > ctx->rope_len) return set_error(DT_ERR_INVALID_ARG, "T=%d exceeds the RoPE table length %d", T, ctx->rope_len);
+    DT_TRY(check_device_binding(ctx));
+    hipStream_t s = static_cast<hipStream_t>(stream);
+
+    const int dm = L->d_model, H = L->n_heads, rows = B * T;
+    const size_t act = (size_t)rows * dm;
+    const float* xd = x;
+    float* od = out;
+    if (mem == DT_MEM_HOST) {
+        DT_TRY(ctx->stage[0].ensure(act * 4));
+        DT_TRY(ctx->stage[1].ensure(act * 4));
+        DT_HIP_TRY(hipMemcpyAsync(ctx->stage[0].ptr, x, act * 4, hipMemcpyHostToDevice, s));
+        xd = static_cast<const float*>(ctx->stage[0].ptr);
+        od = static_cast<float*>(ctx->stage[1].ptr);
+    }
+    DT_TRY(L->qkv32.ensure(act * 3 * 4));
+    float* qkv = static_cast<float*>(L->qkv32.ptr);
+    const float scale = 1.0f / std::sqrt((float)DT_HEAD_DIM);  // OlmoAttention.cpp:91
+
+    if (dtype == DT_FP32_EXACT) {
+        DT_TRY(L->attn.ensure(act * 4));
+        float* attn = static_cast<float*>(L->attn.ptr);
+        // Q|K|V = x [Wq;Wk;Wv]^T in one N = 3*d_model GEMM (OlmoAttention.cpp:68,74,80)
+        DT_TRY(gemm_xwt(ctx, s, rows, 3 * dm, dm, xd, dm, L->w_qkv, dm, qkv, 3 * dm, false));
+        // q/k norm + RoPE in place (OlmoAttention.cpp:70,76,87-88)
+        NormRopeArgs na{qkv, qkv + dm, nullptr, L->q_norm, L->k_norm, qkv, qkv + dm, nullptr, nullptr, nullptr,
+                        ctx->rope_cos, ctx->rope_sin, rows, T, H, 3 * dm, 3 * dm, DT_RMS_EPS};
+        DT_TRY(launch_qk_norm_rope(na, 0, s));
+        FlashArgs fa{qkv, qkv + dm, qkv + 2 * dm, attn, nullptr, nullptr, B, T, H, 3 * dm, 3 * dm, 3 * dm, dm,
+                     scale, 1, seq_lens ? 1 : 0};
+        DT_TRY(run_flash(ctx, fa, seq_lens, DT_FP32_EXACT, s));  // OlmoAttention.cpp:94
+        DT_TRY(gemm_xwt(ctx, s, rows, dm, dm, attn, dm, L->w_o, dm, od, dm, false));  // :104
+    } else {
+        if (!L->w_qkv16) {
+            DT_HIP_TRY(hipMalloc(&L->w_qkv16, (size_t)3 * dm * dm * 2));
+            DT_HIP_TRY(hipMalloc(&L->w_o16, (size_t)dm * dm * 2));
+            DT_TRY(launch_f32_to_bf16(L->w_qkv, L->w_qkv16, (int64_t)3 * dm * dm, s));
+            DT_TRY(launch_f32_to_bf16(L->w_o, L->w_o16, (int64_t)dm * dm, s));
+        }
+        DT_TRY(L->x16.ensure(act * 2));
+        DT_TRY(L->qkv16.ensure(act * 3 * 2));
+        DT_TRY(L->attn.ensure(act * 2));
+        uint16_t* x16 = static_cast<uint16_t*>(L->x16.ptr);
+        uint16_t* qkv16 = static_cast<uint16_t*>(L->qkv16.ptr);
+        uint16_t* attn16 = static_cast<uint16_t*>(L->attn.ptr);
+        DT_TRY(launch_f32_to_bf16(xd, x16, (int64_t)act, s));
+        DT_TRY(gemm_xwt(ctx, s, rows, 3 * dm, dm, x16, dm, L->w_qkv16, dm, qkv, 3 * dm, true));
+        NormRopeArgs na{qkv, qkv + dm, qkv + 2 * dm, L->q_norm, L->k_norm, qkv16, qkv16 + dm, qkv16 + 2 * dm,
+                        nullptr, nullptr, ctx->rope_cos, ctx->rope_sin, rows, T, H, 3 * dm, 3 * dm, DT_RMS_EPS};
+        DT_TRY(launch_qk_norm_rope(na, 1, s));
+        FlashArgs fa{qkv16, qkv16 + dm, qkv16 + 2 * dm, attn16, nullptr, nullptr, B, T, H, 3 * dm, 3 * dm, 3 * dm,
+                     dm, scale, 1, seq_lens ? 1 : 0};
+        DT_TRY(run_flash(ctx, fa, seq_lens, DT_BF16, s));
+        DT_TRY(gemm_xwt(ctx, s, rows, dm, dm, attn16, dm, L->w_o16, dm, od, dm, true));
+    }
+    if (mem == DT_MEM_HOST) {
+        DT_HIP_TRY(hipMemcpyAsync(out, od, act * 4, hipMemcpyDeviceToHost, s));
+        DT_HIP_TRY(hipStreamSynchronize(s));
+    }
+    return DT_OK;
+}
+
+int dt_attn_layer_bwd(dt_attn_layer*, const float*, float*, int, int, int, void*) {
+    clear_error();
+    return set_error(DT_ERR_NOT_IMPLEMENTED,
+                     "OlmoAttention::backward is not implemented on the GPU path (forward-only prefill)");
+}
+
+}  // extern "C"

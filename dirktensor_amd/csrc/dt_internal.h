@@ -1,0 +1,94 @@
+// Internal declarations shared by the HIP kernels and the C ABI.
+#pragma once
+
+#include <hip/hip_runtime.h>
+
+#include <cstdint>
+#include <string>
+
+#include "../../include/dirktensor_amd.h"
+
+namespace dt {
+
+// ---- error reporting (thread-local, read back through dt_last_error) ----
+int set_error(int code, const char* fmt, ...) __attribute__((format(printf, 2, 3)));
+void clear_error();
+
+#define DT_HIP_TRY(expr)                                                                          \
+    do {                                                                                          \
+        hipError_t dt_e_ = (expr);                                                                \
+        if (dt_e_ != hipSuccess)                                                                  \
+            return ::dt::set_error(DT_ERR_HIP, "%s failed: %s (%s:%d)", #expr,                    \
+                                   hipGetErrorString(dt_e_), __FILE__, __LINE__);                 \
+    } while (0)
+
+#define DT_TRY(expr)                  \
+    do {                              \
+        int dt_rc_ = (expr);          \
+        if (dt_rc_ != DT_OK) return dt_rc_; \
+    } while (0)
+
+// ---- a growable device buffer owned by a context or layer ----
+struct DeviceBuffer {
+    void* ptr = nullptr;
+    size_t bytes = 0;
+    int ensure(size_t need);  // grows (hipFree + hipMalloc) when too small
+    void release();
+};
+
+// Per-sequence lengths passed by value in kernel arguments (no device copy).
+constexpr int kMaxRaggedBatch = 256;
+struct SeqLens {
+    int32_t len[kMaxRaggedBatch];
+};
+
+// Arguments of one attention-core launch. Row strides are in elements.
+struct FlashArgs {
+    const void* q;
+    const void* k;
+    const void* v;
+    void* o;
+    float* m;  // nullable
+    float* l;  // nullable
+    int B, T, H;
+    int ldq, ldk, ldv, ldo;  // row (token) strides, elements
+    float scale;
+    int causal;
+    int ragged;  // 1 when seq_lens are used
+};
+
+int launch_flash_fwd_f32(const FlashArgs& a, const SeqLens* lens, hipStream_t stream);
+int launch_flash_fwd_bf16(const FlashArgs& a, const SeqLens* lens, hipStream_t stream);
+
+struct NormRopeArgs {
+    const float* q_in;
+    const float* k_in;
+    const float* v_in;  // nullable: when set, V rows are converted into v_out
+    const float* q_w;
+    const float* k_w;
+    void* q_out;
+    void* k_out;
+    void* v_out;
+    float* q_rms;  // nullable
+    float* k_rms;  // nullable
+    const float* rope_cos;  // [rope_len][D/2]
+    const float* rope_sin;  // [rope_len][D/2]
+    int rows, T, H;
+    int ld_in, ld_out;
+    float eps;
+};
+int launch_qk_norm_rope(const NormRopeArgs& a, int out_bf16, hipStream_t stream);
+int launch_f32_to_bf16(const float* in, uint16_t* out, int64_t n, hipStream_t stream);
+
+}  // namespace dt
+
+// ---- opaque handles ----
+struct dt_ctx {
+    int device = 0;
+    float* rope_cos = nullptr;  // device, [rope_len][64]
+    float* rope_sin = nullptr;
+    int rope_len = 0;
+    float rope_theta = 0.0f;
+    dt::DeviceBuffer stage[6];  // host-memory path staging
+    void* blas = nullptr;        // rocblas_handle, created on first use
+};

@@ -1,0 +1,164 @@
+/*
+ * dirktensor_amd — C ABI for the MI355X (gfx950) causal-attention path.
+ *
+ * Plain pointers, sizes and status codes only; no HIP, torch or C++ types in
+ * the signatures (streams are passed as `void*` holding a hipStream_t, NULL
+ * meaning the null stream). Every entry point validates its arguments before
+ * it makes any HIP call and returns DT_OK (0) or a negative status; the message
+ * for the last failure on the calling thread is available from dt_last_error().
+ *
+ * Tensor layout is the reference's: BTHD (batch, sequence, head, head_dim),
+ * row-major and contiguous, head h occupying features [h*D, (h+1)*D) of a
+ * d_model = H*D row (OlmoAttention.cpp:71; FlashAttention.cpp:87-88).
+ *
+ * Modes:
+ *   DT_FP32_EXACT  fp32 inputs/outputs, fp32 MFMA (v_mfma_f32_32x32x2_f32),
+ *                  fp32 accumulation; parity target 1e-4 of max|O|.
+ *   DT_BF16        bf16 Q/K/V/O, bf16 MFMA (v_mfma_f32_32x32x16_bf16) with
+ *                  fp32 accumulation and fp32 softmax; parity target 2e-2.
+ *   m and l are always fp32.
+ *
+ * Memory:
+ *   DT_MEM_DEVICE  all tensor pointers are device pointers; the call is
+ *                  stream-ordered and returns without synchronising.
+ *   DT_MEM_HOST    all tensor pointers are host pointers; the call copies in,
+ *                  runs, copies out and synchronises (the reference's
+ *                  synchronous value semantics).
+ *   seq_lens is always a host pointer (B int32 values) or NULL.
+ */
+#ifndef DIRKTENSOR_AMD_H
+#define DIRKTENSOR_AMD_H
+
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+#define DT_OK 0
+#define DT_ERR_INVALID_ARG (-1)
+#define DT_ERR_UNSUPPORTED (-2)
+#define DT_ERR_HIP (-3)
+#define DT_ERR_BLAS (-4)
+#define DT_ERR_NOT_IMPLEMENTED (-5)
+#define DT_ERR_IO (-6)
+
+#define DT_FP32_EXACT 0
+#define DT_BF16 1
+
+#define DT_MEM_DEVICE 0
+#define DT_MEM_HOST 1
+
+/* Model constants the kernels are built for (model_config.h:3-7). */
+#define DT_HEAD_DIM 128
+#define DT_MAX_SEQ_LEN 8192
+#define DT_D_MODEL 2048
+#define DT_N_HEADS 16
+#define DT_ROPE_THETA 500000.0f /* OlmoAttention.cpp:16 */
+#define DT_RMS_EPS 1e-6f        /* RMSNorm.h:10 */
+
+typedef struct dt_ctx dt_ctx;
+typedef struct dt_attn_layer dt_attn_layer;
+
+/* Message describing the last failed call on this thread ("" if none). */
+const char* dt_last_error(void);
+
+/* ABI version of this library (bumped on any signature change). */
+int dt_version(void);
+
+/*
+ * Context: owns the device binding, the RoPE tables, the rocBLAS handle and the
+ * host-memory staging buffers. Not thread-safe: use one per host thread.
+ * No reference counterpart: the reference keeps this state in file-scope
+ * statics (OlmoAttention.cpp:34-36) and in TBB's global pool.
+ */
+int dt_ctx_create(int device, dt_ctx** out);
+int dt_ctx_destroy(dt_ctx* ctx);
+
+/*
+ * Builds the RoPE sin/cos tables on the host in fp64, casts them to fp32 and
+ * uploads them (replaces compute_rope_buffers, OlmoAttention.cpp:18-36).
+ * dt_ctx_create already calls it with (DT_ROPE_THETA, DT_MAX_SEQ_LEN).
+ */
+int dt_rope_table_init(dt_ctx* ctx, float theta, int max_seq_len);
+
+/*
+ * Causal flash attention forward (replaces flash_attention_forward,
+ * FlashAttention.h:15-21 / FlashAttention.cpp:24-182).
+ *   q, k, v, o : [B, T, H, D]   (fp32 in DT_FP32_EXACT, bf16 bits in DT_BF16)
+ *   m, l       : [B, T, H] fp32: m = row max of the scaled scores, l = sum of
+ *                exp(s - m) (FlashAttention.cpp:162-163); either may be NULL.
+ *   scale      : score scale (the reference passes 1/sqrt(D), OlmoAttention.cpp:91)
+ *   causal     : 1 = causal (key k > query q masked, FlashAttention.cpp:102);
+ *                0 = full attention.
+ *   seq_lens   : NULL, or B lengths in [1, T]: keys at t >= seq_lens[b] are
+ *                masked and rows t >= seq_lens[b] are written as the
+ *                reference's empty row (O = 0, m = -inf, l = 0,
+ *                FlashAttention.cpp:165-174).
+ * Requires D == 128, 1 <= T <= 8192, B >= 1, 1 <= H.
+ */
+int dt_flash_attn_fwd(dt_ctx* ctx, const void* q, const void* k, const void* v, void* o, float* m, float* l,
+                      int B, int T, int H, int D, float scale, int causal, const int32_t* seq_lens, int dtype,
+                      int mem, void* stream);
+
+/*
+ * Flash attention backward (FlashAttention.h:33-43). Not implemented on the
+ * GPU: always returns DT_ERR_NOT_IMPLEMENTED so that callers fail loudly.
+ */
+int dt_flash_attn_bwd(dt_ctx* ctx, const void* d_o, const void* o, const float* m, const float* l, const void* q,
+                      const void* k, const void* v, void* d_q, void* d_k, void* d_v, int B, int T, int H, int D,
+                      float scale, int causal, int dtype, int mem, void* stream);
+
+/*
+ * Fused q/k RMSNorm + RoPE (replaces RMSNorm::forward for q_norm/k_norm,
+ * RMSNorm.cpp:15-22, plus apply_rope, OlmoAttention.cpp:111-146, as called at
+ * OlmoAttention.cpp:70,76,87-88).
+ *   q_in, k_in   : fp32 rows of the q and k projections, [B*T] rows of d_model
+ *                  = H*D features, with row strides ld_in (elements).
+ *   q_norm_w, k_norm_w : [d_model] fp32 norm weights.
+ *   q_out, k_out : [B*T] rows with stride ld_out, in out_dtype (DT_FP32_EXACT
+ *                  -> fp32, DT_BF16 -> bf16 bits); may alias q_in/k_in when
+ *                  the element types match.
+ *   q_rms, k_rms : [B*T] fp32 (the norms' saved rms), or NULL.
+ * The norm spans all d_model features (not per head); position of row
+ * b*T + t is t. Requires D == 128, T <= the RoPE table length.
+ */
+int dt_qk_norm_rope_fwd(dt_ctx* ctx, const float* q_in, const float* k_in, const float* q_norm_w,
+                        const float* k_norm_w, void* q_out, void* k_out, float* q_rms, float* k_rms, int B, int T,
+                        int H, int D, int ld_in, int ld_out, int out_dtype, int mem, void* stream);
+
+/*
+ * Attention layer (replaces class OlmoAttention, OlmoAttention.h:10-42).
+ * dt_attn_layer_create copies the weights (fp32, [out][in] like torch Linear,
+ * y = x W^T) to the device; with mem == DT_MEM_HOST they are host pointers.
+ * dt_attn_layer_load reads the reference's per-layer .npy files
+ * "{folder}/model.layers.{index}.self_attn.{q,k,v,o}_proj.weight.npy" and
+ * "...{q,k}_norm.weight.npy" (the OlmoAttention(folder, index) constructor,
+ * OlmoAttention.cpp:39-53).
+ */
+int dt_attn_layer_create(dt_ctx* ctx, const float* wq, const float* wk, const float* wv, const float* wo,
+                         const float* q_norm_w, const float* k_norm_w, int d_model, int n_heads, int mem,
+                         dt_attn_layer** out);
+int dt_attn_layer_load(dt_ctx* ctx, const char* folder, unsigned index, dt_attn_layer** out);
+int dt_attn_layer_destroy(dt_attn_layer* layer);
+
+/*
+ * OlmoAttention::forward (OlmoAttention.cpp:56-108): x [B, T, d_model] fp32 ->
+ * out [B, T, d_model] fp32. dtype selects the attention-core mode and the
+ * projection GEMM precision (DT_FP32_EXACT: fp32 GEMMs; DT_BF16: bf16 GEMM
+ * inputs with fp32 accumulation). seq_lens as for dt_flash_attn_fwd.
+ * Forward-only: the reference's saved activations for backward
+ * (OlmoAttention.h:28-38) are not kept.
+ */
+int dt_attn_layer_fwd(dt_attn_layer* layer, const float* x, float* out, int B, int T, const int32_t* seq_lens,
+                      int dtype, int mem, void* stream);
+
+/* OlmoAttention::backward / step / zero_grad (OlmoAttention.cpp:193-330):
+ * not implemented on the GPU; always DT_ERR_NOT_IMPLEMENTED. */
+int dt_attn_layer_bwd(dt_attn_layer* layer, const float* d_out, float* d_x, int B, int T, int mem, void* stream);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* DIRKTENSOR_AMD_H */

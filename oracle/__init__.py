@@ -1,0 +1,163 @@
+"""CPU oracle for the attention path — TEST INFRASTRUCTURE ONLY.
+
+ctypes wrapper of oracle/liboracle.so (built from oracle/dt_oracle.cpp by
+oracle/Makefile). Only tests/, __graft_entry__.smoke() and bench.py's
+cpu_baseline leg use it, as the checker or as the timed CPU baseline; the
+product path (dirktensor_amd) never imports it.
+
+Each function names the reference code it restates; see dt_oracle.cpp.
+"""
+
+from __future__ import annotations
+
+import ctypes
+import os
+import subprocess
+from pathlib import Path
+
+import numpy as np
+
+HERE = Path(__file__).resolve().parent
+LIB_PATH = HERE / "liboracle.so"
+_lib = None
+
+_vp = ctypes.c_void_p
+_i = ctypes.c_int
+_f = ctypes.c_float
+
+
+def build() -> Path:
+    subprocess.run(["make", "-B", "-s", "-C", os.fspath(HERE)], check=True)
+    return LIB_PATH
+
+
+def lib() -> ctypes.CDLL:
+    global _lib
+    if _lib is None:
+        if not LIB_PATH.exists():
+            build()
+        l = ctypes.CDLL(os.fspath(LIB_PATH))
+        l.oracle_version.restype = _i
+        l.oracle_set_mutation.argtypes = [_i]
+        l.oracle_get_mutation.restype = _i
+        l.oracle_rope_tables.argtypes = [_vp, _vp, _i, _i, _f]
+        l.oracle_apply_rope.argtypes = [_vp, _vp, _i, _i, _i, _i, _vp, _vp]
+        l.oracle_rmsnorm_forward.argtypes = [_vp, _vp, _vp, _vp, _i, _i, _f]
+        l.oracle_flash_attention_forward.argtypes = [_vp, _vp, _vp, _vp, _vp, _vp, _i, _i, _i, _i, _f, _i, _i]
+        l.oracle_sgemm_nt.argtypes = [_i, _i, _i, _f, _vp, _i, _vp, _i, _vp, _i, _i]
+        l.oracle_attention_layer_forward.argtypes = [_vp] * 9 + [_vp, _i, _i, _i, _i, _f, _i] + [_vp] * 6
+        _lib = l
+    return _lib
+
+
+def _p(a):
+    return None if a is None else a.ctypes.data_as(_vp)
+
+
+def _c32(a):
+    return np.ascontiguousarray(a, dtype=np.float32)
+
+
+def default_threads() -> int:
+    return max(1, min(16, os.cpu_count() or 1))
+
+
+class mutation:
+    """Context manager planting a known mistake in the oracle (tests only)."""
+
+    def __init__(self, m: int):
+        self.m = m
+
+    def __enter__(self):
+        lib().oracle_set_mutation(self.m)
+
+    def __exit__(self, *exc):
+        lib().oracle_set_mutation(0)
+
+
+def rope_tables(max_seq: int = 8192, D: int = 128, theta: float = 500000.0):
+    """compute_rope_buffers (OlmoAttention.cpp:18-31): sin, cos [max_seq, D] fp32."""
+    s = np.empty((max_seq, D), dtype=np.float32)
+    c = np.empty((max_seq, D), dtype=np.float32)
+    lib().oracle_rope_tables(_p(s), _p(c), max_seq, D, float(theta))
+    return s, c
+
+
+def apply_rope(x, sin_t, cos_t):
+    """OlmoAttention::apply_rope (OlmoAttention.cpp:111-146); x [B,T,H,D]."""
+    x = _c32(x)
+    B, T, H, D = x.shape
+    out = np.empty_like(x)
+    lib().oracle_apply_rope(_p(x), _p(out), B, T, H, D, _p(_c32(sin_t)), _p(_c32(cos_t)))
+    return out
+
+
+def rmsnorm_forward(x, w, eps: float = 1e-6):
+    """RMSNorm::forward (RMSNorm.cpp:15-22) over the last axis; returns (y, rms)."""
+    x = _c32(x)
+    C = x.shape[-1]
+    rows = x.size // C
+    y = np.empty_like(x)
+    rms = np.empty(x.shape[:-1], dtype=np.float32)
+    lib().oracle_rmsnorm_forward(_p(x), _p(_c32(w)), _p(y), _p(rms), rows, C, float(eps))
+    return y, rms
+
+
+def flash_attention_forward(Q, K, V, scale: float, causal: bool = True, nthreads: int | None = None):
+    """flash_attention_forward (FlashAttention.cpp:24-182); returns (O, m, l)."""
+    Q, K, V = _c32(Q), _c32(K), _c32(V)
+    B, T, H, D = Q.shape
+    O = np.empty_like(Q)
+    m = np.empty((B, T, H), dtype=np.float32)
+    l = np.empty((B, T, H), dtype=np.float32)
+    lib().oracle_flash_attention_forward(_p(Q), _p(K), _p(V), _p(O), _p(m), _p(l), B, T, H, D, float(scale),
+                                         int(bool(causal)), nthreads or default_threads())
+    return O, m, l
+
+
+def flash_attention_ragged(Q, K, V, seq_lens, scale: float, nthreads: int | None = None):
+    """Reference semantics of a right-padded batch: each sequence b run alone on its
+    unpadded prefix [0, L_b) (causal rows t < L_b never see later keys); rows t >= L_b
+    get the reference's empty row (O = 0, m = -inf, l = 0, FlashAttention.cpp:165-174)."""
+    Q, K, V = _c32(Q), _c32(K), _c32(V)
+    B, T, H, D = Q.shape
+    O = np.zeros_like(Q)
+    m = np.full((B, T, H), -np.inf, dtype=np.float32)
+    l = np.zeros((B, T, H), dtype=np.float32)
+    for b in range(B):
+        L = int(seq_lens[b])
+        o, mm, ll = flash_attention_forward(Q[b:b + 1, :L], K[b:b + 1, :L], V[b:b + 1, :L], scale, True, nthreads)
+        O[b, :L], m[b, :L], l[b, :L] = o[0], mm[0], ll[0]
+    return O, m, l
+
+
+def sgemm_nt(A, B, alpha: float = 1.0, nthreads: int | None = None):
+    """C = alpha * A B^T (row-major), the oracle's stand-in for cblas_sgemm(NoTrans, Trans)."""
+    A, B = _c32(A), _c32(B)
+    M, K = A.shape
+    N = B.shape[0]
+    Cm = np.empty((M, N), dtype=np.float32)
+    lib().oracle_sgemm_nt(M, N, K, float(alpha), _p(A), K, _p(B), K, _p(Cm), N, nthreads or default_threads())
+    return Cm
+
+
+def attention_layer_forward(x, wq, wk, wv, wo, q_norm, k_norm, *, theta: float = 500000.0, eps: float = 1e-6,
+                            nthreads: int | None = None, return_state: bool = False):
+    """OlmoAttention::forward (OlmoAttention.cpp:56-108) for x [B,T,d_model]."""
+    x = _c32(x)
+    B, T, dm = x.shape
+    D = 128
+    H = dm // D
+    sin_t, cos_t = rope_tables(max(T, 1), D, theta)
+    out = np.empty_like(x)
+    st = None
+    if return_state:
+        st = dict(q_rope=np.empty((B, T, H, D), np.float32), k_rope=np.empty((B, T, H, D), np.float32),
+                  v=np.empty((B, T, H, D), np.float32), attn=np.empty((B, T, H, D), np.float32),
+                  m=np.empty((B, T, H), np.float32), l=np.empty((B, T, H), np.float32))
+    g = (lambda k: _p(st[k])) if st else (lambda k: None)
+    lib().oracle_attention_layer_forward(_p(x), _p(_c32(wq)), _p(_c32(wk)), _p(_c32(wv)), _p(_c32(wo)),
+                                         _p(_c32(q_norm)), _p(_c32(k_norm)), _p(sin_t), _p(cos_t), _p(out),
+                                         B, T, H, D, float(eps), nthreads or default_threads(),
+                                         g("q_rope"), g("k_rope"), g("v"), g("attn"), g("m"), g("l"))
+    return (out, st) if return_state else out

@@ -1,0 +1,336 @@
+// CPU oracle for the causal-attention path — TEST INFRASTRUCTURE ONLY.
+//
+// This file restates, on the CPU, the reference algorithms that the HIP kernels
+// replace. It is linked only by the test suite, by __graft_entry__.smoke() and
+// by bench.py's cpu_baseline leg, always as the checker (or as the timed CPU
+// baseline), never as part of the product path.
+//
+// Functions and the reference code each one follows:
+//   oracle_rope_tables            OlmoAttention.cpp:16-36    (fp64 angles, cast to fp32)
+//   oracle_apply_rope             OlmoAttention.cpp:111-146  (rotate-half, position = t)
+//   oracle_rmsnorm_forward        RMSNorm.cpp:15-22, RMSNorm.h:10 (x / sqrt(mean(x^2)+eps) * w)
+//   oracle_flash_attention_forward FlashAttention.cpp:24-182 (256x256 tiles, tile-local max,
+//                                  alpha/beta online rescale, l==0 -> zero row)
+//   oracle_attention_layer_forward OlmoAttention.cpp:56-108  (projections, q/k norm over all
+//                                  2048 features, RoPE, flash, o_proj)
+//   oracle_sgemm_nt / _nn         stand-ins for the cblas_sgemm calls at FlashAttention.cpp:83,123
+//                                  and xt::linalg::dot at OlmoAttention.cpp:68,74,80,104
+//
+// Parity pins (checked in tests/test_oracle_pins.py): an fp64 full-softmax attention
+// written independently in numpy, torch's scaled_dot_product_attention in fp64,
+// HF transformers' Olmo2 rotate_half / apply_rotary_pos_emb and Olmo2Attention,
+// torch.nn.functional.rms_norm in fp64, closed-form invariants (row 0, Q == 0,
+// causality, RoPE identity at t=0, relative-position property, scale invariance)
+// and brute force at T <= 8. oracle_set_mutation() plants known mistakes so that
+// the tests can show each pin catches them.
+//
+// The BLAS summation order of the reference (whichever CBLAS it links) is not
+// reproduced; parity with it is by tolerance.
+
+#include <algorithm>
+#include <cmath>
+#include <cstdint>
+#include <cstring>
+#include <limits>
+#include <thread>
+#include <vector>
+
+namespace {
+
+int g_mutation = 0;  // 0 = faithful restatement; >0 = planted mistake (tests only)
+
+constexpr float kNegInf = -std::numeric_limits<float>::infinity();
+
+template <class F>
+void parallel_for(int64_t n, int nthreads, F&& fn) {
+    if (nthreads <= 1 || n <= 1) {
+        for (int64_t i = 0; i < n; ++i) fn(i);
+        return;
+    }
+    nthreads = (int)std::min<int64_t>(nthreads, n);
+    std::vector<std::thread> pool;
+    pool.reserve(nthreads);
+    for (int t = 0; t < nthreads; ++t) {
+        pool.emplace_back([&, t] {
+            // contiguous blocks, like tbb::blocked_range over [0, n)
+            int64_t lo = n * t / nthreads, hi = n * (t + 1) / nthreads;
+            for (int64_t i = lo; i < hi; ++i) fn(i);
+        });
+    }
+    for (auto& th : pool) th.join();
+}
+
+// C[i][j] = alpha * sum_k A[i][k] * B[j][k]    (row-major, "NoTrans, Trans")
+void gemm_nt_serial(int M, int N, int K, float alpha, const float* A, int lda, const float* B, int ldb,
+                    float* C, int ldc) {
+    int i = 0;
+    for (; i + 4 <= M; i += 4) {
+        const float* a0 = A + (int64_t)i * lda;
+        const float* a1 = a0 + lda;
+        const float* a2 = a1 + lda;
+        const float* a3 = a2 + lda;
+        int j = 0;
+        for (; j + 2 <= N; j += 2) {
+            const float* b0 = B + (int64_t)j * ldb;
+            const float* b1 = b0 + ldb;
+            float s00 = 0, s01 = 0, s10 = 0, s11 = 0, s20 = 0, s21 = 0, s30 = 0, s31 = 0;
+            for (int k = 0; k < K; ++k) {
+                float x0 = b0[k], x1 = b1[k];
+                s00 += a0[k] * x0; s01 += a0[k] * x1;
+                s10 += a1[k] * x0; s11 += a1[k] * x1;
+                s20 += a2[k] * x0; s21 += a2[k] * x1;
+                s30 += a3[k] * x0; s31 += a3[k] * x1;
+            }
+            float* c = C + (int64_t)i * ldc + j;
+            c[0] = alpha * s00; c[1] = alpha * s01; c += ldc;
+            c[0] = alpha * s10; c[1] = alpha * s11; c += ldc;
+            c[0] = alpha * s20; c[1] = alpha * s21; c += ldc;
+            c[0] = alpha * s30; c[1] = alpha * s31;
+        }
+        for (; j < N; ++j) {
+            const float* b0 = B + (int64_t)j * ldb;
+            float s0 = 0, s1 = 0, s2 = 0, s3 = 0;
+            for (int k = 0; k < K; ++k) {
+                s0 += a0[k] * b0[k]; s1 += a1[k] * b0[k]; s2 += a2[k] * b0[k]; s3 += a3[k] * b0[k];
+            }
+            C[(int64_t)i * ldc + j] = alpha * s0;
+            C[(int64_t)(i + 1) * ldc + j] = alpha * s1;
+            C[(int64_t)(i + 2) * ldc + j] = alpha * s2;
+            C[(int64_t)(i + 3) * ldc + j] = alpha * s3;
+        }
+    }
+    for (; i < M; ++i) {
+        const float* a0 = A + (int64_t)i * lda;
+        for (int j = 0; j < N; ++j) {
+            const float* b0 = B + (int64_t)j * ldb;
+            float s = 0;
+            for (int k = 0; k < K; ++k) s += a0[k] * b0[k];
+            C[(int64_t)i * ldc + j] = alpha * s;
+        }
+    }
+}
+
+// C[i][n] = sum_k A[i][k] * B[k][n]    (row-major, "NoTrans, NoTrans"), beta = 0
+void gemm_nn_serial(int M, int N, int K, const float* A, int lda, const float* B, int ldb, float* C, int ldc) {
+    for (int i = 0; i < M; ++i) {
+        float* c = C + (int64_t)i * ldc;
+        std::fill(c, c + N, 0.0f);
+        const float* a = A + (int64_t)i * lda;
+        for (int k = 0; k < K; ++k) {
+            const float av = a[k];
+            if (av == 0.0f) continue;
+            const float* b = B + (int64_t)k * ldb;
+            for (int n = 0; n < N; ++n) c[n] += av * b[n];
+        }
+    }
+}
+
+}  // namespace
+
+extern "C" {
+
+int oracle_version(void) { return 1; }
+
+// Planted mistakes, for tests that show the pins catch them:
+//   1 flash: drop beta in the online rescale     (FlashAttention.cpp:141-151)
+//   2 flash: mask the diagonal (q_pos <= k_pos)   (FlashAttention.cpp:102)
+//   3 rope:  flip the sign of the sin term         (OlmoAttention.cpp:131-140)
+//   4 rope:  pair d with d+1 instead of d+64       (OlmoAttention.cpp:125)
+//   5 norm:  normalise per head (128) instead of over all features (OlmoAttention.cpp:70)
+//   6 norm:  drop eps                              (RMSNorm.cpp:18)
+//   7 flash: drop the softmax scale                (FlashAttention.cpp:86)
+void oracle_set_mutation(int m) { g_mutation = m; }
+int oracle_get_mutation(void) { return g_mutation; }
+
+// RoPE tables, OlmoAttention.cpp:16-31: inv_freq[i] = 1 / theta^(2i/D) in fp64,
+// angle[p][j] = p * inv_freq[j mod D/2] (halves duplicated by concatenate),
+// sin/cos evaluated in fp64 and cast to fp32. Tables are [max_seq][D].
+void oracle_rope_tables(float* sin_out, float* cos_out, int max_seq, int D, float theta) {
+    const int half = D / 2;
+    std::vector<double> inv_freq(half);
+    for (int i = 0; i < half; ++i) {
+        const double e = (double)(2 * i) / (double)D;  // arange(0, D, 2) / D
+        inv_freq[i] = 1.0 / std::pow((double)theta, e);
+    }
+    for (int p = 0; p < max_seq; ++p) {
+        for (int j = 0; j < D; ++j) {
+            const double ang = (double)p * inv_freq[j % half];
+            sin_out[(int64_t)p * D + j] = (float)std::sin(ang);
+            cos_out[(int64_t)p * D + j] = (float)std::cos(ang);
+        }
+    }
+}
+
+// apply_rope, OlmoAttention.cpp:111-146. in/out are [B,T,H,D]; tables [>=T][D].
+void oracle_apply_rope(const float* in, float* out, int B, int T, int H, int D, const float* sin_t,
+                       const float* cos_t) {
+    const int half = D / 2;
+    const int pair = (g_mutation == 4) ? 1 : half;
+    for (int b = 0; b < B; ++b)
+        for (int t = 0; t < T; ++t)
+            for (int h = 0; h < H; ++h) {
+                const float* x = in + (((int64_t)b * T + t) * H + h) * D;
+                float* y = out + (((int64_t)b * T + t) * H + h) * D;
+                const float* c = cos_t + (int64_t)t * D;
+                const float* s = sin_t + (int64_t)t * D;
+                if (pair == half) {
+                    for (int d = 0; d < half; ++d) {
+                        const float sgn = (g_mutation == 3) ? -1.0f : 1.0f;
+                        y[d] = x[d] * c[d] - sgn * x[d + half] * s[d];
+                        y[d + half] = x[d + half] * c[d + half] + sgn * x[d] * s[d + half];
+                    }
+                } else {  // planted mistake 4: adjacent pairs
+                    for (int d = 0; d < D; d += 2) {
+                        y[d] = x[d] * c[d / 2] - x[d + 1] * s[d / 2];
+                        y[d + 1] = x[d + 1] * c[d / 2] + x[d] * s[d / 2];
+                    }
+                }
+            }
+}
+
+// RMSNorm::forward, RMSNorm.cpp:15-22 (eps RMSNorm.h:10): rms = sqrt(sum(x^2)/C + eps); y = (x / rms) * w.
+// x, y are [rows][C]; rms_out (nullable) is [rows].
+void oracle_rmsnorm_forward(const float* x, const float* w, float* y, float* rms_out, int rows, int C,
+                            float eps) {
+    if (g_mutation == 6) eps = 0.0f;
+    const int group = (g_mutation == 5) ? 128 : C;
+    for (int r = 0; r < rows; ++r) {
+        const float* xr = x + (int64_t)r * C;
+        float* yr = y + (int64_t)r * C;
+        for (int g0 = 0; g0 < C; g0 += group) {
+            float ss = 0.0f;
+            for (int c = g0; c < g0 + group; ++c) ss += xr[c] * xr[c];
+            const float rms = std::sqrt(ss / (float)group + eps);
+            if (rms_out && g0 == 0) rms_out[r] = rms;
+            for (int c = g0; c < g0 + group; ++c) yr[c] = (xr[c] / rms) * w[c];
+        }
+    }
+}
+
+// flash_attention_forward, FlashAttention.cpp:24-182. Q, K, V, O are [B,T,H,D] row-major;
+// m, l are [B,T,H]. Threads split the B*H (batch, head) items like the reference's
+// tbb::parallel_for over bh (FlashAttention.cpp:43-45).
+void oracle_flash_attention_forward(const float* Q, const float* K, const float* V, float* O, float* m_out,
+                                    float* l_out, int B, int T, int H, int D, float scale, int causal,
+                                    int nthreads) {
+    constexpr int BQ = 256, BKV = 256;  // FlashAttention.cpp:21-22
+    const int ld = H * D;
+    auto at = [&](const float* base, int b, int t, int h) { return base + ((int64_t)b * T + t) * ld + (int64_t)h * D; };
+    parallel_for((int64_t)B * H, nthreads, [&](int64_t bh) {
+        const int b = (int)(bh / H), h = (int)(bh % H);
+        std::vector<float> S((size_t)BQ * BKV), P((size_t)BQ * BKV), PV((size_t)BQ * D);
+        std::vector<float> m(BQ), l(BQ), Ob((size_t)BQ * D), m_loc(BQ), l_loc(BQ);
+        for (int q0 = 0; q0 < T; q0 += BQ) {
+            const int Br = std::min(BQ, T - q0);
+            std::fill(m.begin(), m.begin() + Br, kNegInf);
+            std::fill(l.begin(), l.begin() + Br, 0.0f);
+            std::fill(Ob.begin(), Ob.begin() + (size_t)Br * D, 0.0f);
+            for (int k0 = 0; k0 < T; k0 += BKV) {
+                const int Bc = std::min(BKV, T - k0);
+                if (causal && q0 < k0) continue;  // whole tile above the diagonal
+                // S = scale * Q_blk K_blk^T (sgemm alpha), FlashAttention.cpp:83-91
+                const float alpha_s = (g_mutation == 7) ? 1.0f : scale;
+                gemm_nt_serial(Br, Bc, D, alpha_s, at(Q, b, q0, h), ld, at(K, b, k0, h), ld, S.data(), BKV);
+                // mask, tile-local max, P = exp(S - m_local), l_local; FlashAttention.cpp:94-120
+                for (int i = 0; i < Br; ++i) {
+                    float* s = S.data() + (size_t)i * BKV;
+                    float* p = P.data() + (size_t)i * BKV;
+                    m_loc[i] = kNegInf;
+                    for (int j = 0; j < Bc; ++j) {
+                        const int qp = q0 + i, kp = k0 + j;
+                        const bool masked = causal && ((g_mutation == 2) ? (qp <= kp) : (qp < kp));
+                        if (masked) s[j] = kNegInf;
+                        else m_loc[i] = std::max(m_loc[i], s[j]);
+                    }
+                    l_loc[i] = 0.0f;
+                    for (int j = 0; j < Bc; ++j) {
+                        if (s[j] > kNegInf) {
+                            const float e = std::exp(s[j] - m_loc[i]);
+                            p[j] = e;
+                            l_loc[i] += e;
+                        } else {
+                            p[j] = 0.0f;
+                        }
+                    }
+                }
+                // PV = P V_blk, FlashAttention.cpp:123-131
+                gemm_nn_serial(Br, D, Bc, P.data(), BKV, at(V, b, k0, h), ld, PV.data(), D);
+                // online rescale, FlashAttention.cpp:134-156
+                for (int i = 0; i < Br; ++i) {
+                    const float m_new = std::max(m[i], m_loc[i]);
+                    const float a = (m[i] > kNegInf) ? std::exp(m[i] - m_new) : 0.0f;
+                    float be = (m_loc[i] > kNegInf) ? std::exp(m_loc[i] - m_new) : 0.0f;
+                    if (g_mutation == 1) be = 1.0f;
+                    l[i] = l[i] * a + l_loc[i] * be;
+                    float* o = Ob.data() + (size_t)i * D;
+                    const float* pv = PV.data() + (size_t)i * D;
+                    for (int d = 0; d < D; ++d) o[d] = o[d] * a + pv[d] * be;
+                    m[i] = m_new;
+                }
+            }
+            // finalize, FlashAttention.cpp:159-175
+            for (int i = 0; i < Br; ++i) {
+                const int64_t idx = ((int64_t)b * T + q0 + i) * H + h;
+                m_out[idx] = m[i];
+                l_out[idx] = l[i];
+                float* dst = O + idx * D;
+                if (l[i] > 0.0f) {
+                    for (int d = 0; d < D; ++d) dst[d] = Ob[(size_t)i * D + d] / l[i];
+                } else {
+                    for (int d = 0; d < D; ++d) dst[d] = 0.0f;
+                }
+            }
+        }
+    });
+}
+
+// C = alpha * A B^T, row-major, threaded over row blocks of C.
+void oracle_sgemm_nt(int M, int N, int K, float alpha, const float* A, int lda, const float* B, int ldb, float* C,
+                     int ldc, int nthreads) {
+    const int rb = 32;
+    const int nblk = (M + rb - 1) / rb;
+    parallel_for(nblk, nthreads, [&](int64_t blk) {
+        const int i0 = (int)blk * rb, rows = std::min(rb, M - i0);
+        // block over N to keep a panel of B in cache
+        for (int j0 = 0; j0 < N; j0 += 256) {
+            const int cols = std::min(256, N - j0);
+            gemm_nt_serial(rows, cols, K, alpha, A + (int64_t)i0 * lda, lda, B + (int64_t)j0 * ldb, ldb,
+                           C + (int64_t)i0 * ldc + j0, ldc);
+        }
+    });
+}
+
+// OlmoAttention::forward, OlmoAttention.cpp:56-108, for d_model = H*D with D = 128.
+// x, out are [B,T,d_model]; weights are [d_model][d_model] stored [out][in] (y = x W^T);
+// q_norm_w, k_norm_w are [d_model]. rope tables [>=T][D]. Optional saved state:
+// q_rope, k_rope, v_out, attn_out [B,T,H,D], m, l [B,T,H] (each nullable).
+void oracle_attention_layer_forward(const float* x, const float* wq, const float* wk, const float* wv,
+                                    const float* wo, const float* q_norm_w, const float* k_norm_w,
+                                    const float* sin_t, const float* cos_t, float* out, int B, int T, int H,
+                                    int D, float eps, int nthreads, float* q_rope, float* k_rope, float* v_out,
+                                    float* attn_out, float* m_out, float* l_out) {
+    const int dm = H * D;
+    const int64_t rows = (int64_t)B * T;
+    const size_t n = (size_t)rows * dm;
+    std::vector<float> q(n), k(n), v(n), qn(n), kn(n), qr(n), kr(n), o(n);
+    std::vector<float> mm((size_t)rows * H), ll((size_t)rows * H);
+    oracle_sgemm_nt((int)rows, dm, dm, 1.0f, x, dm, wq, dm, q.data(), dm, nthreads);   // :68
+    oracle_rmsnorm_forward(q.data(), q_norm_w, qn.data(), nullptr, (int)rows, dm, eps); // :70
+    oracle_sgemm_nt((int)rows, dm, dm, 1.0f, x, dm, wk, dm, k.data(), dm, nthreads);   // :74
+    oracle_rmsnorm_forward(k.data(), k_norm_w, kn.data(), nullptr, (int)rows, dm, eps); // :76
+    oracle_sgemm_nt((int)rows, dm, dm, 1.0f, x, dm, wv, dm, v.data(), dm, nthreads);   // :80
+    oracle_apply_rope(qn.data(), qr.data(), B, T, H, D, sin_t, cos_t);                  // :87
+    oracle_apply_rope(kn.data(), kr.data(), B, T, H, D, sin_t, cos_t);                  // :88
+    const float scale = 1.0f / std::sqrt((float)D);                                      // :91
+    oracle_flash_attention_forward(qr.data(), kr.data(), v.data(), o.data(), mm.data(), ll.data(), B, T, H, D,
+                                   scale, 1, nthreads);                                  // :94
+    oracle_sgemm_nt((int)rows, dm, dm, 1.0f, o.data(), dm, wo, dm, out, dm, nthreads); // :104
+    if (q_rope) std::memcpy(q_rope, qr.data(), n * sizeof(float));
+    if (k_rope) std::memcpy(k_rope, kr.data(), n * sizeof(float));
+    if (v_out) std::memcpy(v_out, v.data(), n * sizeof(float));
+    if (attn_out) std::memcpy(attn_out, o.data(), n * sizeof(float));
+    if (m_out) std::memcpy(m_out, mm.data(), mm.size() * sizeof(float));
+    if (l_out) std::memcpy(l_out, ll.data(), ll.size() * sizeof(float));
+}
+
+}  // extern "C"
