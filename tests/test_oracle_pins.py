@@ -1,0 +1,262 @@
+"""Pins of the CPU oracle (CPU only).
+
+The reference's own checks of this path cannot run anywhere in this pipeline
+(test_olmo_model.cpp:48-70 and tests/test_backward.py:56-86 need trained
+weights that are Git-LFS pointers, plus network access), so the oracle is
+pinned against things that fix the answer independently of its code:
+
+* an fp64 full-softmax attention written here in numpy (not tiled, no online
+  rescale) and torch's scaled_dot_product_attention in fp64;
+* brute force over every (query, key) pair at T <= 8;
+* closed forms: row 0 returns V[0] with l = 1 and m = scale * q0.k0; Q = 0
+  gives the running mean of V with m = 0 and l = t + 1; causality;
+* HF transformers' OLMo-2 building blocks (a separate implementation of the
+  same model): rotate_half / apply_rotary_pos_emb, Olmo2RotaryEmbedding,
+  Olmo2RMSNorm and the whole Olmo2Attention layer, run in fp64 with the
+  oracle's fp64-derived RoPE tables;
+* torch.nn.functional.rms_norm in fp64, and RoPE invariants (identity at
+  t = 0, pair norms preserved, scores depend only on t1 - t2).
+
+test_planted_mistakes_are_caught then plants each of the oracle's known
+mistakes (oracle_set_mutation) and checks that at least one pin fails.
+"""
+
+import numpy as np
+import pytest
+import torch
+import torch.nn.functional as F
+
+import oracle
+from dirktensor_amd import synth
+
+SCALE = float(np.float32(1.0) / np.sqrt(np.float32(128.0)))
+
+
+# ----------------------------------------------------------------- independent formulations
+def textbook_attention_f64(Q, K, V, scale, causal=True):
+    q, k, v = (np.asarray(x, np.float64).transpose(0, 2, 1, 3) for x in (Q, K, V))  # B,H,T,D
+    s = scale * (q @ k.transpose(0, 1, 3, 2))
+    T = s.shape[-1]
+    if causal:
+        s = np.where(np.triu(np.ones((T, T), bool), 1), -np.inf, s)
+    m = s.max(-1)
+    p = np.exp(s - m[..., None])
+    l = p.sum(-1)
+    o = (p @ v) / l[..., None]
+    return o.transpose(0, 2, 1, 3), m.transpose(0, 2, 1), l.transpose(0, 2, 1)
+
+
+def brute_force_attention(Q, K, V, scale):
+    B, T, H, D = Q.shape
+    O = np.zeros((B, T, H, D))
+    m = np.zeros((B, T, H))
+    l = np.zeros((B, T, H))
+    for b in range(B):
+        for h in range(H):
+            for t in range(T):
+                scores = [scale * sum(float(Q[b, t, h, d]) * float(K[b, j, h, d]) for d in range(D))
+                          for j in range(t + 1)]
+                mx = max(scores)
+                w = [np.exp(x - mx) for x in scores]
+                m[b, t, h], l[b, t, h] = mx, sum(w)
+                for j in range(t + 1):
+                    O[b, t, h] += w[j] * V[b, j, h].astype(np.float64)
+                O[b, t, h] /= l[b, t, h]
+    return O, m, l
+
+
+def rel(a, b):
+    a = np.asarray(a, np.float64)
+    b = np.asarray(b, np.float64)
+    return float(np.max(np.abs(a - b)) / max(np.max(np.abs(b)), 1e-30))
+
+
+def hf_config():
+    from transformers import Olmo2Config
+
+    return Olmo2Config(hidden_size=2048, intermediate_size=8192, num_attention_heads=16, num_key_value_heads=16,
+                       max_position_embeddings=8192, rms_norm_eps=1e-6, attention_bias=False,
+                       rope_parameters={"rope_type": "default", "rope_theta": 500000.0})
+
+
+# ----------------------------------------------------------------- pins (return True when they hold)
+def pin_flash_textbook(causal=True):
+    Q, K, V = synth.qkv(1, 300, 2, seeds=(41, 42, 43))  # 300 > 256 exercises the tile-to-tile rescale
+    O, m, l = oracle.flash_attention_forward(Q, K, V, SCALE, causal)
+    Ot, mt, lt = textbook_attention_f64(Q, K, V, SCALE, causal)
+    return rel(O, Ot) <= 1e-5 and np.max(np.abs(m - mt)) <= 1e-5 * np.max(np.abs(mt)) and rel(l, lt) <= 1e-5
+
+
+def pin_flash_sdpa():
+    Q, K, V = synth.qkv(2, 280, 3, seeds=(51, 52, 53))
+    O, _, _ = oracle.flash_attention_forward(Q, K, V, SCALE)
+    q, k, v = (torch.from_numpy(x).double().transpose(1, 2) for x in (Q, K, V))
+    ref = F.scaled_dot_product_attention(q, k, v, is_causal=True, scale=SCALE).transpose(1, 2).numpy()
+    return rel(O, ref) <= 1e-5
+
+
+def pin_flash_bruteforce():
+    Q, K, V = synth.qkv(1, 8, 2, seeds=(61, 62, 63))
+    O, m, l = oracle.flash_attention_forward(Q, K, V, SCALE)
+    Ob, mb, lb = brute_force_attention(Q, K, V, SCALE)
+    return rel(O, Ob) <= 1e-5 and np.max(np.abs(m - mb)) <= 1e-5 and rel(l, lb) <= 1e-5
+
+
+def pin_flash_closed_forms():
+    Q, K, V = synth.qkv(1, 260, 2, seeds=(71, 72, 73))
+    O, m, l = oracle.flash_attention_forward(Q, K, V, SCALE)
+    ok = np.array_equal(O[0, 0], V[0, 0]) and np.all(l[0, 0] == 1.0)
+    s00 = SCALE * np.sum(Q[0, 0].astype(np.float64) * K[0, 0], axis=-1)
+    ok &= np.max(np.abs(m[0, 0] - s00)) <= 1e-5 * max(1.0, np.max(np.abs(s00)))
+    Z = np.zeros_like(Q)
+    Oz, mz, lz = oracle.flash_attention_forward(Z, K, V, SCALE)
+    mean = np.cumsum(V.astype(np.float64), axis=1) / np.arange(1, 261)[None, :, None, None]
+    ok &= rel(Oz, mean) <= 1e-5 and np.all(mz == 0.0)
+    ok &= np.max(np.abs(lz[0, :, 0] - np.arange(1, 261))) <= 1e-3
+    return bool(ok)
+
+
+def pin_flash_causality():
+    Q, K, V = synth.qkv(1, 300, 2, seeds=(81, 82, 83))
+    O, _, _ = oracle.flash_attention_forward(Q, K, V, SCALE)
+    K2, V2 = K.copy(), V.copy()
+    K2[:, 151:] += 1.0
+    V2[:, 151:] -= 2.0
+    O2, _, _ = oracle.flash_attention_forward(Q, K2, V2, SCALE)
+    return bool(np.array_equal(O[:, :151], O2[:, :151]) and not np.array_equal(O[:, 151:], O2[:, 151:]))
+
+
+def pin_rope_hf():
+    from transformers.models.olmo2.modeling_olmo2 import apply_rotary_pos_emb
+
+    s, c = oracle.rope_tables(64)
+    x = synth.normal(91, (2, 64, 3, 128))
+    y = synth.normal(92, (2, 64, 3, 128))
+    ox, oy = oracle.apply_rope(x, s, c), oracle.apply_rope(y, s, c)
+    cos = torch.from_numpy(c).double()[None]  # [1, T, D]
+    sin = torch.from_numpy(s).double()[None]
+    hx, hy = apply_rotary_pos_emb(torch.from_numpy(x).double(), torch.from_numpy(y).double(), cos, sin,
+                                  unsqueeze_dim=2)
+    return rel(ox, hx.numpy()) <= 1e-6 and rel(oy, hy.numpy()) <= 1e-6
+
+
+def pin_rope_tables():
+    from transformers.models.olmo2.modeling_olmo2 import Olmo2RotaryEmbedding
+
+    s, c = oracle.rope_tables(8192)
+    cos, sin = Olmo2RotaryEmbedding(hf_config())(torch.zeros(1), torch.arange(8192)[None])
+    # HF evaluates the angles in fp32 (a ~1e-4 difference at t ~ 8k); the reference, and the oracle, in fp64.
+    ok = np.max(np.abs(c - cos[0].numpy())) <= 2e-3 and np.max(np.abs(s - sin[0].numpy())) <= 2e-3
+    t = np.arange(8192, dtype=np.float64)
+    ok &= np.array_equal(s[:, 0], np.sin(t).astype(np.float32)) and np.array_equal(c[:, 64], np.cos(t).astype(np.float32))
+    ok &= np.array_equal(s[:, :64], s[:, 64:]) and np.array_equal(c[:, :64], c[:, 64:])
+    inv_last = 1.0 / 500000.0 ** (126.0 / 128.0)
+    ok &= np.array_equal(s[:, 63], np.sin(t * inv_last).astype(np.float32))
+    return bool(ok)
+
+
+def pin_rope_invariants():
+    s, c = oracle.rope_tables(512)
+    x = synth.normal(93, (1, 512, 1, 128))
+    r = oracle.apply_rope(x, s, c)
+    ok = np.array_equal(r[0, 0], x[0, 0])  # t = 0: cos = 1, sin = 0
+    n0 = x[..., :64] ** 2 + x[..., 64:] ** 2
+    n1 = r[..., :64].astype(np.float64) ** 2 + r[..., 64:].astype(np.float64) ** 2
+    ok &= np.max(np.abs(n1 - n0) / np.maximum(n0, 1e-3)) <= 1e-5
+    q = np.broadcast_to(synth.normal(94, (1, 1, 1, 128)), (1, 512, 1, 128)).copy()
+    k = np.broadcast_to(synth.normal(95, (1, 1, 1, 128)), (1, 512, 1, 128)).copy()
+    rq, rk = oracle.apply_rope(q, s, c).astype(np.float64), oracle.apply_rope(k, s, c).astype(np.float64)
+    d1 = np.sum(rq[0, 300, 0] * rk[0, 290, 0])
+    d2 = np.sum(rq[0, 110, 0] * rk[0, 100, 0])
+    ok &= abs(d1 - d2) <= 1e-4 * max(1.0, abs(d1))
+    return bool(ok)
+
+
+def pin_rmsnorm_torch():
+    w = synth.normal(96, (2048,), 1.0, 0.01)
+    ok = True
+    for std in (1.0, 1e-3):  # at std 1e-3 the mean square is ~1e-6, comparable to eps
+        x = synth.normal(97, (5, 2048), 0.0, std)
+        y, rms = oracle.rmsnorm_forward(x, w)
+        ref = F.rms_norm(torch.from_numpy(x).double(), (2048,), torch.from_numpy(w).double(), eps=1e-6).numpy()
+        ok &= rel(y, ref) <= 1e-6
+        ok &= rel(rms, np.sqrt(np.mean(x.astype(np.float64) ** 2, axis=-1) + 1e-6)) <= 1e-6
+    return bool(ok)
+
+
+def pin_rmsnorm_hf():
+    from transformers.models.olmo2.modeling_olmo2 import Olmo2RMSNorm
+
+    w = synth.normal(98, (2048,), 1.0, 0.01)
+    x = synth.normal(99, (3, 7, 2048), 0.0, 2.0)
+    n = Olmo2RMSNorm(2048, 1e-6)
+    with torch.no_grad():
+        n.weight.copy_(torch.from_numpy(w))
+        ref = n(torch.from_numpy(x)).numpy()
+    y, _ = oracle.rmsnorm_forward(x, w)
+    big, _ = oracle.rmsnorm_forward(1000.0 * x, w)  # scale invariance (eps negligible)
+    return rel(y, ref) <= 2e-6 and rel(big, y) <= 2e-6
+
+
+def pin_layer_hf(T=48):
+    from transformers.models.olmo2.modeling_olmo2 import Olmo2Attention
+
+    w = synth.attention_layer_weights()
+    x = synth.normal(2301, (1, T, 2048))
+    out = oracle.attention_layer_forward(x, w["wq"], w["wk"], w["wv"], w["wo"], w["q_norm"], w["k_norm"])
+    cfg = hf_config()
+    cfg._attn_implementation = "eager"
+    attn = Olmo2Attention(cfg, 0).double()
+    with torch.no_grad():
+        attn.q_proj.weight.copy_(torch.from_numpy(w["wq"]))
+        attn.k_proj.weight.copy_(torch.from_numpy(w["wk"]))
+        attn.v_proj.weight.copy_(torch.from_numpy(w["wv"]))
+        attn.o_proj.weight.copy_(torch.from_numpy(w["wo"]))
+        attn.q_norm.weight.copy_(torch.from_numpy(w["q_norm"]))
+        attn.k_norm.weight.copy_(torch.from_numpy(w["k_norm"]))
+        s, c = oracle.rope_tables(T)
+        pe = (torch.from_numpy(c).double()[None], torch.from_numpy(s).double()[None])
+        mask = torch.triu(torch.full((T, T), float("-inf"), dtype=torch.float64), 1)[None, None]
+        ref, _ = attn(torch.from_numpy(x).double(), pe, mask)
+    return rel(out, ref.numpy()) <= 1e-4
+
+
+PINS = {
+    "flash_textbook_causal": lambda: pin_flash_textbook(True),
+    "flash_textbook_full": lambda: pin_flash_textbook(False),
+    "flash_sdpa": pin_flash_sdpa,
+    "flash_bruteforce": pin_flash_bruteforce,
+    "flash_closed_forms": pin_flash_closed_forms,
+    "flash_causality": pin_flash_causality,
+    "rope_hf": pin_rope_hf,
+    "rope_tables": pin_rope_tables,
+    "rope_invariants": pin_rope_invariants,
+    "rmsnorm_torch": pin_rmsnorm_torch,
+    "rmsnorm_hf": pin_rmsnorm_hf,
+    "layer_hf": pin_layer_hf,
+}
+
+
+@pytest.mark.parametrize("name", sorted(PINS))
+def test_pin_holds(name):
+    assert PINS[name](), f"oracle pin {name} failed"
+
+
+# mutation -> the pins expected to catch it
+MUTATIONS = {
+    1: ["flash_textbook_causal", "flash_textbook_full"],  # beta dropped from the online rescale
+    2: ["flash_closed_forms", "flash_bruteforce"],        # diagonal masked
+    3: ["rope_hf", "layer_hf"],                           # sin sign flipped
+    4: ["rope_hf", "rope_invariants"],                    # pairs (d, d+1)
+    5: ["rmsnorm_torch", "layer_hf"],                     # per-head norm
+    6: ["rmsnorm_torch"],                                 # eps dropped
+    7: ["flash_textbook_causal", "flash_sdpa"],           # scale dropped
+}
+
+
+@pytest.mark.parametrize("mut", sorted(MUTATIONS))
+def test_planted_mistakes_are_caught(mut):
+    with oracle.mutation(mut):
+        failing = [n for n in MUTATIONS[mut] if not PINS[n]()]
+    assert failing == MUTATIONS[mut], f"mutation {mut}: only {failing} of {MUTATIONS[mut]} caught it"
+    assert oracle.lib().oracle_get_mutation() == 0
