@@ -143,7 +143,7 @@ def test_npy_loader(tmp_path):
 
 def test_cpp_dropin_headers_compile_and_throw():
     sys.path.insert(0, os.path.join(ROOT, "tests", "cpp"))
-    import build as cpp_build
+    import build_dropin as cpp_build
 
     exe = cpp_build.build()
     r = subprocess.run([str(exe), "cpu"], capture_output=True, text=True, timeout=60)

@@ -20,7 +20,7 @@ SCALE = float(np.float32(1.0) / np.sqrt(np.float32(128.0)))
 
 def exe():
     sys.path.insert(0, os.path.join(ROOT, "tests", "cpp"))
-    import build as cpp_build
+    import build_dropin as cpp_build
 
     return str(cpp_build.BIN if cpp_build.BIN.exists() else cpp_build.build())
 
