@@ -27,15 +27,22 @@
 //     i.e. the MFMA's 8-key k slice taken as two 4-key runs in the
 //     accumulator's key order.
 //
-// Softmax bookkeeping (per query, raw scores s = q.k, c = scale * log2(e)):
-//   m_t  running true maximum of s (gives the reference's m = scale * m_t);
-//   m_s  the maximum the probabilities are currently scaled by. It is raised
-//        to m_t only when some score of the wave exceeds it by more than
-//        8 / c (probabilities would exceed 2^8), so O and l are rescaled
-//        rarely; at the end l is reported relative to m_t:
-//        l = sum exp(s - m) = l_s * exp2((m_s - m_t) * c).
+// Softmax bookkeeping, per query, in the log2 domain of the scaled score
+// s' = (scale * log2 e) * q.k (Q is pre-multiplied by scale * log2 e when its
+// fragment is loaded):
+//   m_t  running true maximum of s' (the reference's m is m_t / log2 e);
+//   m_s  the maximum the probabilities are currently taken relative to. The S
+//        MFMA chain starts from the accumulator -m_s, so it yields t = s' - m_s
+//        directly and p = exp2(t) needs no further arithmetic. m_s is raised
+//        to m_t only when some t of the wave exceeds 8 (p would exceed 2^8),
+//        so O and l are rescaled rarely; at the end l is reported relative to
+//        m_t: l = sum exp(s - m) = l_s * exp2(m_s - m_t).
+//   l    the row sum of the bf16 probabilities that enter the PV product,
+//        accumulated with v_dot2 against (1, 1).
 // Keys with k_pos > q_pos are masked (FlashAttention.cpp:102); a row with no
 // valid key is written as the reference's empty row (FlashAttention.cpp:165-174).
+// K and V tiles are read with buffer loads whose descriptor ends at the
+// sequence's last valid key, so rows past it load as zeros without branches.
 
 #include "dt_internal.h"
 
@@ -49,6 +56,7 @@ typedef float floatx2 __attribute__((ext_vector_type(2)));
 typedef short shortx4 __attribute__((ext_vector_type(4)));
 typedef short shortx8 __attribute__((ext_vector_type(8)));
 typedef __attribute__((address_space(3))) shortx4 lds_shortx4;
+typedef int intx4 __attribute__((ext_vector_type(4)));
 
 constexpr int kD = 128;
 constexpr int kBM = 128;       // queries per item
@@ -60,6 +68,7 @@ constexpr int kStage = kBN * kLdK + kBN * kLdV;  // bf16 elements per (K, V) sta
 constexpr float kLog2e = 1.4426950408889634f;
 constexpr float kNegInf = -__builtin_huge_valf();
 constexpr float kRescaleLog2 = 8.0f;
+constexpr int kBufferDword3 = 0x00020000;  // raw buffer, 32-bit data format (gfx9 family)
 
 __device__ __forceinline__ uint32_t pack_bf16x2(float lo, float hi) {
     bf16x2 r = __builtin_convertvector((floatx2){lo, hi}, bf16x2);
@@ -76,6 +85,18 @@ __device__ __forceinline__ float sum_halves(float x) { return x + __shfl_xor(x, 
 __device__ __forceinline__ shortx4 lds_read_tr16(const uint16_t* p) {
     return __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_shortx4*)(p));
 }
+
+// Buffer descriptor over [base, base + bytes): loads at or past the end return zeros.
+__device__ __forceinline__ __amdgpu_buffer_rsrc_t make_rsrc(const void* base, uint32_t bytes) {
+    return __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(base), (short)0, (int)bytes, kBufferDword3);
+}
+__device__ __forceinline__ uint4 buffer_load16(__amdgpu_buffer_rsrc_t r, uint32_t voff) {
+    const intx4 v = __builtin_amdgcn_raw_buffer_load_b128(r, (int)voff, 0, 0);
+    return __builtin_bit_cast(uint4, v);
+}
+
+__device__ __forceinline__ float bf16_lo(uint32_t w) { return __builtin_bit_cast(float, w << 16); }
+__device__ __forceinline__ float bf16_hi(uint32_t w) { return __builtin_bit_cast(float, w & 0xffff0000u); }
 
 struct Item {
     int b, h, qt;
@@ -105,6 +126,10 @@ __global__ __launch_bounds__(kThreads, 1) void flash_fwd_bf16_kernel(FlashArgs a
     const int ld_col = 8 * (gt & 15);
     const int tr_row = (lane & 15) >> 2;
     const int tr_col = 4 * (lane & 3) + 16 * ((lane >> 4) & 1);
+    // byte offsets of this thread's four 16-byte chunks within a K/V tile (K and V share the row stride)
+    uint32_t voff[4];
+#pragma unroll
+    for (int i = 0; i < 4; ++i) voff[i] = (uint32_t)(((ld_row + 16 * i) * a.ldk + ld_col) * 2);
 
     const int T = a.T;
     const int n_qt = (T + kBM - 1) / kBM;
@@ -112,7 +137,6 @@ __global__ __launch_bounds__(kThreads, 1) void flash_fwd_bf16_kernel(FlashArgs a
     const int n_items = n_qt * BH;
     const int G = gridDim.x;
     const float c = a.scale * kLog2e;
-    const float thr = kRescaleLog2 / c;
 
     uint16_t* const stage_base = smem + grp * 2 * kStage;
 
@@ -146,12 +170,19 @@ __global__ __launch_bounds__(kThreads, 1) void flash_fwd_bf16_kernel(FlashArgs a
         }
 
         // Q fragment: qf[cc] = Q[qrow][16*cc + 8*hh .. +8] (B operand of S^T = K Q^T)
+        // Q fragment, pre-multiplied by scale * log2 e: qf[cc] = Q[qrow][16*cc + 8*hh .. +8] * c
         bf16x8 qf[8];
         if (qrow < T) {
             const uint16_t* qp = Qg + (int64_t)qrow * a.ldq + 8 * hh;
 #pragma unroll
-            for (int cc = 0; cc < 8; ++cc)
-                qf[cc] = __builtin_bit_cast(bf16x8, *reinterpret_cast<const uint4*>(qp + 16 * cc));
+            for (int cc = 0; cc < 8; ++cc) {
+                const uint4 raw = *reinterpret_cast<const uint4*>(qp + 16 * cc);
+                const uint32_t w[4] = {raw.x, raw.y, raw.z, raw.w};
+                uint32_t sw[4];
+#pragma unroll
+                for (int e = 0; e < 4; ++e) sw[e] = pack_bf16x2(bf16_lo(w[e]) * c, bf16_hi(w[e]) * c);
+                qf[cc] = __builtin_bit_cast(bf16x8, make_uint4(sw[0], sw[1], sw[2], sw[3]));
+            }
         } else {
 #pragma unroll
             for (int cc = 0; cc < 8; ++cc) qf[cc] = __builtin_bit_cast(bf16x8, make_uint4(0, 0, 0, 0));
@@ -163,6 +194,9 @@ __global__ __launch_bounds__(kThreads, 1) void flash_fwd_bf16_kernel(FlashArgs a
 #pragma unroll
             for (int i = 0; i < 16; ++i) o[db][i] = 0.0f;
         float m_t = kNegInf, m_s = kNegInf, l_run = 0.0f;
+        floatx16 neg_ms;  // -m_s (0 while m_s is -inf), the starting accumulator of the S chain
+#pragma unroll
+        for (int i = 0; i < 16; ++i) neg_ms[i] = 0.0f;
 
         const int k_end = a.causal ? min(q0 + kBM, L) : L;
         const int n_tiles = (k_end + kBN - 1) / kBN;
@@ -170,16 +204,13 @@ __global__ __launch_bounds__(kThreads, 1) void flash_fwd_bf16_kernel(FlashArgs a
 
         uint4 pk_k[4], pk_v[4];
         auto fetch = [&](int k0) {
+            const uint32_t bytes = (uint32_t)(L - k0) * (uint32_t)a.ldk * 2u;  // rows k0 .. L-1
+            const __amdgpu_buffer_rsrc_t rk = make_rsrc(Kg + (int64_t)k0 * a.ldk, bytes);
+            const __amdgpu_buffer_rsrc_t rv = make_rsrc(Vg + (int64_t)k0 * a.ldk, bytes);
 #pragma unroll
             for (int i = 0; i < 4; ++i) {
-                const int key = k0 + ld_row + 16 * i;
-                if (key < L) {
-                    pk_k[i] = *reinterpret_cast<const uint4*>(&Kg[(int64_t)key * a.ldk + ld_col]);
-                    pk_v[i] = *reinterpret_cast<const uint4*>(&Vg[(int64_t)key * a.ldv + ld_col]);
-                } else {
-                    pk_k[i] = make_uint4(0, 0, 0, 0);
-                    pk_v[i] = make_uint4(0, 0, 0, 0);
-                }
+                pk_k[i] = buffer_load16(rk, voff[i]);
+                pk_v[i] = buffer_load16(rv, voff[i]);
             }
         };
         auto stash = [&](uint16_t* st) {
@@ -203,18 +234,16 @@ __global__ __launch_bounds__(kThreads, 1) void flash_fwd_bf16_kernel(FlashArgs a
             const int k0 = kt * kBN;
 
             if (kt < n_tiles && !(a.causal && k0 > qw0 + 31)) {
+                // t = s' - m_s: the chain starts from -m_s
                 floatx16 st[2];
-#pragma unroll
-                for (int kb = 0; kb < 2; ++kb)
-#pragma unroll
-                    for (int i = 0; i < 16; ++i) st[kb][i] = 0.0f;
 #pragma unroll
                 for (int cc = 0; cc < 8; ++cc)
 #pragma unroll
                     for (int kb = 0; kb < 2; ++kb) {
                         const bf16x8 kf = __builtin_bit_cast(
                             bf16x8, *reinterpret_cast<const uint4*>(&Ks[(32 * kb + ln) * kLdK + 16 * cc + 8 * hh]));
-                        st[kb] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(kf, qf[cc], st[kb], 0, 0, 0);
+                        st[kb] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(kf, qf[cc], cc == 0 ? neg_ms : st[kb], 0, 0,
+                                                                          0);
                     }
 
                 // diagonal / ragged-tail tiles: mask with selects (no per-element branches)
@@ -234,17 +263,29 @@ __global__ __launch_bounds__(kThreads, 1) void flash_fwd_bf16_kernel(FlashArgs a
 #pragma unroll
                     for (int i = 0; i < 16; ++i) tmax = fmaxf(tmax, st[kb][i]);
                 tmax = max_halves(tmax);
-                m_t = fmaxf(m_t, tmax);
-                if (__builtin_amdgcn_ballot_w64(tmax > m_s + thr) != 0) {  // wave-uniform, rare after warm-up
-                    const float alpha = (m_s == kNegInf) ? 0.0f : exp2f((m_s - m_t) * c);
-                    m_s = m_t;
+                const float base = (m_s == kNegInf) ? 0.0f : m_s;  // what the chain subtracted
+                m_t = fmaxf(m_t, tmax + base);
+                const bool grow = (m_s == kNegInf) ? (tmax > kNegInf) : (tmax > kRescaleLog2);
+                if (__builtin_amdgcn_ballot_w64(grow) != 0) {  // wave-uniform, rare after the first tile
+                    const float m_new = m_t;
+                    const float delta = (m_new == kNegInf) ? 0.0f : m_new - base;
+                    const float alpha = (m_s == kNegInf) ? 0.0f : exp2f(m_s - m_new);
+                    m_s = m_new;
                     l_run *= alpha;
 #pragma unroll
                     for (int db = 0; db < 4; ++db)
 #pragma unroll
                         for (int i = 0; i < 16; ++i) o[db][i] *= alpha;
+#pragma unroll
+                    for (int kb = 0; kb < 2; ++kb)
+#pragma unroll
+                        for (int i = 0; i < 16; ++i) st[kb][i] -= delta;
+                    const float nm = (m_s == kNegInf) ? 0.0f : -m_s;
+#pragma unroll
+                    for (int i = 0; i < 16; ++i) neg_ms[i] = nm;
                 }
-                const float mc = (m_s == kNegInf ? 0.0f : m_s) * c;
+                // p = exp2(t) in bf16; the row sum is taken over the bf16 values the PV product uses
+                const bf16x2 ones = {(__bf16)1.0f, (__bf16)1.0f};
                 float psum = 0.0f;
                 bf16x8 pb[2][2];
 #pragma unroll
@@ -254,10 +295,10 @@ __global__ __launch_bounds__(kThreads, 1) void flash_fwd_bf16_kernel(FlashArgs a
                         uint32_t w[4];
 #pragma unroll
                         for (int e = 0; e < 4; ++e) {
-                            const float p0 = __builtin_amdgcn_exp2f(__builtin_fmaf(st[kb][8 * u + 2 * e], c, -mc));
-                            const float p1 = __builtin_amdgcn_exp2f(__builtin_fmaf(st[kb][8 * u + 2 * e + 1], c, -mc));
-                            psum += p0 + p1;
-                            w[e] = pack_bf16x2(p0, p1);
+                            w[e] = pack_bf16x2(__builtin_amdgcn_exp2f(st[kb][8 * u + 2 * e]),
+                                               __builtin_amdgcn_exp2f(st[kb][8 * u + 2 * e + 1]));
+                            psum = __builtin_amdgcn_fdot2_f32_bf16(__builtin_bit_cast(bf16x2, w[e]), ones, psum,
+                                                                   false);
                         }
                         pb[kb][u] = __builtin_bit_cast(bf16x8, make_uint4(w[0], w[1], w[2], w[3]));
                     }
@@ -271,9 +312,9 @@ __global__ __launch_bounds__(kThreads, 1) void flash_fwd_bf16_kernel(FlashArgs a
                         const int kr = 32 * kb + 16 * u + 4 * hh + tr_row;
 #pragma unroll
                         for (int db = 0; db < 4; ++db) {
-                            const uint16_t* base = &Vs[kr * kLdV + 32 * db + tr_col];
-                            const shortx4 lo = lds_read_tr16(base);
-                            const shortx4 hi = lds_read_tr16(base + 8 * kLdV);
+                            const uint16_t* base_v = &Vs[kr * kLdV + 32 * db + tr_col];
+                            const shortx4 lo = lds_read_tr16(base_v);
+                            const shortx4 hi = lds_read_tr16(base_v + 8 * kLdV);
                             const bf16x8 vf = __builtin_bit_cast(
                                 bf16x8, (shortx8){lo[0], lo[1], lo[2], lo[3], hi[0], hi[1], hi[2], hi[3]});
                             o[db] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(vf, pb[kb][u], o[db], 0, 0, 0);
@@ -301,8 +342,8 @@ __global__ __launch_bounds__(kThreads, 1) void flash_fwd_bf16_kernel(FlashArgs a
             const float m1t = xo[4096 + 64 + lane];
             const float l1 = xo[4096 + 128 + lane];
             const float ms = fmaxf(m_s, m1s);
-            const float a0 = (m_s == kNegInf) ? 0.0f : exp2f((m_s - ms) * c);
-            const float a1 = (m1s == kNegInf) ? 0.0f : exp2f((m1s - ms) * c);
+            const float a0 = (m_s == kNegInf) ? 0.0f : exp2f(m_s - ms);
+            const float a1 = (m1s == kNegInf) ? 0.0f : exp2f(m1s - ms);
             const float l = l_run * a0 + l1 * a1;
             const float mt = fmaxf(m_t, m1t);
             if (qrow < T) {
@@ -326,8 +367,8 @@ __global__ __launch_bounds__(kThreads, 1) void flash_fwd_bf16_kernel(FlashArgs a
                         *reinterpret_cast<uint2*>(&op[32 * db + 8 * I + 4 * hh]) = w;
                     }
                 if (hh == 0) {
-                    if (a.m) a.m[stat_base + (int64_t)qrow * a.H] = valid ? mt * a.scale : kNegInf;
-                    if (a.l) a.l[stat_base + (int64_t)qrow * a.H] = valid ? l * exp2f((ms - mt) * c) : 0.0f;
+                    if (a.m) a.m[stat_base + (int64_t)qrow * a.H] = valid ? mt * (1.0f / kLog2e) : kNegInf;
+                    if (a.l) a.l[stat_base + (int64_t)qrow * a.H] = valid ? l * exp2f(ms - mt) : 0.0f;
                 }
             }
         }
@@ -351,6 +392,9 @@ int launch_flash_fwd_bf16(const FlashArgs& a, const SeqLens* lens, hipStream_t s
         DT_HIP_TRY(hipDeviceGetAttribute(&n, hipDeviceAttributeMultiprocessorCount, dev));
         g_num_cus[dev] = n > 0 ? n : 1;
     }
+    if (a.ldk != a.ldv) return set_error(DT_ERR_UNSUPPORTED, "bf16 kernel needs equal K and V row strides");
+    if ((int64_t)a.T * a.ldk * 2 >= ((int64_t)1 << 31))
+        return set_error(DT_ERR_UNSUPPORTED, "K/V extent of one sequence exceeds 2 GiB");
     const int64_t n_items = (int64_t)((a.T + kBM - 1) / kBM) * a.B * a.H;
     if (n_items > 0x7fffffff) return set_error(DT_ERR_UNSUPPORTED, "too many attention items");
     const int grid = (int)(n_items < g_num_cus[dev] ? n_items : g_num_cus[dev]);
