@@ -11,20 +11,26 @@
 //     T = 4096, H = 16 every workgroup gets 33 key tiles of work.
 //   * A workgroup has 8 waves in two groups of 4. Both groups hold the same 128
 //     queries (32 per wave) and split the key tiles: group g takes 64-key tiles
-//     g, g+2, g+4, ... Each group streams its tiles through its own pair of LDS
-//     buffers (double buffering, one barrier per step). At the end group 1
-//     hands its partial (max, sum, O) to group 0 through LDS and group 0 merges
-//     them with the same rescale the reference applies between tiles
-//     (FlashAttention.cpp:134-156).
+//     g, g+2, g+4, ... At the end group 1 hands its partial (max, sum, O) to
+//     group 0 through LDS and group 0 merges them with the same rescale the
+//     reference applies between tiles (FlashAttention.cpp:134-156).
+//   * K and V tiles move from HBM straight into LDS with buffer_load ... lds
+//     (no staging registers), double-buffered in two LDS arrays: while a step
+//     computes on one array, the next tile streams into the other; one barrier
+//     per step. The descriptors end at the sequence's last valid key, so rows
+//     past it arrive as zeros. LDS rows are 256 bytes, unpadded; the 16-byte
+//     chunk c of row r is stored at chunk position c ^ f(r),
+//     f(r) = 4*(r & 3) + ((r >> 2) & 3), which keeps both the row-wise K reads
+//     and the transposing V reads free of bank conflicts.
 //   * Within a wave, S^T = K Q^T comes from v_mfma_f32_32x32x16_bf16 with K
 //     rows from LDS as the A operand and the wave's Q fragment, held in
 //     registers, as B; one lane then owns one query and 16 keys per 32-key
 //     block, so the row max and row sum are a per-lane reduction plus one
 //     exchange between the lane halves. P is converted to bf16 in registers
-//     and used as the B operand of O^T += V^T P^T; the A operand (V^T) comes from the gfx950
-//     transposing LDS read ds_read_b64_tr_b16, where a 16-lane group reads a
-//     4-key x 16-dim block and each lane receives one dim column of 4 keys,
-//     i.e. the MFMA's 8-key k slice taken as two 4-key runs in the
+//     and used as the B operand of O^T += V^T P^T; the A operand (V^T) comes
+//     from the gfx950 transposing LDS read ds_read_b64_tr_b16, where a 16-lane
+//     group reads a 4-key x 16-dim block and each lane receives one dim column
+//     of 4 keys, i.e. the MFMA's 8-key k slice taken as two 4-key runs in the
 //     accumulator's key order.
 //
 // Softmax bookkeeping, per query, in the log2 domain of the scaled score
@@ -41,8 +47,6 @@
 //        accumulated with v_dot2 against (1, 1).
 // Keys with k_pos > q_pos are masked (FlashAttention.cpp:102); a row with no
 // valid key is written as the reference's empty row (FlashAttention.cpp:165-174).
-// K and V tiles are read with buffer loads whose descriptor ends at the
-// sequence's last valid key, so rows past it load as zeros without branches.
 
 #include "dt_internal.h"
 
@@ -56,19 +60,21 @@ typedef float floatx2 __attribute__((ext_vector_type(2)));
 typedef short shortx4 __attribute__((ext_vector_type(4)));
 typedef short shortx8 __attribute__((ext_vector_type(8)));
 typedef __attribute__((address_space(3))) shortx4 lds_shortx4;
-typedef int intx4 __attribute__((ext_vector_type(4)));
+typedef __attribute__((address_space(3))) void lds_void;
 
 constexpr int kD = 128;
 constexpr int kBM = 128;       // queries per item
 constexpr int kBN = 64;        // keys per tile
 constexpr int kThreads = 512;  // 8 waves
-constexpr int kLdK = 136;      // bf16 elements per K row in LDS (272 B: b128 row reads hit distinct banks)
-constexpr int kLdV = 160;      // bf16 elements per V row in LDS (320 B: transposing reads hit distinct banks)
-constexpr int kStage = kBN * kLdK + kBN * kLdV;  // bf16 elements per (K, V) stage
+constexpr int kRowBytes = 256;               // one K or V row (128 bf16), unpadded
+constexpr int kTileBytes = kBN * kRowBytes;  // 16 KB per tensor per tile
 constexpr float kLog2e = 1.4426950408889634f;
 constexpr float kNegInf = -__builtin_huge_valf();
 constexpr float kRescaleLog2 = 8.0f;
 constexpr int kBufferDword3 = 0x00020000;  // raw buffer, 32-bit data format (gfx9 family)
+
+// one LDS stage: [group][K, V][tile bytes]
+typedef uint8_t Stage[2][2][kTileBytes];
 
 __device__ __forceinline__ uint32_t pack_bf16x2(float lo, float hi) {
     bf16x2 r = __builtin_convertvector((floatx2){lo, hi}, bf16x2);
@@ -82,7 +88,7 @@ __device__ __forceinline__ uint32_t pack_bf16x2(float lo, float hi) {
 __device__ __forceinline__ float max_halves(float x) { return fmaxf(x, __shfl_xor(x, 32, 64)); }
 __device__ __forceinline__ float sum_halves(float x) { return x + __shfl_xor(x, 32, 64); }
 
-__device__ __forceinline__ shortx4 lds_read_tr16(const uint16_t* p) {
+__device__ __forceinline__ shortx4 lds_read_tr16(const uint8_t* p) {
     return __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_shortx4*)(p));
 }
 
@@ -90,13 +96,12 @@ __device__ __forceinline__ shortx4 lds_read_tr16(const uint16_t* p) {
 __device__ __forceinline__ __amdgpu_buffer_rsrc_t make_rsrc(const void* base, uint32_t bytes) {
     return __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(base), (short)0, (int)bytes, kBufferDword3);
 }
-__device__ __forceinline__ uint4 buffer_load16(__amdgpu_buffer_rsrc_t r, uint32_t voff) {
-    const intx4 v = __builtin_amdgcn_raw_buffer_load_b128(r, (int)voff, 0, 0);
-    return __builtin_bit_cast(uint4, v);
-}
 
 __device__ __forceinline__ float bf16_lo(uint32_t w) { return __builtin_bit_cast(float, w << 16); }
 __device__ __forceinline__ float bf16_hi(uint32_t w) { return __builtin_bit_cast(float, w & 0xffff0000u); }
+
+// chunk swizzle of an LDS row: chunk c of row r lives at position c ^ swz(r)
+__device__ __forceinline__ int swz(int r) { return ((r & 3) << 2) | ((r >> 2) & 3); }
 
 struct Item {
     int b, h, qt;
@@ -111,25 +116,150 @@ __device__ __forceinline__ Item decode_item(int k, int n_qt, int BH, int H) {
     return it;
 }
 
+// Per-wave state of one item.
+struct Acc {
+    floatx16 o[4];    // O^T: o[db][i] = O[qrow][32*db + 8*(i/4) + 4*hh + (i%4)] (unnormalised)
+    floatx16 neg_ms;  // -m_s (0 while m_s is -inf), the starting accumulator of the S chain
+    float m_t, m_s, l;
+};
+
+// One 64-key tile for one wave: S^T, softmax update, O^T += V^T P^T.
+// kaddr[cc]: byte offset of this lane's K fragment for chunk cc within a K tile (block kb = 0);
+// vaddr[s][db]: byte offset of this lane's transposing read for read s and dim block db
+// (16-key chunk 0; chunk (kb, u) adds 8192*kb + 4096*u).
+__device__ __forceinline__ void tile_step(Acc& A, const bf16x8 (&qf)[8], const uint8_t* Ks, const uint8_t* Vs,
+                                          const uint32_t (&kaddr)[8], const uint32_t (&vaddr)[2][4], int k0,
+                                          bool need_mask, int lim, int hh) {
+    floatx16 st[2];
+#pragma unroll
+    for (int cc = 0; cc < 8; ++cc)
+#pragma unroll
+        for (int kb = 0; kb < 2; ++kb) {
+            const bf16x8 kf =
+                __builtin_bit_cast(bf16x8, *reinterpret_cast<const uint4*>(Ks + kaddr[cc] + kb * 8192));
+            st[kb] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(kf, qf[cc], cc == 0 ? A.neg_ms : st[kb], 0, 0, 0);
+        }
+
+    if (need_mask) {  // diagonal / ragged-tail tiles: selects, no per-element branches
+#pragma unroll
+        for (int kb = 0; kb < 2; ++kb)
+#pragma unroll
+            for (int i = 0; i < 16; ++i) {
+                const int key = k0 + 32 * kb + 8 * (i / 4) + 4 * hh + (i % 4);
+                st[kb][i] = key > lim ? kNegInf : st[kb][i];
+            }
+    }
+    float tmax = kNegInf;
+#pragma unroll
+    for (int kb = 0; kb < 2; ++kb)
+#pragma unroll
+        for (int i = 0; i < 16; ++i) tmax = fmaxf(tmax, st[kb][i]);
+    tmax = max_halves(tmax);
+    const float base = (A.m_s == kNegInf) ? 0.0f : A.m_s;  // what the S chain subtracted
+    A.m_t = fmaxf(A.m_t, tmax + base);
+    const bool grow = (A.m_s == kNegInf) ? (tmax > kNegInf) : (tmax > kRescaleLog2);
+    if (__builtin_amdgcn_ballot_w64(grow) != 0) {  // wave-uniform, rare after the first tile
+        const float m_new = A.m_t;
+        const float delta = (m_new == kNegInf) ? 0.0f : m_new - base;
+        const float alpha = (A.m_s == kNegInf) ? 0.0f : exp2f(A.m_s - m_new);
+        A.m_s = m_new;
+        A.l *= alpha;
+#pragma unroll
+        for (int db = 0; db < 4; ++db)
+#pragma unroll
+            for (int i = 0; i < 16; ++i) A.o[db][i] *= alpha;
+#pragma unroll
+        for (int kb = 0; kb < 2; ++kb)
+#pragma unroll
+            for (int i = 0; i < 16; ++i) st[kb][i] -= delta;
+        const float nm = (A.m_s == kNegInf) ? 0.0f : -A.m_s;
+#pragma unroll
+        for (int i = 0; i < 16; ++i) A.neg_ms[i] = nm;
+    }
+    // p = exp2(t) in bf16; the row sum is over the bf16 values the PV product uses
+    const bf16x2 ones = {(__bf16)1.0f, (__bf16)1.0f};
+    float psum = 0.0f;
+    bf16x8 pb[2][2];
+#pragma unroll
+    for (int kb = 0; kb < 2; ++kb)
+#pragma unroll
+        for (int u = 0; u < 2; ++u) {
+            uint32_t w[4];
+#pragma unroll
+            for (int e = 0; e < 4; ++e) {
+                w[e] = pack_bf16x2(__builtin_amdgcn_exp2f(st[kb][8 * u + 2 * e]),
+                                   __builtin_amdgcn_exp2f(st[kb][8 * u + 2 * e + 1]));
+                psum = __builtin_amdgcn_fdot2_f32_bf16(__builtin_bit_cast(bf16x2, w[e]), ones, psum, false);
+            }
+            pb[kb][u] = __builtin_bit_cast(bf16x8, make_uint4(w[0], w[1], w[2], w[3]));
+        }
+    A.l += sum_halves(psum);
+
+    // O^T += V^T P^T; chunk (kb, u): k index 8*hh + e <-> key 32*kb + 16*u + 8*(e/4) + 4*hh + (e%4)
+#pragma unroll
+    for (int kb = 0; kb < 2; ++kb)
+#pragma unroll
+        for (int u = 0; u < 2; ++u)
+#pragma unroll
+            for (int db = 0; db < 4; ++db) {
+                const int rows = kb * 8192 + u * 4096;
+                const shortx4 lo = lds_read_tr16(Vs + vaddr[0][db] + rows);
+                const shortx4 hi = lds_read_tr16(Vs + vaddr[1][db] + rows + 2048);
+                const bf16x8 vf =
+                    __builtin_bit_cast(bf16x8, (shortx8){lo[0], lo[1], lo[2], lo[3], hi[0], hi[1], hi[2], hi[3]});
+                A.o[db] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(vf, pb[kb][u], A.o[db], 0, 0, 0);
+            }
+}
+
+// Barrier for the double-buffered loop: this wave's LDS DMA and LDS accesses are
+// complete before any wave passes it.
+__device__ __forceinline__ void stage_barrier() { asm volatile("s_waitcnt vmcnt(0) lgkmcnt(0)\n\ts_barrier" ::: "memory"); }
+
 __global__ __launch_bounds__(kThreads, 1) void flash_fwd_bf16_kernel(FlashArgs a, SeqLens lens) {
-    __shared__ __attribute__((aligned(16))) uint16_t smem[2 * 2 * kStage];
+    __shared__ __attribute__((aligned(1024))) Stage stage0;
+    __shared__ __attribute__((aligned(1024))) Stage stage1;
 
     const int tid = threadIdx.x;
     const int lane = tid & 63;
     const int wave = tid >> 6;
     const int grp = wave >> 2;  // key-tile group
-    const int wq = wave & 3;    // 32-query block within the item
+    const int wq = wave & 3;    // 32-query block within the item (also this wave's share of a DMA tile)
     const int ln = lane & 31;
     const int hh = lane >> 5;
-    const int gt = tid & 255;  // thread index within the group
-    const int ld_row = gt >> 4;
-    const int ld_col = 8 * (gt & 15);
-    const int tr_row = (lane & 15) >> 2;
-    const int tr_col = 4 * (lane & 3) + 16 * ((lane >> 4) & 1);
-    // byte offsets of this thread's four 16-byte chunks within a K/V tile (K and V share the row stride)
+
+    // DMA: instruction i of wave wq fills rows 16*i + 4*wq + lane/16 of a tile, 16 bytes per lane at
+    // chunk position lane%16; the lane fetches the global chunk that the swizzle puts there.
     uint32_t voff[4];
+    {
+        const int rlo = lane >> 4;
+        const int chunk = (lane & 15) ^ (4 * rlo + wq);  // swz(16*i + 4*wq + rlo) does not depend on i
 #pragma unroll
-    for (int i = 0; i < 4; ++i) voff[i] = (uint32_t)(((ld_row + 16 * i) * a.ldk + ld_col) * 2);
+        for (int i = 0; i < 4; ++i) voff[i] = (uint32_t)(((16 * i + 4 * wq + rlo) * a.ldk + 8 * chunk) * 2);
+    }
+    // K fragment reads: row 32*kb + ln, chunk 2*cc + hh
+    uint32_t kaddr[8];
+    {
+        const int g = hh ^ swz(ln);
+#pragma unroll
+        for (int cc = 0; cc < 8; ++cc) kaddr[cc] = (uint32_t)(ln * kRowBytes + (((2 * cc) ^ g) << 4));
+    }
+    // V transposing reads: lane i of 16-lane group G reads row 4*hh + i/4 (+8 for the second read)
+    // of a 16-key chunk, dims 32*db + 16*(G&1) + 4*(i&3) .. +3
+    uint32_t vaddr[2][4];
+    {
+        const int i16 = lane & 15;
+        const int tr_row = i16 >> 2;
+        const int g2 = (lane >> 4) & 1;
+#pragma unroll
+        for (int s = 0; s < 2; ++s) {
+            const int r = 4 * hh + tr_row + 8 * s;
+#pragma unroll
+            for (int db = 0; db < 4; ++db) {
+                const int chunk = 4 * db + 2 * g2 + ((i16 & 3) >> 1);
+                vaddr[s][db] = (uint32_t)((r - 8 * s) * kRowBytes + ((chunk ^ swz(r)) << 4) + 8 * (i16 & 1));
+            }
+        }
+    }
 
     const int T = a.T;
     const int n_qt = (T + kBM - 1) / kBM;
@@ -137,8 +267,6 @@ __global__ __launch_bounds__(kThreads, 1) void flash_fwd_bf16_kernel(FlashArgs a
     const int n_items = n_qt * BH;
     const int G = gridDim.x;
     const float c = a.scale * kLog2e;
-
-    uint16_t* const stage_base = smem + grp * 2 * kStage;
 
     for (int round = 0;; ++round) {
         const int k_item = (round & 1) ? (round + 1) * G - 1 - (int)blockIdx.x : round * G + (int)blockIdx.x;
@@ -169,7 +297,6 @@ __global__ __launch_bounds__(kThreads, 1) void flash_fwd_bf16_kernel(FlashArgs a
             continue;  // no LDS was touched: no barrier needed
         }
 
-        // Q fragment: qf[cc] = Q[qrow][16*cc + 8*hh .. +8] (B operand of S^T = K Q^T)
         // Q fragment, pre-multiplied by scale * log2 e: qf[cc] = Q[qrow][16*cc + 8*hh .. +8] * c
         bf16x8 qf[8];
         if (qrow < T) {
@@ -188,164 +315,79 @@ __global__ __launch_bounds__(kThreads, 1) void flash_fwd_bf16_kernel(FlashArgs a
             for (int cc = 0; cc < 8; ++cc) qf[cc] = __builtin_bit_cast(bf16x8, make_uint4(0, 0, 0, 0));
         }
 
-        floatx16 o[4];
+        Acc A;
 #pragma unroll
         for (int db = 0; db < 4; ++db)
 #pragma unroll
-            for (int i = 0; i < 16; ++i) o[db][i] = 0.0f;
-        float m_t = kNegInf, m_s = kNegInf, l_run = 0.0f;
-        floatx16 neg_ms;  // -m_s (0 while m_s is -inf), the starting accumulator of the S chain
+            for (int i = 0; i < 16; ++i) A.o[db][i] = 0.0f;
 #pragma unroll
-        for (int i = 0; i < 16; ++i) neg_ms[i] = 0.0f;
+        for (int i = 0; i < 16; ++i) A.neg_ms[i] = 0.0f;
+        A.m_t = kNegInf;
+        A.m_s = kNegInf;
+        A.l = 0.0f;
 
         const int k_end = a.causal ? min(q0 + kBM, L) : L;
         const int n_tiles = (k_end + kBN - 1) / kBN;
         const int n_iter = (n_tiles + 1) / 2;
 
-        uint4 pk_k[4], pk_v[4];
-        auto fetch = [&](int k0) {
+        // tile kt of this group -> one LDS stage, straight from HBM
+        auto dma = [&](Stage& stg, int kt) {
+            const int k0 = kt * kBN;
             const uint32_t bytes = (uint32_t)(L - k0) * (uint32_t)a.ldk * 2u;  // rows k0 .. L-1
             const __amdgpu_buffer_rsrc_t rk = make_rsrc(Kg + (int64_t)k0 * a.ldk, bytes);
             const __amdgpu_buffer_rsrc_t rv = make_rsrc(Vg + (int64_t)k0 * a.ldk, bytes);
 #pragma unroll
             for (int i = 0; i < 4; ++i) {
-                pk_k[i] = buffer_load16(rk, voff[i]);
-                pk_v[i] = buffer_load16(rv, voff[i]);
+                __builtin_amdgcn_raw_ptr_buffer_load_lds(rk, (lds_void*)&stg[grp][0][(4 * i + wq) * 1024], 16,
+                                                         voff[i], 0, 0, 0);
+                __builtin_amdgcn_raw_ptr_buffer_load_lds(rv, (lds_void*)&stg[grp][1][(4 * i + wq) * 1024], 16,
+                                                         voff[i], 0, 0, 0);
             }
         };
-        auto stash = [&](uint16_t* st) {
-#pragma unroll
-            for (int i = 0; i < 4; ++i) {
-                *reinterpret_cast<uint4*>(&st[(ld_row + 16 * i) * kLdK + ld_col]) = pk_k[i];
-                *reinterpret_cast<uint4*>(&st[kBN * kLdK + (ld_row + 16 * i) * kLdV + ld_col]) = pk_v[i];
-            }
-        };
-
-        if (grp < n_tiles) fetch(grp * kBN);
-        stash(stage_base);
-        __syncthreads();
-
-        for (int it = 0; it < n_iter; ++it) {
-            const int kt = 2 * it + grp;
-            const int kt_next = kt + 2;
-            if (kt_next < n_tiles) fetch(kt_next * kBN);
-            const uint16_t* Ks = stage_base + (it & 1) * kStage;
-            const uint16_t* Vs = Ks + kBN * kLdK;
+        auto compute = [&](const Stage& stg, int kt) {
             const int k0 = kt * kBN;
+            if (kt >= n_tiles || (a.causal && k0 > qw0 + 31)) return;  // nothing of this tile is visible
+            const bool need_mask = (a.causal && k0 + kBN - 1 > qw0) || k0 + kBN > L;
+            const int lim = a.causal ? min(qrow, L - 1) : L - 1;  // keys > lim are masked
+            tile_step(A, qf, stg[grp][0], stg[grp][1], kaddr, vaddr, k0, need_mask, lim, hh);
+        };
 
-            if (kt < n_tiles && !(a.causal && k0 > qw0 + 31)) {
-                // t = s' - m_s: the chain starts from -m_s
-                floatx16 st[2];
-#pragma unroll
-                for (int cc = 0; cc < 8; ++cc)
-#pragma unroll
-                    for (int kb = 0; kb < 2; ++kb) {
-                        const bf16x8 kf = __builtin_bit_cast(
-                            bf16x8, *reinterpret_cast<const uint4*>(&Ks[(32 * kb + ln) * kLdK + 16 * cc + 8 * hh]));
-                        st[kb] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(kf, qf[cc], cc == 0 ? neg_ms : st[kb], 0, 0,
-                                                                          0);
-                    }
-
-                // diagonal / ragged-tail tiles: mask with selects (no per-element branches)
-                if ((a.causal && k0 + kBN - 1 > qw0) || k0 + kBN > L) {
-                    const int lim = a.causal ? min(qrow, L - 1) : L - 1;  // keys > lim are masked
-#pragma unroll
-                    for (int kb = 0; kb < 2; ++kb)
-#pragma unroll
-                        for (int i = 0; i < 16; ++i) {
-                            const int key = k0 + 32 * kb + 8 * (i / 4) + 4 * hh + (i % 4);
-                            st[kb][i] = key > lim ? kNegInf : st[kb][i];
-                        }
-                }
-                float tmax = kNegInf;
-#pragma unroll
-                for (int kb = 0; kb < 2; ++kb)
-#pragma unroll
-                    for (int i = 0; i < 16; ++i) tmax = fmaxf(tmax, st[kb][i]);
-                tmax = max_halves(tmax);
-                const float base = (m_s == kNegInf) ? 0.0f : m_s;  // what the chain subtracted
-                m_t = fmaxf(m_t, tmax + base);
-                const bool grow = (m_s == kNegInf) ? (tmax > kNegInf) : (tmax > kRescaleLog2);
-                if (__builtin_amdgcn_ballot_w64(grow) != 0) {  // wave-uniform, rare after the first tile
-                    const float m_new = m_t;
-                    const float delta = (m_new == kNegInf) ? 0.0f : m_new - base;
-                    const float alpha = (m_s == kNegInf) ? 0.0f : exp2f(m_s - m_new);
-                    m_s = m_new;
-                    l_run *= alpha;
-#pragma unroll
-                    for (int db = 0; db < 4; ++db)
-#pragma unroll
-                        for (int i = 0; i < 16; ++i) o[db][i] *= alpha;
-#pragma unroll
-                    for (int kb = 0; kb < 2; ++kb)
-#pragma unroll
-                        for (int i = 0; i < 16; ++i) st[kb][i] -= delta;
-                    const float nm = (m_s == kNegInf) ? 0.0f : -m_s;
-#pragma unroll
-                    for (int i = 0; i < 16; ++i) neg_ms[i] = nm;
-                }
-                // p = exp2(t) in bf16; the row sum is taken over the bf16 values the PV product uses
-                const bf16x2 ones = {(__bf16)1.0f, (__bf16)1.0f};
-                float psum = 0.0f;
-                bf16x8 pb[2][2];
-#pragma unroll
-                for (int kb = 0; kb < 2; ++kb)
-#pragma unroll
-                    for (int u = 0; u < 2; ++u) {
-                        uint32_t w[4];
-#pragma unroll
-                        for (int e = 0; e < 4; ++e) {
-                            w[e] = pack_bf16x2(__builtin_amdgcn_exp2f(st[kb][8 * u + 2 * e]),
-                                               __builtin_amdgcn_exp2f(st[kb][8 * u + 2 * e + 1]));
-                            psum = __builtin_amdgcn_fdot2_f32_bf16(__builtin_bit_cast(bf16x2, w[e]), ones, psum,
-                                                                   false);
-                        }
-                        pb[kb][u] = __builtin_bit_cast(bf16x8, make_uint4(w[0], w[1], w[2], w[3]));
-                    }
-                l_run += sum_halves(psum);
-
-                // O^T += V^T P^T; chunk (kb, u): k index 8*hh + e <-> key 32*kb + 16*u + 8*(e/4) + 4*hh + (e%4)
-#pragma unroll
-                for (int kb = 0; kb < 2; ++kb)
-#pragma unroll
-                    for (int u = 0; u < 2; ++u) {
-                        const int kr = 32 * kb + 16 * u + 4 * hh + tr_row;
-#pragma unroll
-                        for (int db = 0; db < 4; ++db) {
-                            const uint16_t* base_v = &Vs[kr * kLdV + 32 * db + tr_col];
-                            const shortx4 lo = lds_read_tr16(base_v);
-                            const shortx4 hi = lds_read_tr16(base_v + 8 * kLdV);
-                            const bf16x8 vf = __builtin_bit_cast(
-                                bf16x8, (shortx8){lo[0], lo[1], lo[2], lo[3], hi[0], hi[1], hi[2], hi[3]});
-                            o[db] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(vf, pb[kb][u], o[db], 0, 0, 0);
-                        }
-                    }
-            }
-            if (it + 1 < n_iter) stash(stage_base + ((it + 1) & 1) * kStage);
-            __syncthreads();
+        if (grp < n_tiles) dma(stage0, grp);
+        stage_barrier();
+        for (int it = 0; it < n_iter; it += 2) {
+            // even step: compute from stage0 while the group's next tile streams into stage1
+            if (2 * (it + 1) + grp < n_tiles) dma(stage1, 2 * (it + 1) + grp);
+            compute(stage0, 2 * it + grp);
+            stage_barrier();
+            if (it + 1 >= n_iter) break;
+            // odd step: compute from stage1 while the tile after it streams into stage0
+            if (2 * (it + 2) + grp < n_tiles) dma(stage0, 2 * (it + 2) + grp);
+            compute(stage1, 2 * (it + 1) + grp);
+            stage_barrier();
         }
 
-        // merge the two groups' partial results through LDS (the stage buffers are free now)
-        float* xo = reinterpret_cast<float*>(smem) + wq * (64 * 64 + 3 * 64);
+        // merge the two groups' partial results through LDS (no DMA is in flight now)
+        float* xo = reinterpret_cast<float*>(&stage0[0][0][0]) + wq * (64 * 64);
+        float* xs = reinterpret_cast<float*>(&stage1[0][0][0]) + wq * (3 * 64);
         if (grp == 1) {
 #pragma unroll
             for (int db = 0; db < 4; ++db)
 #pragma unroll
-                for (int i = 0; i < 16; ++i) xo[(16 * db + i) * 64 + lane] = o[db][i];
-            xo[4096 + lane] = m_s;
-            xo[4096 + 64 + lane] = m_t;
-            xo[4096 + 128 + lane] = l_run;
+                for (int i = 0; i < 16; ++i) xo[(16 * db + i) * 64 + lane] = A.o[db][i];
+            xs[lane] = A.m_s;
+            xs[64 + lane] = A.m_t;
+            xs[128 + lane] = A.l;
         }
         __syncthreads();
         if (grp == 0) {
-            const float m1s = xo[4096 + lane];
-            const float m1t = xo[4096 + 64 + lane];
-            const float l1 = xo[4096 + 128 + lane];
-            const float ms = fmaxf(m_s, m1s);
-            const float a0 = (m_s == kNegInf) ? 0.0f : exp2f(m_s - ms);
+            const float m1s = xs[lane];
+            const float m1t = xs[64 + lane];
+            const float l1 = xs[128 + lane];
+            const float ms = fmaxf(A.m_s, m1s);
+            const float a0 = (A.m_s == kNegInf) ? 0.0f : exp2f(A.m_s - ms);
             const float a1 = (m1s == kNegInf) ? 0.0f : exp2f(m1s - ms);
-            const float l = l_run * a0 + l1 * a1;
-            const float mt = fmaxf(m_t, m1t);
+            const float l = A.l * a0 + l1 * a1;
+            const float mt = fmaxf(A.m_t, m1t);
             if (qrow < T) {
                 const bool valid = qrow < L && l > 0.0f;
                 const float inv = valid ? 1.0f / l : 0.0f;
@@ -359,7 +401,7 @@ __global__ __launch_bounds__(kThreads, 1) void flash_fwd_bf16_kernel(FlashArgs a
 #pragma unroll
                         for (int r = 0; r < 4; ++r) {
                             const int i = 4 * I + r;
-                            v[r] = o[db][i] * s0 + xo[(16 * db + i) * 64 + lane] * s1;
+                            v[r] = A.o[db][i] * s0 + xo[(16 * db + i) * 64 + lane] * s1;
                         }
                         uint2 w;
                         w.x = pack_bf16x2(v[0], v[1]);
@@ -384,6 +426,9 @@ int launch_flash_fwd_bf16(const FlashArgs& a, const SeqLens* lens, hipStream_t s
     SeqLens sl;
     if (a.ragged) sl = *lens;
     else sl.len[0] = a.T;
+    if (a.ldk != a.ldv) return set_error(DT_ERR_UNSUPPORTED, "bf16 kernel needs equal K and V row strides");
+    if ((int64_t)a.T * a.ldk * 2 >= ((int64_t)1 << 31))
+        return set_error(DT_ERR_UNSUPPORTED, "K/V extent of one sequence exceeds 2 GiB");
     int dev = 0;
     DT_HIP_TRY(hipGetDevice(&dev));
     if (dev < 0 || dev >= 64) return set_error(DT_ERR_UNSUPPORTED, "device index %d out of range", dev);
@@ -392,9 +437,6 @@ int launch_flash_fwd_bf16(const FlashArgs& a, const SeqLens* lens, hipStream_t s
         DT_HIP_TRY(hipDeviceGetAttribute(&n, hipDeviceAttributeMultiprocessorCount, dev));
         g_num_cus[dev] = n > 0 ? n : 1;
     }
-    if (a.ldk != a.ldv) return set_error(DT_ERR_UNSUPPORTED, "bf16 kernel needs equal K and V row strides");
-    if ((int64_t)a.T * a.ldk * 2 >= ((int64_t)1 << 31))
-        return set_error(DT_ERR_UNSUPPORTED, "K/V extent of one sequence exceeds 2 GiB");
     const int64_t n_items = (int64_t)((a.T + kBM - 1) / kBM) * a.B * a.H;
     if (n_items > 0x7fffffff) return set_error(DT_ERR_UNSUPPORTED, "too many attention items");
     const int grid = (int)(n_items < g_num_cus[dev] ? n_items : g_num_cus[dev]);
