@@ -30,6 +30,7 @@ HIPCC_FLAGS = [
     "-Xclang", "-target-feature", "-Xclang", "-packed-fp32-ops",
     "-Wall",
     "-Wno-unused-command-line-argument",
+    f"-I{PKG.parent / 'include'}",
 ]
 
 

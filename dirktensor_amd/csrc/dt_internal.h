@@ -6,7 +6,7 @@
 #include <cstdint>
 #include <string>
 
-#include "../../include/dirktensor_amd.h"
+#include "dirktensor_amd.h"  // include/, on the include path
 
 namespace dt {
 

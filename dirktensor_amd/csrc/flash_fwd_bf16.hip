@@ -45,6 +45,10 @@
 //        m_t: l = sum exp(s - m) = l_s * exp2(m_s - m_t).
 //   l    the row sum of the bf16 probabilities that enter the PV product,
 //        accumulated with v_dot2 against (1, 1).
+// The two lane halves that share a query keep their own m_t and l (over their
+// own keys) and exchange them only when m_s must move and once at the end, so
+// the common path of a tile has no cross-lane traffic; m_s itself is always
+// the same in both halves.
 // Keys with k_pos > q_pos are masked (FlashAttention.cpp:102); a row with no
 // valid key is written as the reference's empty row (FlashAttention.cpp:165-174).
 
@@ -139,8 +143,18 @@ __device__ __forceinline__ void tile_step(Acc& A, const bf16x8 (&qf)[8], const u
                 __builtin_bit_cast(bf16x8, *reinterpret_cast<const uint4*>(Ks + kaddr[cc] + kb * 8192));
             st[kb] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(kf, qf[cc], cc == 0 ? A.neg_ms : st[kb], 0, 0, 0);
         }
+    // keep the K fragment reads four ahead of the MFMAs that consume them
+    __builtin_amdgcn_sched_group_barrier(0x100, 4, 0);
+#define DT_MFMA_READ                                   \
+    __builtin_amdgcn_sched_group_barrier(0x008, 1, 0); \
+    __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);
+    DT_MFMA_READ DT_MFMA_READ DT_MFMA_READ DT_MFMA_READ DT_MFMA_READ DT_MFMA_READ
+    DT_MFMA_READ DT_MFMA_READ DT_MFMA_READ DT_MFMA_READ DT_MFMA_READ DT_MFMA_READ
+#undef DT_MFMA_READ
+    __builtin_amdgcn_sched_group_barrier(0x008, 4, 0);
 
     if (need_mask) {  // diagonal / ragged-tail tiles: selects, no per-element branches
+        asm volatile("");  // keeps this rare block a branch (it must not be speculated into every tile)
 #pragma unroll
         for (int kb = 0; kb < 2; ++kb)
 #pragma unroll
@@ -149,17 +163,19 @@ __device__ __forceinline__ void tile_step(Acc& A, const bf16x8 (&qf)[8], const u
                 st[kb][i] = key > lim ? kNegInf : st[kb][i];
             }
     }
-    float tmax = kNegInf;
+    float tm0 = kNegInf, tm1 = kNegInf;  // two independent chains
 #pragma unroll
-    for (int kb = 0; kb < 2; ++kb)
-#pragma unroll
-        for (int i = 0; i < 16; ++i) tmax = fmaxf(tmax, st[kb][i]);
-    tmax = max_halves(tmax);
+    for (int i = 0; i < 16; ++i) {
+        tm0 = fmaxf(tm0, st[0][i]);
+        tm1 = fmaxf(tm1, st[1][i]);
+    }
+    const float tmax = fmaxf(tm0, tm1);  // this lane half's maximum of t
     const float base = (A.m_s == kNegInf) ? 0.0f : A.m_s;  // what the S chain subtracted
-    A.m_t = fmaxf(A.m_t, tmax + base);
+    A.m_t = fmaxf(A.m_t, tmax + base);                      // this half's running maximum
     const bool grow = (A.m_s == kNegInf) ? (tmax > kNegInf) : (tmax > kRescaleLog2);
     if (__builtin_amdgcn_ballot_w64(grow) != 0) {  // wave-uniform, rare after the first tile
-        const float m_new = A.m_t;
+        asm volatile("");  // keeps this rare block a branch (it must not be speculated into every tile)
+        const float m_new = max_halves(A.m_t);     // the query's maximum over both halves
         const float delta = (m_new == kNegInf) ? 0.0f : m_new - base;
         const float alpha = (A.m_s == kNegInf) ? 0.0f : exp2f(A.m_s - m_new);
         A.m_s = m_new;
@@ -178,7 +194,7 @@ __device__ __forceinline__ void tile_step(Acc& A, const bf16x8 (&qf)[8], const u
     }
     // p = exp2(t) in bf16; the row sum is over the bf16 values the PV product uses
     const bf16x2 ones = {(__bf16)1.0f, (__bf16)1.0f};
-    float psum = 0.0f;
+    float psum[2] = {0.0f, 0.0f};
     bf16x8 pb[2][2];
 #pragma unroll
     for (int kb = 0; kb < 2; ++kb)
@@ -189,11 +205,11 @@ __device__ __forceinline__ void tile_step(Acc& A, const bf16x8 (&qf)[8], const u
             for (int e = 0; e < 4; ++e) {
                 w[e] = pack_bf16x2(__builtin_amdgcn_exp2f(st[kb][8 * u + 2 * e]),
                                    __builtin_amdgcn_exp2f(st[kb][8 * u + 2 * e + 1]));
-                psum = __builtin_amdgcn_fdot2_f32_bf16(__builtin_bit_cast(bf16x2, w[e]), ones, psum, false);
+                psum[kb] = __builtin_amdgcn_fdot2_f32_bf16(__builtin_bit_cast(bf16x2, w[e]), ones, psum[kb], false);
             }
             pb[kb][u] = __builtin_bit_cast(bf16x8, make_uint4(w[0], w[1], w[2], w[3]));
         }
-    A.l += sum_halves(psum);
+    A.l += psum[0] + psum[1];  // this half's keys only
 
     // O^T += V^T P^T; chunk (kb, u): k index 8*hh + e <-> key 32*kb + 16*u + 8*(e/4) + 4*hh + (e%4)
 #pragma unroll
@@ -221,7 +237,7 @@ __global__ __launch_bounds__(kThreads, 1) void flash_fwd_bf16_kernel(FlashArgs a
 
     const int tid = threadIdx.x;
     const int lane = tid & 63;
-    const int wave = tid >> 6;
+    const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);  // wave-uniform, held in an SGPR
     const int grp = wave >> 2;  // key-tile group
     const int wq = wave & 3;    // 32-query block within the item (also this wave's share of a DMA tile)
     const int ln = lane & 31;
@@ -366,7 +382,10 @@ __global__ __launch_bounds__(kThreads, 1) void flash_fwd_bf16_kernel(FlashArgs a
             stage_barrier();
         }
 
-        // merge the two groups' partial results through LDS (no DMA is in flight now)
+        // combine the lane halves' maxima and sums, then merge the two groups through LDS
+        // (no DMA is in flight now)
+        A.m_t = max_halves(A.m_t);
+        A.l = sum_halves(A.l);
         float* xo = reinterpret_cast<float*>(&stage0[0][0][0]) + wq * (64 * 64);
         float* xs = reinterpret_cast<float*>(&stage1[0][0][0]) + wq * (3 * 64);
         if (grp == 1) {
