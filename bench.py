@@ -65,14 +65,43 @@ def cpu_baseline(T: int, H: int, D: int, budget_s: float = 10.0) -> dict:
 
 
 def load_traffic(mode: str, T: int):
-    """HBM bytes per launch from the committed rocprofv3 --pmc summary, when one exists for this workload."""
-    p = ROOT / "profiles" / f"flash_fwd_{mode}_t{T}_traffic.json"
+    """HBM bytes per launch from the committed rocprofv3 --pmc summary of this workload, when one
+    exists: the line ``traffic_bytes_per_launch: N`` of profiles/flash_fwd_<mode>_t<T>_pmc.md."""
+    import re
+
+    p = ROOT / "profiles" / f"flash_fwd_{mode}_t{T}_pmc.md"
     if not p.exists():
         return None
-    try:
-        return json.loads(p.read_text()).get("traffic_bytes")
-    except Exception:
-        return None
+    m = re.search(r"^traffic_bytes_per_launch:\s*(\d+)\s*$", p.read_text(), flags=re.M)
+    return int(m.group(1)) if m else None
+
+
+def copy_calibration(mib: int, steps: int, warmup: int) -> int:
+    """Times torch.neg over ``mib`` MiB of bf16 (reads mib MiB, writes mib MiB per launch). Profiled
+    with rocprofv3 --pmc FETCH_SIZE / WRITE_SIZE, it gives the factor between those counters and
+    the bytes a kernel really moves to and from HBM."""
+    import torch
+
+    n = mib * (1 << 20) // 2
+    src = torch.randn(n, device="cuda:0").to(torch.bfloat16)
+    dst = torch.empty_like(src)
+    stream = torch.cuda.current_stream()
+    for _ in range(warmup):
+        torch.neg(src, out=dst)
+    torch.cuda.synchronize()
+    ev0 = torch.cuda.Event(enable_timing=True)
+    ev1 = torch.cuda.Event(enable_timing=True)
+    ev0.record(stream)
+    for _ in range(steps):
+        torch.neg(src, out=dst)
+    ev1.record(stream)
+    torch.cuda.synchronize()
+    ms = ev0.elapsed_time(ev1) / steps
+    nbytes = 2 * mib * (1 << 20)
+    print(json.dumps({"metric": "copy calibration", "bytes_per_launch": nbytes, "read_bytes": nbytes // 2,
+                      "write_bytes": nbytes // 2, "ms_per_launch": round(ms, 5),
+                      "GB_per_s": round(nbytes / (ms * 1e-3) / 1e9, 1)}), flush=True)
+    return 0
 
 
 def main() -> int:
@@ -83,6 +112,8 @@ def main() -> int:
     ap.add_argument("--T", type=int, default=4096)
     ap.add_argument("--mode", choices=["bf16", "fp32"], default="bf16")
     ap.add_argument("--cpu-budget", type=float, default=10.0, help="seconds of CPU-baseline timing (0 = skip)")
+    ap.add_argument("--copy-mib", type=int, default=0,
+                    help="instead of attention, time a plain copy kernel over this many MiB (counter calibration)")
     args = ap.parse_args()
 
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) > 1:
@@ -93,6 +124,9 @@ def main() -> int:
 
     import numpy as np
     import torch
+
+    if args.copy_mib > 0:
+        return copy_calibration(args.copy_mib, args.steps, args.warmup)
 
     import dirktensor_amd as dt
     from dirktensor_amd import _capi, synth
