@@ -54,6 +54,9 @@
 
 #include "dt_internal.h"
 
+#include <type_traits>
+#include <utility>
+
 namespace dt {
 namespace {
 
@@ -127,31 +130,58 @@ struct Acc {
     float m_t, m_s, l;
 };
 
-// One 64-key tile for one wave: S^T, softmax update, O^T += V^T P^T.
-// kaddr[cc]: byte offset of this lane's K fragment for chunk cc within a K tile (block kb = 0);
-// vaddr[s][db]: byte offset of this lane's transposing read for read s and dim block db
-// (16-key chunk 0; chunk (kb, u) adds 8192*kb + 4096*u).
+template <typename F, int... Is>
+__device__ __forceinline__ void static_for_impl(F&& f, std::integer_sequence<int, Is...>) {
+    (f(std::integral_constant<int, Is>{}), ...);
+}
+// calls f(std::integral_constant<int, I>{}) for I = 0 .. N-1 (compile-time unrolled)
+template <int N, typename F>
+__device__ __forceinline__ void static_for(F&& f) {
+    static_for_impl(f, std::make_integer_sequence<int, N>{});
+}
+// keeps each MFMA with the LDS read issued beside it: the scheduler may not move work across
+#define DT_BUNDLE_END __builtin_amdgcn_sched_barrier(0)
+
+// LDS fragment reads of one 64-key tile.
+// K fragment r = 2*cc + kb: rows 32*kb + ln, dims 16*cc + 8*hh .. +8 (kaddr[cc]: block kb = 0).
+__device__ __forceinline__ bf16x8 read_k(const uint8_t* Ks, const uint32_t (&kaddr)[8], int r) {
+    return __builtin_bit_cast(bf16x8, *reinterpret_cast<const uint4*>(Ks + kaddr[r >> 1] + (r & 1) * 8192));
+}
+// V^T chunk c = 8*kb + 4*u + db: keys 32*kb + 16*u .. +16 (two transposing reads), dims 32*db .. +32.
+// vaddr[s][db]: this lane's read s of dim block db in 16-key chunk 0; chunk (kb, u) adds 8192*kb + 4096*u.
+__device__ __forceinline__ bf16x8 read_v(const uint8_t* Vs, const uint32_t (&vaddr)[2][4], int c) {
+    const int rows = (c >> 3) * 8192 + ((c >> 2) & 1) * 4096;
+    const int db = c & 3;
+    const shortx4 lo = lds_read_tr16(Vs + vaddr[0][db] + rows);
+    const shortx4 hi = lds_read_tr16(Vs + vaddr[1][db] + rows + 2048);
+    return __builtin_bit_cast(bf16x8, (shortx8){lo[0], lo[1], lo[2], lo[3], hi[0], hi[1], hi[2], hi[3]});
+}
+
+// One 64-key tile for one wave: S^T, softmax update, O^T += V^T P^T. Both products read their LDS
+// fragments through four-deep rings, three reads ahead of the MFMA that consumes them, so an MFMA never
+// waits for a read issued just before it.
 __device__ __forceinline__ void tile_step(Acc& A, const bf16x8 (&qf)[8], const uint8_t* Ks, const uint8_t* Vs,
                                           const uint32_t (&kaddr)[8], const uint32_t (&vaddr)[2][4], int k0,
                                           bool need_mask, int lim, int hh) {
     floatx16 st[2];
-#pragma unroll
-    for (int cc = 0; cc < 8; ++cc)
-#pragma unroll
-        for (int kb = 0; kb < 2; ++kb) {
-            const bf16x8 kf =
-                __builtin_bit_cast(bf16x8, *reinterpret_cast<const uint4*>(Ks + kaddr[cc] + kb * 8192));
-            st[kb] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(kf, qf[cc], cc == 0 ? A.neg_ms : st[kb], 0, 0, 0);
-        }
-    // keep the K fragment reads four ahead of the MFMAs that consume them
-    __builtin_amdgcn_sched_group_barrier(0x100, 4, 0);
-#define DT_MFMA_READ                                   \
-    __builtin_amdgcn_sched_group_barrier(0x008, 1, 0); \
-    __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);
-    DT_MFMA_READ DT_MFMA_READ DT_MFMA_READ DT_MFMA_READ DT_MFMA_READ DT_MFMA_READ
-    DT_MFMA_READ DT_MFMA_READ DT_MFMA_READ DT_MFMA_READ DT_MFMA_READ DT_MFMA_READ
-#undef DT_MFMA_READ
-    __builtin_amdgcn_sched_group_barrier(0x008, 4, 0);
+    {
+        bf16x8 kr[4];
+        kr[0] = read_k(Ks, kaddr, 0);
+        kr[1] = read_k(Ks, kaddr, 1);
+        kr[2] = read_k(Ks, kaddr, 2);
+        static_for<16>([&](auto R) {
+            constexpr int r = decltype(R)::value;  // = 2*cc + kb
+            if constexpr (r + 3 < 16) kr[(r + 3) & 3] = read_k(Ks, kaddr, r + 3);
+            st[r & 1] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(kr[r & 3], qf[r >> 1], (r >> 1) == 0 ? A.neg_ms : st[r & 1],
+                                                                0, 0, 0);
+            DT_BUNDLE_END;
+        });
+    }
+    // the first V chunks stream in while the softmax runs
+    bf16x8 vr[4];
+    vr[0] = read_v(Vs, vaddr, 0);
+    vr[1] = read_v(Vs, vaddr, 1);
+    vr[2] = read_v(Vs, vaddr, 2);
 
     if (need_mask) {  // diagonal / ragged-tail tiles: selects, no per-element branches
         asm volatile("");  // keeps this rare block a branch (it must not be speculated into every tile)
@@ -212,19 +242,12 @@ __device__ __forceinline__ void tile_step(Acc& A, const bf16x8 (&qf)[8], const u
     A.l += psum[0] + psum[1];  // this half's keys only
 
     // O^T += V^T P^T; chunk (kb, u): k index 8*hh + e <-> key 32*kb + 16*u + 8*(e/4) + 4*hh + (e%4)
-#pragma unroll
-    for (int kb = 0; kb < 2; ++kb)
-#pragma unroll
-        for (int u = 0; u < 2; ++u)
-#pragma unroll
-            for (int db = 0; db < 4; ++db) {
-                const int rows = kb * 8192 + u * 4096;
-                const shortx4 lo = lds_read_tr16(Vs + vaddr[0][db] + rows);
-                const shortx4 hi = lds_read_tr16(Vs + vaddr[1][db] + rows + 2048);
-                const bf16x8 vf =
-                    __builtin_bit_cast(bf16x8, (shortx8){lo[0], lo[1], lo[2], lo[3], hi[0], hi[1], hi[2], hi[3]});
-                A.o[db] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(vf, pb[kb][u], A.o[db], 0, 0, 0);
-            }
+    static_for<16>([&](auto C) {
+        constexpr int c = decltype(C)::value;  // = 8*kb + 4*u + db
+        if constexpr (c + 3 < 16) vr[(c + 3) & 3] = read_v(Vs, vaddr, c + 3);
+        A.o[c & 3] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(vr[c & 3], pb[c >> 3][(c >> 2) & 1], A.o[c & 3], 0, 0, 0);
+        DT_BUNDLE_END;
+    });
 }
 
 // Barrier for the double-buffered loop: this wave's LDS DMA and LDS accesses are
