@@ -107,8 +107,11 @@ def copy_calibration(mib: int, steps: int, warmup: int) -> int:
 def main() -> int:
     ap = argparse.ArgumentParser(description=__doc__, formatter_class=argparse.RawDescriptionHelpFormatter)
     ap.add_argument("--gpus", type=int, default=1)
-    ap.add_argument("--steps", type=int, default=100)
-    ap.add_argument("--warmup", type=int, default=10)
+    ap.add_argument("--steps", type=int, default=200)
+    # The MI355X shader clock ramps from about 1.6 GHz to about 2.0 GHz over the first 30-50 ms of
+    # sustained load (measured in-kernel with s_memtime against s_memrealtime); 500 launches of the
+    # T=4096 workload (about 45 ms) put the timed region at the settled clock a sustained workload runs at.
+    ap.add_argument("--warmup", type=int, default=500)
     ap.add_argument("--T", type=int, default=4096)
     ap.add_argument("--mode", choices=["bf16", "fp32"], default="bf16")
     ap.add_argument("--cpu-budget", type=float, default=10.0, help="seconds of CPU-baseline timing (0 = skip)")

@@ -160,9 +160,11 @@ __device__ __forceinline__ bf16x8 read_v(const uint8_t* Vs, const uint32_t (&vad
 // One 64-key tile for one wave: S^T, softmax update, O^T += V^T P^T. Both products read their LDS
 // fragments through four-deep rings, three reads ahead of the MFMA that consumes them, so an MFMA never
 // waits for a read issued just before it.
+// mid() runs between the softmax and the PV product (the caller issues the next tile's V DMA there).
+template <typename Mid>
 __device__ __forceinline__ void tile_step(Acc& A, const bf16x8 (&qf)[8], const uint8_t* Ks, const uint8_t* Vs,
                                           const uint32_t (&kaddr)[8], const uint32_t (&vaddr)[2][4], int k0,
-                                          bool need_mask, int lim, int hh) {
+                                          bool need_mask, int lim, int hh, Mid&& mid) {
     floatx16 st[2];
     {
         bf16x8 kr[4];
@@ -240,6 +242,7 @@ __device__ __forceinline__ void tile_step(Acc& A, const bf16x8 (&qf)[8], const u
             pb[kb][u] = __builtin_bit_cast(bf16x8, make_uint4(w[0], w[1], w[2], w[3]));
         }
     A.l += psum[0] + psum[1];  // this half's keys only
+    mid();
 
     // O^T += V^T P^T; chunk (kb, u): k index 8*hh + e <-> key 32*kb + 16*u + 8*(e/4) + 4*hh + (e%4)
     static_for<16>([&](auto C) {
@@ -369,39 +372,46 @@ __global__ __launch_bounds__(kThreads, 1) void flash_fwd_bf16_kernel(FlashArgs a
         const int n_tiles = (k_end + kBN - 1) / kBN;
         const int n_iter = (n_tiles + 1) / 2;
 
-        // tile kt of this group -> one LDS stage, straight from HBM
-        auto dma = [&](Stage& stg, int kt) {
+        // K (kv = 0) or V (kv = 1) of tile kt of this group -> one LDS stage, straight from HBM
+        auto dma = [&](Stage& stg, int kv, int kt) {
             const int k0 = kt * kBN;
             const uint32_t bytes = (uint32_t)(L - k0) * (uint32_t)a.ldk * 2u;  // rows k0 .. L-1
-            const __amdgpu_buffer_rsrc_t rk = make_rsrc(Kg + (int64_t)k0 * a.ldk, bytes);
-            const __amdgpu_buffer_rsrc_t rv = make_rsrc(Vg + (int64_t)k0 * a.ldk, bytes);
+            const __amdgpu_buffer_rsrc_t r = make_rsrc((kv ? Vg : Kg) + (int64_t)k0 * a.ldk, bytes);
 #pragma unroll
-            for (int i = 0; i < 4; ++i) {
-                __builtin_amdgcn_raw_ptr_buffer_load_lds(rk, (lds_void*)&stg[grp][0][(4 * i + wq) * 1024], 16,
-                                                         voff[i], 0, 0, 0);
-                __builtin_amdgcn_raw_ptr_buffer_load_lds(rv, (lds_void*)&stg[grp][1][(4 * i + wq) * 1024], 16,
-                                                         voff[i], 0, 0, 0);
-            }
+            for (int i = 0; i < 4; ++i)
+                __builtin_amdgcn_raw_ptr_buffer_load_lds(r, (lds_void*)&stg[grp][kv][(4 * i + wq) * 1024], 16, voff[i],
+                                                         0, 0, 0);
         };
-        auto compute = [&](const Stage& stg, int kt) {
+        // Step on stage `cur` (tile kt) while the group's next tile kn streams into `nxt`: its K at the start
+        // of the step, its V after the softmax, so the V rows do not compete with this step's K reads.
+        auto step = [&](const Stage& cur, Stage& nxt, int kt, int kn) {
+            const bool dn = kn < n_tiles;
+            if (dn) dma(nxt, 0, kn);
+            auto mid = [&]() {
+                if (dn) dma(nxt, 1, kn);
+            };
             const int k0 = kt * kBN;
-            if (kt >= n_tiles || (a.causal && k0 > qw0 + 31)) return;  // nothing of this tile is visible
+            if (kt >= n_tiles || (a.causal && k0 > qw0 + 31)) {  // nothing of this tile is visible
+                mid();
+                return;
+            }
             const bool need_mask = (a.causal && k0 + kBN - 1 > qw0) || k0 + kBN > L;
             const int lim = a.causal ? min(qrow, L - 1) : L - 1;  // keys > lim are masked
-            tile_step(A, qf, stg[grp][0], stg[grp][1], kaddr, vaddr, k0, need_mask, lim, hh);
+            tile_step(A, qf, cur[grp][0], cur[grp][1], kaddr, vaddr, k0, need_mask, lim, hh, mid);
         };
 
-        if (grp < n_tiles) dma(stage0, grp);
+        if (grp < n_tiles) {
+            dma(stage0, 0, grp);
+            dma(stage0, 1, grp);
+        }
         stage_barrier();
         for (int it = 0; it < n_iter; it += 2) {
             // even step: compute from stage0 while the group's next tile streams into stage1
-            if (2 * (it + 1) + grp < n_tiles) dma(stage1, 2 * (it + 1) + grp);
-            compute(stage0, 2 * it + grp);
+            step(stage0, stage1, 2 * it + grp, 2 * (it + 1) + grp);
             stage_barrier();
             if (it + 1 >= n_iter) break;
             // odd step: compute from stage1 while the tile after it streams into stage0
-            if (2 * (it + 2) + grp < n_tiles) dma(stage0, 2 * (it + 2) + grp);
-            compute(stage1, 2 * (it + 1) + grp);
+            step(stage1, stage0, 2 * (it + 1) + grp, 2 * (it + 2) + grp);
             stage_barrier();
         }
 
