@@ -16,8 +16,10 @@
 //     reference applies between tiles (FlashAttention.cpp:134-156).
 //   * K and V tiles move from HBM straight into LDS with buffer_load ... lds
 //     (no staging registers), double-buffered in two LDS arrays: while a step
-//     computes on one array, the next tile streams into the other; one barrier
-//     per step. The descriptors end at the sequence's last valid key, so rows
+//     computes on one array, the next tile streams into the other (its K rows
+//     at the start of the step, its V rows after the softmax, so they do not
+//     land while this step's K fragments are read); one barrier per step.
+//     The descriptors end at the sequence's last valid key, so rows
 //     past it arrive as zeros. LDS rows are 256 bytes, unpadded; the 16-byte
 //     chunk c of row r is stored at chunk position c ^ f(r),
 //     f(r) = 4*(r & 3) + ((r >> 2) & 3), which keeps both the row-wise K reads
@@ -32,6 +34,9 @@
 //     group reads a 4-key x 16-dim block and each lane receives one dim column
 //     of 4 keys, i.e. the MFMA's 8-key k slice taken as two 4-key runs in the
 //     accumulator's key order.
+//   * Both products read their LDS fragments through four-deep register rings,
+//     three reads ahead of the MFMA that consumes them, so no MFMA waits for a
+//     read issued just before it.
 //
 // Softmax bookkeeping, per query, in the log2 domain of the scaled score
 // s' = (scale * log2 e) * q.k (Q is pre-multiplied by scale * log2 e when its
