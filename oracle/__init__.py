@@ -46,6 +46,10 @@ def lib() -> ctypes.CDLL:
         l.oracle_flash_attention_forward.argtypes = [_vp, _vp, _vp, _vp, _vp, _vp, _i, _i, _i, _i, _f, _i, _i]
         l.oracle_sgemm_nt.argtypes = [_i, _i, _i, _f, _vp, _i, _vp, _i, _vp, _i, _i]
         l.oracle_attention_layer_forward.argtypes = [_vp] * 9 + [_vp, _i, _i, _i, _i, _f, _i] + [_vp] * 6
+        l.oracle_flash_attention_backward.argtypes = [_vp] * 10 + [_i, _i, _i, _i, _f, _i, _i]
+        l.oracle_apply_rope_backward.argtypes = [_vp, _vp, _i, _i, _i, _i, _vp, _vp]
+        l.oracle_rmsnorm_backward.argtypes = [_vp] * 6 + [_i, _i]
+        l.oracle_attention_layer_backward.argtypes = [_vp] * 17 + [_i, _i, _i, _i, _f, _i]
         _lib = l
     return _lib
 
@@ -161,3 +165,54 @@ def attention_layer_forward(x, wq, wk, wv, wo, q_norm, k_norm, *, theta: float =
                                          B, T, H, D, float(eps), nthreads or default_threads(),
                                          g("q_rope"), g("k_rope"), g("v"), g("attn"), g("m"), g("l"))
     return (out, st) if return_state else out
+
+
+def flash_attention_backward(dO, O, m, l, Q, K, V, scale: float, causal: bool = True, nthreads: int | None = None):
+    """flash_attention_backward (FlashAttention.cpp:185-359); returns (dQ, dK, dV)."""
+    dO, O, m, l, Q, K, V = (_c32(a) for a in (dO, O, m, l, Q, K, V))
+    B, T, H, D = Q.shape
+    dQ, dK, dV = np.empty_like(Q), np.empty_like(Q), np.empty_like(Q)
+    lib().oracle_flash_attention_backward(_p(dO), _p(O), _p(m), _p(l), _p(Q), _p(K), _p(V), _p(dQ), _p(dK), _p(dV),
+                                          B, T, H, D, float(scale), int(bool(causal)), nthreads or default_threads())
+    return dQ, dK, dV
+
+
+def apply_rope_backward(d_out, sin_t, cos_t):
+    """OlmoAttention::apply_rope_backward (OlmoAttention.cpp:149-190); d_out [B,T,H,D]."""
+    d_out = _c32(d_out)
+    B, T, H, D = d_out.shape
+    d_in = np.empty_like(d_out)
+    lib().oracle_apply_rope_backward(_p(d_out), _p(d_in), B, T, H, D, _p(_c32(sin_t)), _p(_c32(cos_t)))
+    return d_in
+
+
+def rmsnorm_backward(dy, y, rms, w):
+    """RMSNorm::backward (RMSNorm.cpp:24-36) from the forward's output y and rms; returns (dx, dw)."""
+    dy, y, rms, w = _c32(dy), _c32(y), _c32(rms), _c32(w)
+    C = y.shape[-1]
+    rows = y.size // C
+    dx = np.empty_like(y)
+    dw = np.zeros(C, dtype=np.float32)
+    lib().oracle_rmsnorm_backward(_p(dy), _p(y), _p(rms), _p(w), _p(dx), _p(dw), rows, C)
+    return dx, dw
+
+
+def attention_layer_backward(x, wq, wk, wv, wo, q_norm, k_norm, d_out, *, theta: float = 500000.0,
+                             eps: float = 1e-6, nthreads: int | None = None):
+    """OlmoAttention::backward (OlmoAttention.cpp:193-312) after a forward on x [B,T,d_model].
+    Returns d_x and the gradients {wq, wk, wv, wo, q_norm, k_norm} accumulated from zero."""
+    x, d_out = _c32(x), _c32(d_out)
+    B, T, dm = x.shape
+    D = 128
+    H = dm // D
+    sin_t, cos_t = rope_tables(max(T, 1), D, theta)
+    d_x = np.empty_like(x)
+    g = {k: np.zeros((dm, dm), np.float32) for k in ("wq", "wk", "wv", "wo")}
+    g["q_norm"] = np.zeros(dm, np.float32)
+    g["k_norm"] = np.zeros(dm, np.float32)
+    lib().oracle_attention_layer_backward(_p(x), _p(_c32(wq)), _p(_c32(wk)), _p(_c32(wv)), _p(_c32(wo)),
+                                          _p(_c32(q_norm)), _p(_c32(k_norm)), _p(sin_t), _p(cos_t), _p(d_out),
+                                          _p(d_x), _p(g["wq"]), _p(g["wk"]), _p(g["wv"]), _p(g["wo"]),
+                                          _p(g["q_norm"]), _p(g["k_norm"]), B, T, H, D, float(eps),
+                                          nthreads or default_threads())
+    return d_x, g

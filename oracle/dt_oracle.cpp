@@ -15,6 +15,12 @@
 //                                  2048 features, RoPE, flash, o_proj)
 //   oracle_sgemm_nt / _nn         stand-ins for the cblas_sgemm calls at FlashAttention.cpp:83,123
 //                                  and xt::linalg::dot at OlmoAttention.cpp:68,74,80,104
+//   oracle_flash_attention_backward FlashAttention.cpp:185-359 (D = O.dO, P from the saved m and l,
+//                                  dS = P (dP - D) scale, 256x256 blocks)
+//   oracle_apply_rope_backward    OlmoAttention.cpp:149-190  (transpose of the rotation)
+//   oracle_rmsnorm_backward       RMSNorm.cpp:24-36          (c = mean(dy*y), n = y/w recomputed)
+//   oracle_attention_layer_backward OlmoAttention.cpp:193-312 (o_proj, flash, RoPE, norms and
+//                                  q/k/v projection backward; weight gradients accumulated)
 //
 // Parity pins (checked in tests/test_oracle_pins.py): an fp64 full-softmax attention
 // written independently in numpy, torch's scaled_dot_product_attention in fp64,
@@ -110,6 +116,21 @@ void gemm_nt_serial(int M, int N, int K, float alpha, const float* A, int lda, c
     }
 }
 
+// C[i][n] = beta * C[i][n] + sum_k A[k][i] * B[k][n]    (row-major, "Trans, NoTrans")
+void gemm_tn_serial(int M, int N, int K, const float* A, int lda, const float* B, int ldb, float beta, float* C,
+                    int ldc) {
+    for (int i = 0; i < M; ++i) {
+        float* c = C + (int64_t)i * ldc;
+        if (beta == 0.0f) std::fill(c, c + N, 0.0f);
+        for (int k = 0; k < K; ++k) {
+            const float av = A[(int64_t)k * lda + i];
+            if (av == 0.0f) continue;
+            const float* b = B + (int64_t)k * ldb;
+            for (int n = 0; n < N; ++n) c[n] += av * b[n];
+        }
+    }
+}
+
 // C[i][n] = sum_k A[i][k] * B[k][n]    (row-major, "NoTrans, NoTrans"), beta = 0
 void gemm_nn_serial(int M, int N, int K, const float* A, int lda, const float* B, int ldb, float* C, int ldc) {
     for (int i = 0; i < M; ++i) {
@@ -139,6 +160,10 @@ int oracle_version(void) { return 1; }
 //   5 norm:  normalise per head (128) instead of over all features (OlmoAttention.cpp:70)
 //   6 norm:  drop eps                              (RMSNorm.cpp:18)
 //   7 flash: drop the softmax scale                (FlashAttention.cpp:86)
+//   8 flash backward: drop D = O . dO               (FlashAttention.cpp:232-238, 288-295)
+//   9 rope backward: rotate forwards, not back      (OlmoAttention.cpp:174-182)
+//  10 norm backward: drop the c = mean(dy * y) term (RMSNorm.cpp:26, 35)
+//  11 flash backward: P without the 1 / l           (FlashAttention.cpp:272)
 void oracle_set_mutation(int m) { g_mutation = m; }
 int oracle_get_mutation(void) { return g_mutation; }
 
@@ -331,6 +356,198 @@ void oracle_attention_layer_forward(const float* x, const float* wq, const float
     if (attn_out) std::memcpy(attn_out, o.data(), n * sizeof(float));
     if (m_out) std::memcpy(m_out, mm.data(), mm.size() * sizeof(float));
     if (l_out) std::memcpy(l_out, ll.data(), ll.size() * sizeof(float));
+}
+
+
+// flash_attention_backward, FlashAttention.cpp:185-359. dO, O, Q, K, V, dQ, dK, dV are [B,T,H,D];
+// m, l are the forward's [B,T,H] statistics. Per (batch, head) and 256-query block:
+// D_i = O_i . dO_i (:232-238); per 256-key block (skipped when causal and q_start < k_start, :247):
+// S = scale Q K^T (:249-258), P = exp(S - m) / l with masked entries 0 (:260-275),
+// dP = dO V^T (:277-286), dS = P (dP - D) scale (:288-295), dV += P^T dO (:297-313),
+// dQ += dS K (:316-325), dK += dS^T Q (:327-343).
+void oracle_flash_attention_backward(const float* dO, const float* O, const float* m, const float* l,
+                                     const float* Q, const float* K, const float* V, float* dQ, float* dK,
+                                     float* dV, int B, int T, int H, int D, float scale, int causal,
+                                     int nthreads) {
+    constexpr int BQ = 256, BKV = 256;  // FlashAttention.cpp:21-22
+    const int ld = H * D;
+    auto at = [&](const float* base, int b, int t, int h) { return base + ((int64_t)b * T + t) * ld + (int64_t)h * D; };
+    auto atw = [&](float* base, int b, int t, int h) { return base + ((int64_t)b * T + t) * ld + (int64_t)h * D; };
+    for (int b = 0; b < B; ++b)
+        for (int t = 0; t < T; ++t)
+            for (int h = 0; h < H; ++h) {
+                std::fill(atw(dQ, b, t, h), atw(dQ, b, t, h) + D, 0.0f);
+                std::fill(atw(dK, b, t, h), atw(dK, b, t, h) + D, 0.0f);
+                std::fill(atw(dV, b, t, h), atw(dV, b, t, h) + D, 0.0f);
+            }
+    parallel_for((int64_t)B * H, nthreads, [&](int64_t bh) {
+        const int b = (int)(bh / H), h = (int)(bh % H);
+        std::vector<float> S((size_t)BQ * BKV), P((size_t)BQ * BKV), dP((size_t)BQ * BKV), dS((size_t)BQ * BKV);
+        std::vector<float> Di(BQ), dQb((size_t)BQ * D), dKb((size_t)BKV * D), dVb((size_t)BKV * D);
+        for (int q0 = 0; q0 < T; q0 += BQ) {
+            const int Br = std::min(BQ, T - q0);
+            for (int i = 0; i < Br; ++i) {
+                const float* o = at(O, b, q0 + i, h);
+                const float* g = at(dO, b, q0 + i, h);
+                float acc = 0.0f;
+                for (int d = 0; d < D; ++d) acc += o[d] * g[d];
+                Di[i] = (g_mutation == 8) ? 0.0f : acc;
+            }
+            std::fill(dQb.begin(), dQb.begin() + (size_t)Br * D, 0.0f);
+            for (int k0 = 0; k0 < T; k0 += BKV) {
+                const int Bc = std::min(BKV, T - k0);
+                if (causal && q0 < k0) continue;
+                gemm_nt_serial(Br, Bc, D, scale, at(Q, b, q0, h), ld, at(K, b, k0, h), ld, S.data(), BKV);
+                for (int i = 0; i < Br; ++i) {
+                    const int64_t si = ((int64_t)b * T + q0 + i) * H + h;
+                    const float mi = m[si];
+                    const float li = (g_mutation == 11) ? 1.0f : l[si];
+                    for (int j = 0; j < Bc; ++j) {
+                        const bool masked = causal && (q0 + i < k0 + j);
+                        P[(size_t)i * BKV + j] = masked ? 0.0f : std::exp(S[(size_t)i * BKV + j] - mi) / li;
+                    }
+                }
+                gemm_nt_serial(Br, Bc, D, 1.0f, at(dO, b, q0, h), ld, at(V, b, k0, h), ld, dP.data(), BKV);
+                for (int i = 0; i < Br; ++i)
+                    for (int j = 0; j < Bc; ++j)
+                        dS[(size_t)i * BKV + j] = P[(size_t)i * BKV + j] * (dP[(size_t)i * BKV + j] - Di[i]) * scale;
+                // dV_blk = P^T dO, accumulated into dV
+                gemm_tn_serial(Bc, D, Br, P.data(), BKV, at(dO, b, q0, h), ld, 0.0f, dVb.data(), D);
+                for (int j = 0; j < Bc; ++j) {
+                    float* dst = atw(dV, b, k0 + j, h);
+                    for (int d = 0; d < D; ++d) dst[d] += dVb[(size_t)j * D + d];
+                }
+                // dQ_blk += dS K
+                for (int i = 0; i < Br; ++i) {
+                    float* dq = dQb.data() + (size_t)i * D;
+                    for (int j = 0; j < Bc; ++j) {
+                        const float w = dS[(size_t)i * BKV + j];
+                        if (w == 0.0f) continue;
+                        const float* kr = at(K, b, k0 + j, h);
+                        for (int d = 0; d < D; ++d) dq[d] += w * kr[d];
+                    }
+                }
+                // dK_blk = dS^T Q, accumulated into dK
+                gemm_tn_serial(Bc, D, Br, dS.data(), BKV, at(Q, b, q0, h), ld, 0.0f, dKb.data(), D);
+                for (int j = 0; j < Bc; ++j) {
+                    float* dst = atw(dK, b, k0 + j, h);
+                    for (int d = 0; d < D; ++d) dst[d] += dKb[(size_t)j * D + d];
+                }
+            }
+            for (int i = 0; i < Br; ++i) std::memcpy(atw(dQ, b, q0 + i, h), dQb.data() + (size_t)i * D, D * sizeof(float));
+        }
+    });
+}
+
+// apply_rope_backward, OlmoAttention.cpp:149-190: the transpose of the rotation,
+// d_in[d] = d_out[d] cos[d] + d_out[d+64] sin[d+64], d_in[d+64] = -d_out[d] sin[d] + d_out[d+64] cos[d+64].
+void oracle_apply_rope_backward(const float* d_out, float* d_in, int B, int T, int H, int D, const float* sin_t,
+                                const float* cos_t) {
+    const int half = D / 2;
+    const float sgn = (g_mutation == 9) ? -1.0f : 1.0f;
+    for (int b = 0; b < B; ++b)
+        for (int t = 0; t < T; ++t)
+            for (int h = 0; h < H; ++h) {
+                const float* g = d_out + (((int64_t)b * T + t) * H + h) * D;
+                float* y = d_in + (((int64_t)b * T + t) * H + h) * D;
+                const float* c = cos_t + (int64_t)t * D;
+                const float* s = sin_t + (int64_t)t * D;
+                for (int d = 0; d < half; ++d) {
+                    y[d] = g[d] * c[d] + sgn * g[d + half] * s[d + half];
+                    y[d + half] = -sgn * g[d] * s[d] + g[d + half] * c[d + half];
+                }
+            }
+}
+
+// RMSNorm::backward, RMSNorm.cpp:24-36, from the forward's saved output y and rms:
+// c = mean(dy * y) over the row; n = y / w (recomputed, :29); dw += sum over rows of dy * n;
+// dx = (w * dy - n * c) / rms. x-shaped arrays are [rows][C]; dw is accumulated (+=).
+void oracle_rmsnorm_backward(const float* dy, const float* y, const float* rms, const float* w, float* dx,
+                             float* dw, int rows, int C) {
+    for (int r = 0; r < rows; ++r) {
+        const float* g = dy + (int64_t)r * C;
+        const float* yr = y + (int64_t)r * C;
+        float acc = 0.0f;
+        for (int c = 0; c < C; ++c) acc += g[c] * yr[c];
+        const float cm = (g_mutation == 10) ? 0.0f : acc / (float)C;
+        float* out = dx + (int64_t)r * C;
+        for (int c = 0; c < C; ++c) {
+            const float n = yr[c] / w[c];
+            dw[c] += g[c] * n;
+            out[c] = (w[c] * g[c] - n * cm) / rms[r];
+        }
+    }
+}
+
+// C = A B (row-major, "NoTrans, NoTrans"), threaded over row blocks of C.
+void oracle_sgemm_nn(int M, int N, int K, const float* A, int lda, const float* B, int ldb, float* C, int ldc,
+                     int nthreads) {
+    const int rb = 16;
+    parallel_for((M + rb - 1) / rb, nthreads, [&](int64_t blk) {
+        const int i0 = (int)blk * rb, rows = std::min(rb, M - i0);
+        gemm_nn_serial(rows, N, K, A + (int64_t)i0 * lda, lda, B, ldb, C + (int64_t)i0 * ldc, ldc);
+    });
+}
+
+// C += A^T B (row-major, "Trans, NoTrans", beta = 1), threaded over row blocks of C.
+void oracle_sgemm_tn_acc(int M, int N, int K, const float* A, int lda, const float* B, int ldb, float* C, int ldc,
+                         int nthreads) {
+    const int rb = 16;
+    parallel_for((M + rb - 1) / rb, nthreads, [&](int64_t blk) {
+        const int i0 = (int)blk * rb, rows = std::min(rb, M - i0);
+        gemm_tn_serial(rows, N, K, A + i0, lda, B, ldb, 1.0f, C + (int64_t)i0 * ldc, ldc);
+    });
+}
+
+// OlmoAttention::backward, OlmoAttention.cpp:193-312, for d_model = H*D with D = 128. The
+// forward's saved state (OlmoAttention.h:28-38) is recomputed from x and the weights. d_out and
+// d_x are [B,T,d_model]; the weight gradients are accumulated (+=, the reference's beta = 1 at
+// :207-211, :257-277, and RMSNorm.cpp:31): dwq/dwk/dwv/dwo [d_model][d_model], dq_norm/dk_norm [d_model].
+void oracle_attention_layer_backward(const float* x, const float* wq, const float* wk, const float* wv,
+                                     const float* wo, const float* q_norm_w, const float* k_norm_w,
+                                     const float* sin_t, const float* cos_t, const float* d_out, float* d_x,
+                                     float* dwq, float* dwk, float* dwv, float* dwo, float* dq_norm,
+                                     float* dk_norm, int B, int T, int H, int D, float eps, int nthreads) {
+    const int dm = H * D;
+    const int rows = B * T;
+    const size_t n = (size_t)rows * dm;
+    // forward, keeping what the reference saves (OlmoAttention.cpp:64-100)
+    std::vector<float> q(n), k(n), v(n), qn(n), kn(n), qr(n), kr(n), o(n), q_rms(rows), k_rms(rows);
+    std::vector<float> mm((size_t)rows * H), ll((size_t)rows * H);
+    oracle_sgemm_nt(rows, dm, dm, 1.0f, x, dm, wq, dm, q.data(), dm, nthreads);
+    oracle_rmsnorm_forward(q.data(), q_norm_w, qn.data(), q_rms.data(), rows, dm, eps);
+    oracle_sgemm_nt(rows, dm, dm, 1.0f, x, dm, wk, dm, k.data(), dm, nthreads);
+    oracle_rmsnorm_forward(k.data(), k_norm_w, kn.data(), k_rms.data(), rows, dm, eps);
+    oracle_sgemm_nt(rows, dm, dm, 1.0f, x, dm, wv, dm, v.data(), dm, nthreads);
+    oracle_apply_rope(qn.data(), qr.data(), B, T, H, D, sin_t, cos_t);
+    oracle_apply_rope(kn.data(), kr.data(), B, T, H, D, sin_t, cos_t);
+    const float scale = 1.0f / std::sqrt((float)D);
+    oracle_flash_attention_forward(qr.data(), kr.data(), v.data(), o.data(), mm.data(), ll.data(), B, T, H, D,
+                                   scale, 1, nthreads);
+    // step 1, :198-217: dWo += d_out^T attn; d_attn = d_out Wo
+    oracle_sgemm_tn_acc(dm, dm, rows, d_out, dm, o.data(), dm, dwo, dm, nthreads);
+    std::vector<float> d_attn(n), dqr(n), dkr(n), dv(n), dqn(n), dkn(n), dq(n), dk(n);
+    oracle_sgemm_nn(rows, dm, dm, d_out, dm, wo, dm, d_attn.data(), dm, nthreads);
+    // step 2, :219-232: flash backward from the saved statistics
+    oracle_flash_attention_backward(d_attn.data(), o.data(), mm.data(), ll.data(), qr.data(), kr.data(), v.data(),
+                                    dqr.data(), dkr.data(), dv.data(), B, T, H, D, scale, 1, nthreads);
+    // step 3, :234-236: RoPE backward
+    oracle_apply_rope_backward(dqr.data(), dqn.data(), B, T, H, D, sin_t, cos_t);
+    oracle_apply_rope_backward(dkr.data(), dkn.data(), B, T, H, D, sin_t, cos_t);
+    // step 4, :238-244: q/k RMSNorm backward
+    oracle_rmsnorm_backward(dqn.data(), qn.data(), q_rms.data(), q_norm_w, dq.data(), dq_norm, rows, dm);
+    oracle_rmsnorm_backward(dkn.data(), kn.data(), k_rms.data(), k_norm_w, dk.data(), dk_norm, rows, dm);
+    // step 5, :246-277: dW += d_proj^T x
+    oracle_sgemm_tn_acc(dm, dm, rows, dq.data(), dm, x, dm, dwq, dm, nthreads);
+    oracle_sgemm_tn_acc(dm, dm, rows, dk.data(), dm, x, dm, dwk, dm, nthreads);
+    oracle_sgemm_tn_acc(dm, dm, rows, dv.data(), dm, x, dm, dwv, dm, nthreads);
+    // :279-309: d_x = dq Wq + dk Wk + dv Wv
+    std::vector<float> t1(n);
+    oracle_sgemm_nn(rows, dm, dm, dq.data(), dm, wq, dm, d_x, dm, nthreads);
+    oracle_sgemm_nn(rows, dm, dm, dk.data(), dm, wk, dm, t1.data(), dm, nthreads);
+    for (size_t i = 0; i < n; ++i) d_x[i] += t1[i];
+    oracle_sgemm_nn(rows, dm, dm, dv.data(), dm, wv, dm, t1.data(), dm, nthreads);
+    for (size_t i = 0; i < n; ++i) d_x[i] += t1[i];
 }
 
 }  // extern "C"

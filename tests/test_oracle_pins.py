@@ -17,6 +17,12 @@ pinned against things that fix the answer independently of its code:
 * torch.nn.functional.rms_norm in fp64, and RoPE invariants (identity at
   t = 0, pair norms preserved, scores depend only on t1 - t2).
 
+* backward: torch autograd in fp64 through scaled_dot_product_attention,
+  F.rms_norm, HF's apply_rotary_pos_emb and the whole Olmo2Attention layer
+  (d_x and all six weight gradients); central finite differences of a numpy
+  fp64 attention; the adjoint identity <rope(x), g> = <x, rope_bwd(g)>; and
+  the row-stochastic invariants sum_k dK = 0, sum_k dV = sum_q dO.
+
 test_planted_mistakes_are_caught then plants each of the oracle's known
 mistakes (oracle_set_mutation) and checks that at least one pin fails.
 """
@@ -221,6 +227,129 @@ def pin_layer_hf(T=48):
     return rel(out, ref.numpy()) <= 1e-4
 
 
+# ----------------------------------------------------------------- backward pins
+def _fwd_bwd(Q, K, V, G, causal=True):
+    O, m, l = oracle.flash_attention_forward(Q, K, V, SCALE, causal)
+    return O, oracle.flash_attention_backward(G, O, m, l, Q, K, V, SCALE, causal)
+
+
+def _autograd_attention(Q, K, V, G, causal=True):
+    q, k, v = (torch.from_numpy(np.asarray(x, np.float64)).transpose(1, 2).requires_grad_() for x in (Q, K, V))
+    o = F.scaled_dot_product_attention(q, k, v, is_causal=causal, scale=SCALE).transpose(1, 2)
+    (o * torch.from_numpy(np.asarray(G, np.float64))).sum().backward()
+    return [t.grad.transpose(1, 2).numpy() for t in (q, k, v)]
+
+
+def pin_flash_bwd_autograd(causal=True):
+    Q, K, V = synth.qkv(1, 300, 2, seeds=(141, 142, 143))  # 300 > 256: crosses the reference's block edge
+    G = synth.normal(144, Q.shape)
+    _, grads = _fwd_bwd(Q, K, V, G, causal)
+    ref = _autograd_attention(Q, K, V, G, causal)
+    return all(rel(a, b) <= 1e-4 for a, b in zip(grads, ref))
+
+
+def pin_flash_bwd_finite_difference():
+    """Central differences of L = sum(O * G) in fp64 (numpy textbook attention), no autograd."""
+    Q, K, V = synth.qkv(1, 6, 1, seeds=(151, 152, 153))
+    G = synth.normal(154, Q.shape)
+    _, (dQ, dK, dV) = _fwd_bwd(Q, K, V, G)
+    X = [np.asarray(a, np.float64) for a in (Q, K, V)]
+
+    def loss(xs):
+        o, _, _ = textbook_attention_f64(*xs, SCALE)
+        return float(np.sum(o * G))
+
+    ok = True
+    rng = np.random.default_rng(155)
+    for which, grad in enumerate((dQ, dK, dV)):
+        for _ in range(6):
+            idx = (0, int(rng.integers(6)), 0, int(rng.integers(128)))
+            h = 1e-5
+            xp = [a.copy() for a in X]
+            xm = [a.copy() for a in X]
+            xp[which][idx] += h
+            xm[which][idx] -= h
+            fd = (loss(xp) - loss(xm)) / (2 * h)
+            ok &= abs(fd - float(grad[idx])) <= 1e-4 * max(1.0, abs(fd))
+    return bool(ok)
+
+
+def pin_flash_bwd_invariants():
+    """Rows of P sum to 1, so the keys' dK sum to 0 and the keys' dV sum to the queries' dO sum."""
+    Q, K, V = synth.qkv(1, 280, 2, seeds=(161, 162, 163))
+    G = synth.normal(164, Q.shape)
+    _, (dQ, dK, dV) = _fwd_bwd(Q, K, V, G)
+    sk = np.abs(dK.astype(np.float64).sum(axis=1)).max() / np.abs(dK).max()
+    sv = rel(dV.astype(np.float64).sum(axis=1), G.astype(np.float64).sum(axis=1))
+    return sk <= 1e-4 and sv <= 1e-5
+
+
+def pin_rope_bwd_adjoint():
+    """apply_rope_backward is the transpose of apply_rope: <rope(x), g> = <x, rope_bwd(g)>, per (t, h)."""
+    s, c = oracle.rope_tables(300)
+    x = synth.normal(171, (2, 300, 3, 128))
+    g = synth.normal(172, (2, 300, 3, 128))
+    lhs = np.sum(oracle.apply_rope(x, s, c).astype(np.float64) * g, axis=-1)
+    rhs = np.sum(x.astype(np.float64) * oracle.apply_rope_backward(g, s, c), axis=-1)
+    back = oracle.apply_rope_backward(oracle.apply_rope(x, s, c), s, c)  # a rotation: the inverse too
+    return rel(lhs, rhs) <= 1e-5 and rel(back, x) <= 1e-5
+
+
+def pin_rope_bwd_autograd():
+    from transformers.models.olmo2.modeling_olmo2 import apply_rotary_pos_emb
+
+    s, c = oracle.rope_tables(64)
+    x = torch.from_numpy(synth.normal(173, (1, 64, 2, 128))).double().requires_grad_()
+    g = synth.normal(174, (1, 64, 2, 128))
+    y, _ = apply_rotary_pos_emb(x, x.detach(), torch.from_numpy(c).double()[None], torch.from_numpy(s).double()[None],
+                                unsqueeze_dim=2)
+    (y * torch.from_numpy(g).double()).sum().backward()
+    return rel(oracle.apply_rope_backward(g, s, c), x.grad.numpy()) <= 1e-6
+
+
+def pin_rmsnorm_bwd_autograd():
+    w = synth.normal(181, (2048,), 1.0, 0.01)
+    ok = True
+    for std in (1.0, 1e-3):
+        x = synth.normal(182, (5, 2048), 0.0, std)
+        g = synth.normal(183, (5, 2048))
+        y, rms = oracle.rmsnorm_forward(x, w)
+        dx, dw = oracle.rmsnorm_backward(g, y, rms, w)
+        xt = torch.from_numpy(x).double().requires_grad_()
+        wt = torch.from_numpy(w).double().requires_grad_()
+        (F.rms_norm(xt, (2048,), wt, eps=1e-6) * torch.from_numpy(g).double()).sum().backward()
+        ok &= rel(dx, xt.grad.numpy()) <= 1e-5 and rel(dw, wt.grad.numpy()) <= 1e-5
+    return bool(ok)
+
+
+def pin_layer_bwd_hf(T=40):
+    """d_x and all six weight gradients against torch autograd through HF's Olmo2Attention in fp64."""
+    from transformers.models.olmo2.modeling_olmo2 import Olmo2Attention
+
+    w = synth.attention_layer_weights()
+    x = synth.normal(2401, (1, T, 2048))
+    g = synth.normal(2402, (1, T, 2048))
+    d_x, grads = oracle.attention_layer_backward(x, w["wq"], w["wk"], w["wv"], w["wo"], w["q_norm"], w["k_norm"], g)
+    cfg = hf_config()
+    cfg._attn_implementation = "eager"
+    attn = Olmo2Attention(cfg, 0).double()
+    names = {"wq": attn.q_proj, "wk": attn.k_proj, "wv": attn.v_proj, "wo": attn.o_proj,
+             "q_norm": attn.q_norm, "k_norm": attn.k_norm}
+    with torch.no_grad():
+        for k, mod in names.items():
+            mod.weight.copy_(torch.from_numpy(w[k]))
+    s, c = oracle.rope_tables(T)
+    pe = (torch.from_numpy(c).double()[None], torch.from_numpy(s).double()[None])
+    mask = torch.triu(torch.full((T, T), float("-inf"), dtype=torch.float64), 1)[None, None]
+    xt = torch.from_numpy(x).double().requires_grad_()
+    out, _ = attn(xt, pe, mask)
+    (out * torch.from_numpy(g).double()).sum().backward()
+    ok = rel(d_x, xt.grad.numpy()) <= 1e-4
+    for k, mod in names.items():
+        ok &= rel(grads[k], mod.weight.grad.numpy()) <= 1e-4
+    return bool(ok)
+
+
 PINS = {
     "flash_textbook_causal": lambda: pin_flash_textbook(True),
     "flash_textbook_full": lambda: pin_flash_textbook(False),
@@ -234,6 +363,14 @@ PINS = {
     "rmsnorm_torch": pin_rmsnorm_torch,
     "rmsnorm_hf": pin_rmsnorm_hf,
     "layer_hf": pin_layer_hf,
+    "flash_bwd_autograd_causal": lambda: pin_flash_bwd_autograd(True),
+    "flash_bwd_autograd_full": lambda: pin_flash_bwd_autograd(False),
+    "flash_bwd_finite_difference": pin_flash_bwd_finite_difference,
+    "flash_bwd_invariants": pin_flash_bwd_invariants,
+    "rope_bwd_adjoint": pin_rope_bwd_adjoint,
+    "rope_bwd_autograd": pin_rope_bwd_autograd,
+    "rmsnorm_bwd_autograd": pin_rmsnorm_bwd_autograd,
+    "layer_bwd_hf": pin_layer_bwd_hf,
 }
 
 
@@ -251,6 +388,10 @@ MUTATIONS = {
     5: ["rmsnorm_torch", "layer_hf"],                     # per-head norm
     6: ["rmsnorm_torch"],                                 # eps dropped
     7: ["flash_textbook_causal", "flash_sdpa"],           # scale dropped
+    8: ["flash_bwd_autograd_causal", "flash_bwd_finite_difference", "flash_bwd_invariants"],  # D dropped
+    9: ["rope_bwd_adjoint", "rope_bwd_autograd", "layer_bwd_hf"],                            # forward rotation
+    10: ["rmsnorm_bwd_autograd", "layer_bwd_hf"],                                            # c term dropped
+    11: ["flash_bwd_autograd_causal", "flash_bwd_finite_difference"],                        # 1 / l dropped
 }
 
 
