@@ -3,8 +3,8 @@
     flash_attention_forward(Q, K, V, scale, causal=True) -> FlashAttentionResult
         FlashAttention.h:15-21 (returns output, softmax_m, softmax_l,
         FlashAttention.h:6-10)
-    flash_attention_backward(...)
-        FlashAttention.h:33-43 -- raises: the GPU path is forward-only
+    flash_attention_backward(dO, O, m, l, Q, K, V, scale, causal=True) -> FlashAttentionGradients
+        FlashAttention.h:33-43 (returns d_Q, d_K, d_V, FlashAttention.h:27-31)
     OlmoAttention(folder, index) / OlmoAttention.from_weights(...)
         OlmoAttention.h:10-42; forward(x) -> out
     qk_norm_rope(q_proj, k_proj, q_norm_w, k_norm_w)
@@ -158,11 +158,54 @@ def flash_attention_forward(Q, K, V, scale: float, causal: bool = True, *, seq_l
     return FlashAttentionResult(O, m, l)
 
 
-def flash_attention_backward(d_output, output, softmax_m, softmax_l, Q, K, V, scale: float, causal: bool = True):
-    """FlashAttention.h:33-43. The GPU path is forward-only: this raises DTError (NOT_IMPLEMENTED)."""
-    ctx = default_context(0)
-    C.call("dt_flash_attn_bwd", ctx.handle, None, None, None, None, None, None, None, None, None, None,
-           0, 0, 0, 0, float(scale), int(bool(causal)), C.DT_FP32_EXACT, C.DT_MEM_DEVICE, None)
+@dataclass
+class FlashAttentionGradients:
+    """FlashAttention.h:27-31: d_Q, d_K, d_V [B,T,H,D]."""
+
+    d_Q: object
+    d_K: object
+    d_V: object
+
+
+def flash_attention_backward(d_output, output, softmax_m, softmax_l, Q, K, V, scale: float, causal: bool = True, *,
+                             mode: Optional[str] = None, ctx: Optional[Context] = None) -> FlashAttentionGradients:
+    """Flash attention backward (FlashAttention.cpp:185-359) on the GPU.
+
+    d_output, output, Q, K, V: [B, T, H, 128] in one dtype (fp32: exact mode, bf16: MFMA mode), all torch
+    device tensors or all numpy host arrays; softmax_m, softmax_l: the forward's [B, T, H] fp32
+    statistics. Returns the three gradients in the inputs' dtype.
+    """
+    shape = tuple(Q.shape)
+    for name, x in (("d_output", d_output), ("output", output), ("K", K), ("V", V)):
+        if tuple(x.shape) != shape:
+            raise ValueError(f"{name} has shape {tuple(x.shape)}, expected {shape}")
+    if len(shape) != 4:
+        raise ValueError(f"expected [B,T,H,D] tensors, got {shape}")
+    B, T, H, D = shape
+    if tuple(softmax_m.shape) != (B, T, H) or tuple(softmax_l.shape) != (B, T, H):
+        raise ValueError("softmax_m and softmax_l must have shape [B, T, H]")
+    dtype = _mode_of(Q, mode)
+    if _is_torch(Q):
+        ins = [t.contiguous() for t in (d_output, output, Q, K, V)]
+        if any(not _is_torch(t) or not t.is_cuda or t.dtype != Q.dtype for t in ins):
+            raise TypeError("d_output, output, Q, K, V must be torch device tensors of one dtype")
+        m, l = softmax_m.contiguous().float(), softmax_l.contiguous().float()
+        ctx = ctx or default_context(Q.device.index or 0)
+        dQ, dK, dV = (torch.empty_like(ins[2]) for _ in range(3))
+        C.call("dt_flash_attn_bwd", ctx.handle, ins[0].data_ptr(), ins[1].data_ptr(), m.data_ptr(), l.data_ptr(),
+               ins[2].data_ptr(), ins[3].data_ptr(), ins[4].data_ptr(), dQ.data_ptr(), dK.data_ptr(), dV.data_ptr(),
+               B, T, H, D, float(scale), int(bool(causal)), dtype, C.DT_MEM_DEVICE, _stream_of(Q))
+        return FlashAttentionGradients(dQ, dK, dV)
+    ctx = ctx or default_context(0)
+    np_dt = np.float32 if dtype == C.DT_FP32_EXACT else np.uint16
+    ins = [np.ascontiguousarray(x, dtype=np_dt) for x in (d_output, output, Q, K, V)]
+    m = np.ascontiguousarray(softmax_m, dtype=np.float32)
+    l = np.ascontiguousarray(softmax_l, dtype=np.float32)
+    dQ, dK, dV = (np.empty_like(ins[2]) for _ in range(3))
+    C.call("dt_flash_attn_bwd", ctx.handle, ins[0].ctypes.data, ins[1].ctypes.data, m.ctypes.data, l.ctypes.data,
+           ins[2].ctypes.data, ins[3].ctypes.data, ins[4].ctypes.data, dQ.ctypes.data, dK.ctypes.data,
+           dV.ctypes.data, B, T, H, D, float(scale), int(bool(causal)), dtype, C.DT_MEM_HOST, None)
+    return FlashAttentionGradients(dQ, dK, dV)
 
 
 def qk_norm_rope(q_proj, k_proj, q_norm_w, k_norm_w, *, n_heads: int = C.N_HEADS, out_dtype: str = "fp32",

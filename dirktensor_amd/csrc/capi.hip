@@ -240,6 +240,7 @@ int dt_ctx_destroy(dt_ctx* ctx) {
     if (ctx->rope_cos) (void)hipFree(ctx->rope_cos);
     if (ctx->rope_sin) (void)hipFree(ctx->rope_sin);
     for (auto& b : ctx->stage) b.release();
+    ctx->bwd_stats.release();
     if (ctx->blas) rocblas_destroy_handle(static_cast<rocblas_handle>(ctx->blas));
     delete ctx;
     return DT_OK;
@@ -304,11 +305,64 @@ int dt_flash_attn_fwd(dt_ctx* ctx, const void* q, const void* k, const void* v, 
     return DT_OK;
 }
 
-int dt_flash_attn_bwd(dt_ctx*, const void*, const void*, const float*, const float*, const void*, const void*,
-                      const void*, void*, void*, void*, int, int, int, int, float, int, int, int, void*) {
+int dt_flash_attn_bwd(dt_ctx* ctx, const void* d_o, const void* o, const float* m, const float* l, const void* q,
+                      const void* k, const void* v, void* d_q, void* d_k, void* d_v, int B, int T, int H, int D,
+                      float scale, int causal, int dtype, int mem, void* stream) {
     clear_error();
-    return set_error(DT_ERR_NOT_IMPLEMENTED,
-                     "flash_attention_backward is not implemented on the GPU path (forward-only prefill)");
+    if (!d_o || !o || !m || !l || !q || !k || !v || !d_q || !d_k || !d_v)
+        return set_error(DT_ERR_INVALID_ARG, "all tensor pointers must be non-NULL");
+    if (D != DT_HEAD_DIM) return set_error(DT_ERR_UNSUPPORTED, "head_dim D=%d, kernels are built for D=%d", D, DT_HEAD_DIM);
+    if (B < 1 || H < 1 || T < 1) return set_error(DT_ERR_INVALID_ARG, "B=%d, T=%d, H=%d must be >= 1", B, T, H);
+    if (T > DT_MAX_SEQ_LEN) return set_error(DT_ERR_INVALID_ARG, "T=%d exceeds max_seq_len %d", T, DT_MAX_SEQ_LEN);
+    if (H > 65535 || B > 65535) return set_error(DT_ERR_UNSUPPORTED, "B=%d or H=%d exceeds grid limits", B, H);
+    if (dtype != DT_FP32_EXACT && dtype != DT_BF16) return set_error(DT_ERR_INVALID_ARG, "unknown dtype %d", dtype);
+    if (mem != DT_MEM_DEVICE && mem != DT_MEM_HOST) return set_error(DT_ERR_INVALID_ARG, "unknown mem %d", mem);
+    if (!(scale > 0.0f) || !std::isfinite(scale)) return set_error(DT_ERR_INVALID_ARG, "scale %g must be finite and > 0", scale);
+    if (causal != 0 && causal != 1) return set_error(DT_ERR_INVALID_ARG, "causal must be 0 or 1");
+    if (mem == DT_MEM_DEVICE && (!aligned16(d_o) || !aligned16(o) || !aligned16(q) || !aligned16(k) || !aligned16(v) ||
+                                 !aligned16(d_q) || !aligned16(d_k) || !aligned16(d_v)))
+        return set_error(DT_ERR_INVALID_ARG, "device tensors must be 16-byte aligned");
+    if (!ctx) return set_error(DT_ERR_INVALID_ARG, "ctx is NULL");
+    DT_TRY(check_device_binding(ctx));
+
+    hipStream_t s = static_cast<hipStream_t>(stream);
+    const int ld = H * D;
+    const size_t nst = (size_t)B * T * H;
+    DT_TRY(ctx->bwd_stats.ensure(2 * nst * sizeof(float)));
+    float* stats = static_cast<float*>(ctx->bwd_stats.ptr);
+    FlashBwdArgs ba{q, k, v, o, d_o, m, l, d_q, d_k, d_v, stats, stats + nst, B, T, H, ld, ld, ld, scale, causal};
+    auto run = [&](const FlashBwdArgs& x) {
+        return dtype == DT_BF16 ? launch_flash_bwd_bf16(x, s) : launch_flash_bwd_f32(x, s);
+    };
+    if (mem == DT_MEM_DEVICE) return run(ba);
+
+    // host memory: stage through context buffers, synchronous like the reference
+    const size_t esz = dtype == DT_BF16 ? 2 : 4;
+    const size_t nel = (size_t)B * T * H * D;
+    for (int i = 0; i < 8; ++i) DT_TRY(ctx->stage[i].ensure(nel * esz));
+    DT_TRY(ctx->stage[8].ensure(nst * sizeof(float)));
+    DT_TRY(ctx->stage[9].ensure(nst * sizeof(float)));
+    const void* src[5] = {d_o, o, q, k, v};
+    for (int i = 0; i < 5; ++i) DT_HIP_TRY(hipMemcpyAsync(ctx->stage[i].ptr, src[i], nel * esz, hipMemcpyHostToDevice, s));
+    DT_HIP_TRY(hipMemcpyAsync(ctx->stage[8].ptr, m, nst * sizeof(float), hipMemcpyHostToDevice, s));
+    DT_HIP_TRY(hipMemcpyAsync(ctx->stage[9].ptr, l, nst * sizeof(float), hipMemcpyHostToDevice, s));
+    FlashBwdArgs bd = ba;
+    bd.d_o = ctx->stage[0].ptr;
+    bd.o = ctx->stage[1].ptr;
+    bd.q = ctx->stage[2].ptr;
+    bd.k = ctx->stage[3].ptr;
+    bd.v = ctx->stage[4].ptr;
+    bd.d_q = ctx->stage[5].ptr;
+    bd.d_k = ctx->stage[6].ptr;
+    bd.d_v = ctx->stage[7].ptr;
+    bd.m = static_cast<const float*>(ctx->stage[8].ptr);
+    bd.l = static_cast<const float*>(ctx->stage[9].ptr);
+    DT_TRY(run(bd));
+    DT_HIP_TRY(hipMemcpyAsync(d_q, bd.d_q, nel * esz, hipMemcpyDeviceToHost, s));
+    DT_HIP_TRY(hipMemcpyAsync(d_k, bd.d_k, nel * esz, hipMemcpyDeviceToHost, s));
+    DT_HIP_TRY(hipMemcpyAsync(d_v, bd.d_v, nel * esz, hipMemcpyDeviceToHost, s));
+    DT_HIP_TRY(hipStreamSynchronize(s));
+    return DT_OK;
 }
 
 int dt_qk_norm_rope_fwd(dt_ctx* ctx, const float* q_in, const float* k_in, const float* q_norm_w,

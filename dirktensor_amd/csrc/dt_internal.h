@@ -60,6 +60,31 @@ struct FlashArgs {
 int launch_flash_fwd_f32(const FlashArgs& a, const SeqLens* lens, hipStream_t stream);
 int launch_flash_fwd_bf16(const FlashArgs& a, const SeqLens* lens, hipStream_t stream);
 
+// Arguments of one attention-core backward (FlashAttention.cpp:185-359). Row strides in elements.
+struct FlashBwdArgs {
+    const void* q;
+    const void* k;
+    const void* v;
+    const void* o;
+    const void* d_o;
+    const float* m;  // forward statistics, [B][T][H]
+    const float* l;
+    void* d_q;
+    void* d_k;
+    void* d_v;
+    float* delta;  // workspace [B][H][T]: rowsum(O * dO)
+    float* lse2;   // workspace [B][H][T]: m log2(e) + log2(l), +inf for an empty row
+    int B, T, H;
+    int ld_qkv;  // row stride of q, k and v
+    int ld_o;    // row stride of o and d_o
+    int ld_grad; // row stride of d_q, d_k and d_v
+    float scale;
+    int causal;
+};
+int launch_flash_bwd_prep(const FlashBwdArgs& a, int bf16, hipStream_t stream);  // fills delta and lse2
+int launch_flash_bwd_bf16(const FlashBwdArgs& a, hipStream_t stream);
+int launch_flash_bwd_f32(const FlashBwdArgs& a, hipStream_t stream);
+
 struct NormRopeArgs {
     const float* q_in;
     const float* k_in;
@@ -89,6 +114,7 @@ struct dt_ctx {
     float* rope_sin = nullptr;
     int rope_len = 0;
     float rope_theta = 0.0f;
-    dt::DeviceBuffer stage[6];  // host-memory path staging
+    dt::DeviceBuffer stage[10];  // host-memory path staging
+    dt::DeviceBuffer bwd_stats;  // attention-core backward: delta and lse2, 2 x [B][H][T] fp32
     void* blas = nullptr;        // rocblas_handle, created on first use
 };

@@ -1,0 +1,461 @@
+// Causal flash attention backward, bf16 MFMA mode, for gfx950 (CDNA4).
+//
+// Replaces flash_attention_backward (FlashAttention.cpp:185-359) with bf16
+// Q/K/V/O/dO/dQ/dK/dV, fp32 accumulation and fp32 P / dS arithmetic.
+//
+// The reference walks (query block, key block) pairs and accumulates all three
+// gradients from each pair; dK and dV rows receive contributions from many
+// query blocks and dQ rows from many key blocks. Here each gradient has one
+// owner, so nothing is accumulated through memory and the result does not
+// depend on scheduling:
+//   * flash_bwd_dkdv: a workgroup owns 128 keys of one (batch, head), 32 per
+//     wave, holds their K and V fragments in registers and streams 64-query
+//     tiles of Q and dO (plus the rows' lse2 and delta) through LDS. Per tile
+//     a wave forms S = Q K^T and dP = dO V^T for its keys, then
+//     P = exp2(S c - lse2) and dS = P (dP - delta), and accumulates
+//     dV^T += dO^T P and dK^T += Q^T dS.
+//   * flash_bwd_dq: a workgroup owns 128 queries, 32 per wave, holds their Q
+//     and dO fragments in registers and streams 64-key tiles of K and V.
+//     Per tile a wave forms S^T = K Q^T and dP^T = V dO^T, the same P and dS,
+//     and accumulates dQ^T += K^T dS^T.
+//   S and dP are recomputed in both kernels (7 MFMA products per tile pair
+//   instead of the reference's 5) in exchange for no atomics.
+// Causality (FlashAttention.cpp:247, 265-268) limits the dK/dV kernel to query
+// tiles at or after its keys and the dQ kernel to key tiles at or before its
+// queries; a workgroup takes block j and block n-1-j of the same head so that
+// every workgroup has the same number of tiles.
+//
+// MFMA operand layouts (v_mfma_f32_32x32x16_bf16): the A operand is a 32-row
+// fragment, lane l holding row l%32 and k elements 8*(l/32) .. +8; the B
+// operand is a 32-column fragment, lane l holding column l%32 and the same k
+// elements; accumulator element i of lane l is row 8*(i/4) + 4*(l/32) + i%4,
+// column l%32. An accumulator can therefore feed the next product directly as
+// its B operand (its rows become the k index, in that permuted order), with the
+// A operand read from LDS by the gfx950 transposing read ds_read_b64_tr_b16 in
+// the same permuted order; this is how P, dS (dK/dV kernel) and dS^T (dQ
+// kernel) enter the second products without leaving registers.
+//
+// LDS tiles are 64 rows of 256 bytes, unpadded, with 16-byte chunk c of row r
+// stored at c ^ swz(r), swz(r) = 4*(r & 3) + ((r >> 2) & 3): row-wise fragment
+// reads and transposing reads are both free of bank conflicts. Tiles arrive
+// by LDS DMA (buffer_load ... lds), double-buffered, one barrier per tile;
+// buffer descriptors end at row T - 1 so rows past the sequence arrive as zeros.
+
+#include "dt_internal.h"
+
+#include <type_traits>
+#include <utility>
+
+namespace dt {
+namespace {
+
+typedef float floatx16 __attribute__((ext_vector_type(16)));
+typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
+typedef __bf16 bf16x2 __attribute__((ext_vector_type(2)));
+typedef float floatx2 __attribute__((ext_vector_type(2)));
+typedef short shortx4 __attribute__((ext_vector_type(4)));
+typedef short shortx8 __attribute__((ext_vector_type(8)));
+typedef __attribute__((address_space(3))) shortx4 lds_shortx4;
+typedef __attribute__((address_space(3))) void lds_void;
+
+constexpr int kD = 128;
+constexpr int kTile = 64;                      // rows per streamed tile
+constexpr int kRowBytes = 256;                 // one row of 128 bf16
+constexpr int kTileBytes = kTile * kRowBytes;  // 16 KB
+constexpr int kBlk = 128;                      // rows owned by a workgroup: 4 waves x 32
+constexpr int kThreads = 256;
+constexpr float kLog2e = 1.4426950408889634f;
+constexpr int kBufferDword3 = 0x00020000;  // raw buffer, 32-bit data format (gfx9 family)
+
+__device__ __forceinline__ uint32_t pack_bf16x2(float lo, float hi) {
+    bf16x2 r = __builtin_convertvector((floatx2){lo, hi}, bf16x2);
+    return __builtin_bit_cast(uint32_t, r);
+}
+__device__ __forceinline__ __amdgpu_buffer_rsrc_t make_rsrc(const void* base, uint32_t bytes) {
+    return __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(base), (short)0, (int)bytes, kBufferDword3);
+}
+__device__ __forceinline__ int swz(int r) { return ((r & 3) << 2) | ((r >> 2) & 3); }
+__device__ __forceinline__ floatx16 mfma(bf16x8 a, bf16x8 b, floatx16 c) {
+    return __builtin_amdgcn_mfma_f32_32x32x16_bf16(a, b, c, 0, 0, 0);
+}
+__device__ __forceinline__ floatx16 zero16() {
+    floatx16 z;
+#pragma unroll
+    for (int i = 0; i < 16; ++i) z[i] = 0.0f;
+    return z;
+}
+
+template <typename F, int... Is>
+__device__ __forceinline__ void static_for_impl(F&& f, std::integer_sequence<int, Is...>) {
+    (f(std::integral_constant<int, Is>{}), ...);
+}
+template <int N, typename F>
+__device__ __forceinline__ void static_for(F&& f) {
+    static_for_impl(f, std::make_integer_sequence<int, N>{});
+}
+
+// Row fragment r = 2*cc + blk of a tile: rows 32*blk + ln, dims 16*cc + 8*hh .. +8 (the A operand
+// with the tile's rows as M). raddr[cc] is this lane's address of chunk 2*cc + hh in block 0.
+__device__ __forceinline__ bf16x8 read_row(const uint8_t* tile, const uint32_t (&raddr)[8], int cc, int blk) {
+    return __builtin_bit_cast(bf16x8, *reinterpret_cast<const uint4*>(tile + raddr[cc] + blk * 8192));
+}
+// Transposed fragment c = 8*blk + 4*u + db of a tile: rows 32*blk + 16*u + {4*hh .. +4, 8 + 4*hh .. +4}
+// (the accumulator's row order) as k, dims 32*db + ln as M (two transposing reads).
+__device__ __forceinline__ bf16x8 read_tr(const uint8_t* tile, const uint32_t (&taddr)[2][4], int c) {
+    const int rows = (c >> 3) * 8192 + ((c >> 2) & 1) * 4096;
+    const int db = c & 3;
+    const shortx4 lo = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_shortx4*)(tile + taddr[0][db] + rows));
+    const shortx4 hi = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_shortx4*)(tile + taddr[1][db] + rows + 2048));
+    return __builtin_bit_cast(bf16x8, (shortx8){lo[0], lo[1], lo[2], lo[3], hi[0], hi[1], hi[2], hi[3]});
+}
+
+// Lane addresses shared by both kernels.
+struct LaneAddr {
+    uint32_t raddr[8];
+    uint32_t taddr[2][4];
+};
+__device__ __forceinline__ LaneAddr lane_addr(int lane) {
+    LaneAddr A;
+    const int ln = lane & 31, hh = lane >> 5;
+    const int g = hh ^ swz(ln);
+#pragma unroll
+    for (int cc = 0; cc < 8; ++cc) A.raddr[cc] = (uint32_t)(ln * kRowBytes + (((2 * cc) ^ g) << 4));
+    // transposing reads: lane i of 16-lane group G reads row 4*hh + i/4 (+8 for the second read) of a
+    // 16-row chunk, dims 32*db + 16*(G & 1) + 4*(i & 3) .. +3
+    const int i16 = lane & 15;
+    const int g2 = (lane >> 4) & 1;
+#pragma unroll
+    for (int s = 0; s < 2; ++s) {
+        const int r = 4 * hh + (i16 >> 2) + 8 * s;
+#pragma unroll
+        for (int db = 0; db < 4; ++db) {
+            const int chunk = 4 * db + 2 * g2 + ((i16 & 3) >> 1);
+            A.taddr[s][db] = (uint32_t)((r - 8 * s) * kRowBytes + ((chunk ^ swz(r)) << 4) + 8 * (i16 & 1));
+        }
+    }
+    return A;
+}
+
+// DMA offsets of a 64-row tile with row stride ld (elements): instruction i of wave w fills rows
+// 16*i + 4*w + lane/16, 16 bytes per lane at chunk position lane%16, fetching the global chunk the
+// swizzle puts there.
+__device__ __forceinline__ void dma_offsets(uint32_t (&voff)[4], int lane, int wave, int ld) {
+    const int rlo = lane >> 4;
+    const int chunk = (lane & 15) ^ (4 * rlo + wave);
+#pragma unroll
+    for (int i = 0; i < 4; ++i) voff[i] = (uint32_t)(((16 * i + 4 * wave + rlo) * ld + 8 * chunk) * 2);
+}
+// rows r0 .. T-1 of a [T][ld] bf16 tensor -> one LDS tile (rows past T arrive as zeros)
+__device__ __forceinline__ void dma_tile(uint8_t* tile, const uint16_t* base, int r0, int T, int ld,
+                                         const uint32_t (&voff)[4], int wave) {
+    const __amdgpu_buffer_rsrc_t r = make_rsrc(base + (int64_t)r0 * ld, (uint32_t)(T - r0) * (uint32_t)ld * 2u);
+#pragma unroll
+    for (int i = 0; i < 4; ++i)
+        __builtin_amdgcn_raw_ptr_buffer_load_lds(r, (lds_void*)(tile + (4 * i + wave) * 1024), 16, voff[i], 0, 0, 0);
+}
+// 64 floats t0 .. t0+63 of a [T] row -> LDS (one wave; entries past T arrive as zeros)
+__device__ __forceinline__ void dma_stats(float* dst, const float* base, int t0, int T, int lane) {
+    const __amdgpu_buffer_rsrc_t r = make_rsrc(base + t0, (uint32_t)(T - t0) * 4u);
+    __builtin_amdgcn_raw_ptr_buffer_load_lds(r, (lds_void*)dst, 4, (uint32_t)lane * 4u, 0, 0, 0);
+}
+
+// this wave's LDS DMA and LDS accesses are complete before any wave passes it
+__device__ __forceinline__ void stage_barrier() { asm volatile("s_waitcnt vmcnt(0) lgkmcnt(0)\n\ts_barrier" ::: "memory"); }
+
+// one 32-row x 128 fragment set from global memory: f[cc] = X[row][16*cc + 8*hh .. +8], zeros when row >= T
+__device__ __forceinline__ void load_frags(bf16x8 (&f)[8], const uint16_t* base, int row, int T, int ld, int hh) {
+    if (row < T) {
+        const uint16_t* p = base + (int64_t)row * ld + 8 * hh;
+#pragma unroll
+        for (int cc = 0; cc < 8; ++cc) f[cc] = __builtin_bit_cast(bf16x8, *reinterpret_cast<const uint4*>(p + 16 * cc));
+    } else {
+#pragma unroll
+        for (int cc = 0; cc < 8; ++cc) f[cc] = __builtin_bit_cast(bf16x8, make_uint4(0, 0, 0, 0));
+    }
+}
+
+// accumulator X^T (4 blocks of 32 dims x 32 rows, lane = row) * mul -> bf16 row `row` of [T][ld] at base
+__device__ __forceinline__ void store_rows(uint16_t* base, int row, int ld, int hh, const floatx16 (&x)[4], float mul) {
+    uint16_t* p = base + (int64_t)row * ld;
+#pragma unroll
+    for (int db = 0; db < 4; ++db)
+#pragma unroll
+        for (int g = 0; g < 4; ++g) {
+            uint2 w;
+            w.x = pack_bf16x2(x[db][4 * g] * mul, x[db][4 * g + 1] * mul);
+            w.y = pack_bf16x2(x[db][4 * g + 2] * mul, x[db][4 * g + 3] * mul);
+            *reinterpret_cast<uint2*>(p + 32 * db + 8 * g + 4 * hh) = w;
+        }
+}
+
+// ------------------------------------------------------------------------------------------------ dK, dV
+// LDS stage: Q tile, dO tile, and the tile rows' lse2 and delta
+struct DkdvStage {
+    uint8_t q[kTileBytes];
+    uint8_t g[kTileBytes];
+    float lse2[kTile];
+    float delta[kTile];
+};
+
+__global__ __launch_bounds__(kThreads, 1) void flash_bwd_dkdv_bf16_kernel(FlashBwdArgs a) {
+    __shared__ __attribute__((aligned(1024))) DkdvStage st0;
+    __shared__ __attribute__((aligned(1024))) DkdvStage st1;
+
+    const int tid = threadIdx.x;
+    const int lane = tid & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+    const int ln = lane & 31;
+    const int hh = lane >> 5;
+    const int T = a.T;
+    const float c = a.scale * kLog2e;
+
+    const int nkb = (T + kBlk - 1) / kBlk;
+    const int npair = (nkb + 1) / 2;
+    const int pair = blockIdx.x % npair;
+    const int bh = blockIdx.x / npair;
+    const int b = bh / a.H, h = bh % a.H;
+
+    const LaneAddr LA = lane_addr(lane);
+    uint32_t voff_q[4], voff_g[4];
+    dma_offsets(voff_q, lane, wave, a.ld_qkv);
+    dma_offsets(voff_g, lane, wave, a.ld_o);
+
+    const uint16_t* Qg = static_cast<const uint16_t*>(a.q) + (int64_t)b * T * a.ld_qkv + (int64_t)h * kD;
+    const uint16_t* Kg = static_cast<const uint16_t*>(a.k) + (int64_t)b * T * a.ld_qkv + (int64_t)h * kD;
+    const uint16_t* Vg = static_cast<const uint16_t*>(a.v) + (int64_t)b * T * a.ld_qkv + (int64_t)h * kD;
+    const uint16_t* Gg = static_cast<const uint16_t*>(a.d_o) + (int64_t)b * T * a.ld_o + (int64_t)h * kD;
+    const float* lse2g = a.lse2 + (int64_t)bh * T;
+    const float* deltag = a.delta + (int64_t)bh * T;
+    uint16_t* dKg = static_cast<uint16_t*>(a.d_k) + (int64_t)b * T * a.ld_grad + (int64_t)h * kD;
+    uint16_t* dVg = static_cast<uint16_t*>(a.d_v) + (int64_t)b * T * a.ld_grad + (int64_t)h * kD;
+
+    for (int half = 0; half < 2; ++half) {
+        const int kb = half ? nkb - 1 - pair : pair;
+        if (half && kb == pair) break;  // odd count: the middle block once
+        const int kw = kb * kBlk + 32 * wave;  // the wave's first key
+        const int key = kw + ln;               // this lane's key (the products' N index)
+
+        bf16x8 kf[8], vf[8];
+        load_frags(kf, Kg, key, T, a.ld_qkv, hh);
+        load_frags(vf, Vg, key, T, a.ld_qkv, hh);
+        floatx16 dv[4], dk[4];
+#pragma unroll
+        for (int db = 0; db < 4; ++db) {
+            dv[db] = zero16();
+            dk[db] = zero16();
+        }
+
+        const int q_begin = a.causal ? kb * kBlk : 0;
+        const int n_steps = (T - q_begin + kTile - 1) / kTile;
+
+        auto dma = [&](DkdvStage& s, int q0) {
+            dma_tile(s.q, Qg, q0, T, a.ld_qkv, voff_q, wave);
+            dma_tile(s.g, Gg, q0, T, a.ld_o, voff_g, wave);
+            if (wave == 0) dma_stats(s.lse2, lse2g, q0, T, lane);
+            if (wave == 1) dma_stats(s.delta, deltag, q0, T, lane);
+        };
+        auto step = [&](const DkdvStage& s, DkdvStage& nxt, int q0, bool has_next) {
+            if (has_next) dma(nxt, q0 + kTile);
+            if (a.causal && q0 + kTile - 1 < kw) return;  // every query of the tile precedes the wave's keys
+            const bool need_mask = a.causal && q0 < kw + 31;
+            // S = Q K^T and dP = dO V^T for 64 queries (two 32-row blocks) x the wave's 32 keys
+            floatx16 sc[2], dp[2];
+#pragma unroll
+            for (int qb = 0; qb < 2; ++qb) {
+                sc[qb] = zero16();
+                dp[qb] = zero16();
+#pragma unroll
+                for (int cc = 0; cc < 8; ++cc) {
+                    sc[qb] = mfma(read_row(s.q, LA.raddr, cc, qb), kf[cc], sc[qb]);
+                    dp[qb] = mfma(read_row(s.g, LA.raddr, cc, qb), vf[cc], dp[qb]);
+                }
+            }
+            // P = exp2(S c - lse2), dS = P (dP - delta); element i of block qb is query
+            // q0 + 32*qb + 8*(i/4) + 4*hh + i%4
+            bf16x8 pb[2][2], dsb[2][2];
+#pragma unroll
+            for (int qb = 0; qb < 2; ++qb) {
+                float p[16], ds[16];
+#pragma unroll
+                for (int g = 0; g < 4; ++g) {
+                    const int qi = 32 * qb + 8 * g + 4 * hh;
+                    const float4 L4 = *reinterpret_cast<const float4*>(&s.lse2[qi]);
+                    const float4 D4 = *reinterpret_cast<const float4*>(&s.delta[qi]);
+                    const float Lr[4] = {L4.x, L4.y, L4.z, L4.w};
+                    const float Dr[4] = {D4.x, D4.y, D4.z, D4.w};
+#pragma unroll
+                    for (int r = 0; r < 4; ++r) {
+                        const int i = 4 * g + r;
+                        float pv = __builtin_amdgcn_exp2f(sc[qb][i] * c - Lr[r]);
+                        if (need_mask && key > q0 + qi + r) pv = 0.0f;
+                        p[i] = pv;
+                        ds[i] = pv * (dp[qb][i] - Dr[r]);
+                    }
+                }
+#pragma unroll
+                for (int u = 0; u < 2; ++u) {
+                    uint32_t wp[4], wd[4];
+#pragma unroll
+                    for (int e = 0; e < 4; ++e) {
+                        wp[e] = pack_bf16x2(p[8 * u + 2 * e], p[8 * u + 2 * e + 1]);
+                        wd[e] = pack_bf16x2(ds[8 * u + 2 * e], ds[8 * u + 2 * e + 1]);
+                    }
+                    pb[qb][u] = __builtin_bit_cast(bf16x8, make_uint4(wp[0], wp[1], wp[2], wp[3]));
+                    dsb[qb][u] = __builtin_bit_cast(bf16x8, make_uint4(wd[0], wd[1], wd[2], wd[3]));
+                }
+            }
+            // dV^T += dO^T P, dK^T += Q^T dS (k = the tile's queries, in accumulator row order)
+            static_for<16>([&](auto C) {
+                constexpr int ci = decltype(C)::value;  // = 8*qb + 4*u + db
+                dv[ci & 3] = mfma(read_tr(s.g, LA.taddr, ci), pb[ci >> 3][(ci >> 2) & 1], dv[ci & 3]);
+                dk[ci & 3] = mfma(read_tr(s.q, LA.taddr, ci), dsb[ci >> 3][(ci >> 2) & 1], dk[ci & 3]);
+            });
+        };
+
+        dma(st0, q_begin);
+        stage_barrier();
+        for (int it = 0; it < n_steps; it += 2) {
+            const int q0 = q_begin + it * kTile;
+            step(st0, st1, q0, it + 1 < n_steps);
+            stage_barrier();
+            if (it + 1 >= n_steps) break;
+            step(st1, st0, q0 + kTile, it + 2 < n_steps);
+            stage_barrier();
+        }
+        if (key < T) {
+            store_rows(dKg, key, a.ld_grad, hh, dk, a.scale);  // dS carries the reference's scale (:293)
+            store_rows(dVg, key, a.ld_grad, hh, dv, 1.0f);
+        }
+    }
+}
+
+// ------------------------------------------------------------------------------------------------ dQ
+struct DqStage {
+    uint8_t k[kTileBytes];
+    uint8_t v[kTileBytes];
+};
+
+__global__ __launch_bounds__(kThreads, 1) void flash_bwd_dq_bf16_kernel(FlashBwdArgs a) {
+    __shared__ __attribute__((aligned(1024))) DqStage st0;
+    __shared__ __attribute__((aligned(1024))) DqStage st1;
+
+    const int tid = threadIdx.x;
+    const int lane = tid & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+    const int ln = lane & 31;
+    const int hh = lane >> 5;
+    const int T = a.T;
+    const float c = a.scale * kLog2e;
+
+    const int nqb = (T + kBlk - 1) / kBlk;
+    const int npair = (nqb + 1) / 2;
+    const int pair = blockIdx.x % npair;
+    const int bh = blockIdx.x / npair;
+    const int b = bh / a.H, h = bh % a.H;
+
+    const LaneAddr LA = lane_addr(lane);
+    uint32_t voff[4];
+    dma_offsets(voff, lane, wave, a.ld_qkv);
+
+    const uint16_t* Qg = static_cast<const uint16_t*>(a.q) + (int64_t)b * T * a.ld_qkv + (int64_t)h * kD;
+    const uint16_t* Kg = static_cast<const uint16_t*>(a.k) + (int64_t)b * T * a.ld_qkv + (int64_t)h * kD;
+    const uint16_t* Vg = static_cast<const uint16_t*>(a.v) + (int64_t)b * T * a.ld_qkv + (int64_t)h * kD;
+    const uint16_t* Gg = static_cast<const uint16_t*>(a.d_o) + (int64_t)b * T * a.ld_o + (int64_t)h * kD;
+    uint16_t* dQg = static_cast<uint16_t*>(a.d_q) + (int64_t)b * T * a.ld_grad + (int64_t)h * kD;
+
+    for (int half = 0; half < 2; ++half) {
+        const int qb = half ? nqb - 1 - pair : pair;
+        if (half && qb == pair) break;
+        const int qw = qb * kBlk + 32 * wave;  // the wave's first query
+        const int q = qw + ln;                 // this lane's query (the products' N index)
+
+        bf16x8 qf[8], gf[8];
+        load_frags(qf, Qg, q, T, a.ld_qkv, hh);
+        load_frags(gf, Gg, q, T, a.ld_o, hh);
+        const float lse2 = q < T ? a.lse2[(int64_t)bh * T + q] : 0.0f;
+        const float delta = q < T ? a.delta[(int64_t)bh * T + q] : 0.0f;
+        const int lim = a.causal ? min(q, T - 1) : T - 1;  // keys > lim are masked
+        floatx16 dq[4];
+#pragma unroll
+        for (int db = 0; db < 4; ++db) dq[db] = zero16();
+
+        const int k_end = a.causal ? min(qb * kBlk + kBlk, T) : T;
+        const int n_steps = (k_end + kTile - 1) / kTile;
+
+        auto dma = [&](DqStage& s, int k0) {
+            dma_tile(s.k, Kg, k0, T, a.ld_qkv, voff, wave);
+            dma_tile(s.v, Vg, k0, T, a.ld_qkv, voff, wave);
+        };
+        auto step = [&](const DqStage& s, DqStage& nxt, int k0, bool has_next) {
+            if (has_next) dma(nxt, k0 + kTile);
+            if (a.causal && k0 > qw + 31) return;  // every key of the tile follows the wave's queries
+            const bool need_mask = (a.causal && k0 + kTile - 1 > qw) || k0 + kTile > T;
+            // S^T = K Q^T and dP^T = V dO^T for 64 keys (two 32-row blocks) x the wave's 32 queries
+            floatx16 sc[2], dp[2];
+#pragma unroll
+            for (int kb = 0; kb < 2; ++kb) {
+                sc[kb] = zero16();
+                dp[kb] = zero16();
+#pragma unroll
+                for (int cc = 0; cc < 8; ++cc) {
+                    sc[kb] = mfma(read_row(s.k, LA.raddr, cc, kb), qf[cc], sc[kb]);
+                    dp[kb] = mfma(read_row(s.v, LA.raddr, cc, kb), gf[cc], dp[kb]);
+                }
+            }
+            // dS^T = P^T (dP^T - delta); element i of block kb is key k0 + 32*kb + 8*(i/4) + 4*hh + i%4
+            bf16x8 dsb[2][2];
+#pragma unroll
+            for (int kb = 0; kb < 2; ++kb) {
+                float ds[16];
+#pragma unroll
+                for (int i = 0; i < 16; ++i) {
+                    float pv = __builtin_amdgcn_exp2f(sc[kb][i] * c - lse2);
+                    if (need_mask && k0 + 32 * kb + 8 * (i / 4) + 4 * hh + (i % 4) > lim) pv = 0.0f;
+                    ds[i] = pv * (dp[kb][i] - delta);
+                }
+#pragma unroll
+                for (int u = 0; u < 2; ++u) {
+                    uint32_t wd[4];
+#pragma unroll
+                    for (int e = 0; e < 4; ++e) wd[e] = pack_bf16x2(ds[8 * u + 2 * e], ds[8 * u + 2 * e + 1]);
+                    dsb[kb][u] = __builtin_bit_cast(bf16x8, make_uint4(wd[0], wd[1], wd[2], wd[3]));
+                }
+            }
+            // dQ^T += K^T dS^T (k = the tile's keys, in accumulator row order)
+            static_for<16>([&](auto C) {
+                constexpr int ci = decltype(C)::value;  // = 8*kb + 4*u + db
+                dq[ci & 3] = mfma(read_tr(s.k, LA.taddr, ci), dsb[ci >> 3][(ci >> 2) & 1], dq[ci & 3]);
+            });
+        };
+
+        dma(st0, 0);
+        stage_barrier();
+        for (int it = 0; it < n_steps; it += 2) {
+            const int k0 = it * kTile;
+            step(st0, st1, k0, it + 1 < n_steps);
+            stage_barrier();
+            if (it + 1 >= n_steps) break;
+            step(st1, st0, k0 + kTile, it + 2 < n_steps);
+            stage_barrier();
+        }
+        if (q < T) store_rows(dQg, q, a.ld_grad, hh, dq, a.scale);
+    }
+}
+
+}  // namespace
+
+int launch_flash_bwd_bf16(const FlashBwdArgs& a, hipStream_t stream) {
+    if ((int64_t)a.T * a.ld_qkv * 2 >= ((int64_t)1 << 31) || (int64_t)a.T * a.ld_o * 2 >= ((int64_t)1 << 31))
+        return set_error(DT_ERR_UNSUPPORTED, "extent of one sequence exceeds 2 GiB");
+    DT_TRY(launch_flash_bwd_prep(a, 1, stream));
+    const int64_t npair = ((a.T + kBlk - 1) / kBlk + 1) / 2;
+    const int64_t grid = npair * a.B * a.H;
+    if (grid > 0x7fffffff) return set_error(DT_ERR_UNSUPPORTED, "too many workgroups");
+    hipLaunchKernelGGL(flash_bwd_dkdv_bf16_kernel, dim3((unsigned)grid), dim3(kThreads), 0, stream, a);
+    DT_HIP_TRY(hipGetLastError());
+    hipLaunchKernelGGL(flash_bwd_dq_bf16_kernel, dim3((unsigned)grid), dim3(kThreads), 0, stream, a);
+    DT_HIP_TRY(hipGetLastError());
+    return DT_OK;
+}
+
+}  // namespace dt
