@@ -51,8 +51,12 @@ SIGNATURES = {
     "dt_attn_layer_create": (_c_int, [_vp, _vp, _vp, _vp, _vp, _vp, _vp, _c_int, _c_int, _c_int, ctypes.POINTER(_vp)]),
     "dt_attn_layer_load": (_c_int, [_vp, ctypes.c_char_p, ctypes.c_uint, ctypes.POINTER(_vp)]),
     "dt_attn_layer_destroy": (_c_int, [_vp]),
-    "dt_attn_layer_fwd": (_c_int, [_vp, _vp, _vp, _c_int, _c_int, _vp, _c_int, _c_int, _vp]),
+    "dt_attn_layer_fwd": (_c_int, [_vp, _vp, _vp, _c_int, _c_int, _vp, _c_int, _c_int, _c_int, _vp]),
     "dt_attn_layer_bwd": (_c_int, [_vp, _vp, _vp, _c_int, _c_int, _c_int, _vp]),
+    "dt_attn_layer_step": (_c_int, [_vp, ctypes.c_float, _vp]),
+    "dt_attn_layer_zero_grad": (_c_int, [_vp, _vp]),
+    "dt_attn_layer_get_weights": (_c_int, [_vp] * 7 + [_c_int, _vp]),
+    "dt_attn_layer_get_grads": (_c_int, [_vp] * 7 + [_c_int, _vp]),
 }
 
 _lib = None

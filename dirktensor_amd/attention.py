@@ -255,13 +255,14 @@ class OlmoAttention:
     ``OlmoAttention(folder, index)`` loads the reference's per-layer .npy files
     (OlmoAttention.cpp:39-53); ``OlmoAttention.from_weights`` takes arrays
     (fp32, [out, in] like torch Linear). ``forward(x)`` maps [B, T, d_model]
-    fp32 to [B, T, d_model] fp32 (OlmoAttention.cpp:56-108). backward, step and
-    zero_grad raise: the GPU path is forward-only.
+    fp32 to [B, T, d_model] fp32 (OlmoAttention.cpp:56-108); backward, step and
+    zero_grad follow OlmoAttention.cpp:193-330.
     """
 
     def __init__(self, folder: Optional[str] = None, index: int = 0, *, ctx: Optional[Context] = None,
                  _handle: Optional[ctypes.c_void_p] = None):
         self.ctx = ctx or default_context(0)
+        self.d_model = None
         if _handle is not None:
             self.handle = _handle
             return
@@ -270,6 +271,8 @@ class OlmoAttention:
         h = ctypes.c_void_p()
         C.call("dt_attn_layer_load", self.ctx.handle, str(folder).encode(), int(index), ctypes.byref(h))
         self.handle = h
+        self.d_model = int(np.load(f"{folder}/model.layers.{index}.self_attn.q_norm.weight.npy",
+                                   mmap_mode="r").shape[0])
 
     @classmethod
     def from_weights(cls, wq, wk, wv, wo, q_norm, k_norm, *, ctx: Optional[Context] = None) -> "OlmoAttention":
@@ -285,7 +288,9 @@ class OlmoAttention:
             ws = [np.ascontiguousarray(w, dtype=np.float32) for w in (wq, wk, wv, wo, q_norm, k_norm)]
             C.call("dt_attn_layer_create", ctx.handle, *[w.ctypes.data for w in ws], dm, dm // C.HEAD_DIM,
                    C.DT_MEM_HOST, ctypes.byref(h))
-        return cls(ctx=ctx, _handle=h)
+        layer = cls(ctx=ctx, _handle=h)
+        layer.d_model = dm
+        return layer
 
     def close(self) -> None:
         if getattr(self, "handle", None):
@@ -298,29 +303,74 @@ class OlmoAttention:
         except Exception:
             pass
 
-    def forward(self, x, *, seq_lens=None, mode: str = "fp32"):
+    def forward(self, x, *, seq_lens=None, mode: str = "fp32", save_for_backward: Optional[bool] = None):
+        """OlmoAttention::forward. Keeps the state backward needs (as the reference always does) unless
+        ``save_for_backward`` is False; the default keeps it for full sequences and not with ``seq_lens``
+        (the backward covers full sequences only)."""
         B, T, dm = (int(s) for s in x.shape)
         dtype = _mode_of(x, mode)
         lens_arr, lens_p = _seq_lens_arg(seq_lens, B)
+        save = int(seq_lens is None) if save_for_backward is None else int(bool(save_for_backward))
         if _is_torch(x):
             xi = x.contiguous().float()
             out = torch.empty_like(xi)
             C.call("dt_attn_layer_fwd", self.handle, xi.data_ptr(), out.data_ptr(), B, T, lens_p, dtype,
-                   C.DT_MEM_DEVICE, _stream_of(xi))
+                   C.DT_MEM_DEVICE, save, _stream_of(xi))
             return out
         xi = np.ascontiguousarray(x, dtype=np.float32)
         out = np.empty_like(xi)
         C.call("dt_attn_layer_fwd", self.handle, xi.ctypes.data, out.ctypes.data, B, T, lens_p, dtype,
-               C.DT_MEM_HOST, None)
+               C.DT_MEM_HOST, save, None)
         return out
 
     __call__ = forward
 
     def backward(self, d_output):
-        C.call("dt_attn_layer_bwd", self.handle, None, None, 0, 0, C.DT_MEM_DEVICE, None)
+        """OlmoAttention::backward (OlmoAttention.cpp:193-312): returns d_input and accumulates the
+        parameter gradients, for the last forward that kept its state."""
+        B, T, dm = (int(s) for s in d_output.shape)
+        if _is_torch(d_output):
+            g = d_output.contiguous().float()
+            dx = torch.empty_like(g)
+            C.call("dt_attn_layer_bwd", self.handle, g.data_ptr(), dx.data_ptr(), B, T, C.DT_MEM_DEVICE,
+                   _stream_of(g))
+            return dx
+        g = np.ascontiguousarray(d_output, dtype=np.float32)
+        dx = np.empty_like(g)
+        C.call("dt_attn_layer_bwd", self.handle, g.ctypes.data, dx.ctypes.data, B, T, C.DT_MEM_HOST, None)
+        return dx
 
     def step(self, lr: float):
-        raise NotImplementedError("OlmoAttention.step: the GPU path is forward-only (no gradients are kept)")
+        """OlmoAttention::step (OlmoAttention.cpp:314-321): w -= lr * grad."""
+        C.call("dt_attn_layer_step", self.handle, float(lr), self._stream())
 
     def zero_grad(self):
-        raise NotImplementedError("OlmoAttention.zero_grad: the GPU path is forward-only (no gradients are kept)")
+        """OlmoAttention::zero_grad (OlmoAttention.cpp:323-330)."""
+        C.call("dt_attn_layer_zero_grad", self.handle, self._stream())
+
+    def _stream(self):
+        if torch is not None and torch.cuda.is_available():
+            return ctypes.c_void_p(torch.cuda.current_stream(self.ctx.device).cuda_stream)
+        return None
+
+    def _copy_out(self, fn: str) -> dict:
+        dm = self._d_model()
+        arrs = {k: np.empty((dm, dm), np.float32) for k in ("wq", "wk", "wv", "wo")}
+        arrs["q_norm"] = np.empty(dm, np.float32)
+        arrs["k_norm"] = np.empty(dm, np.float32)
+        C.call(fn, self.handle, *[arrs[k].ctypes.data for k in ("wq", "wk", "wv", "wo", "q_norm", "k_norm")],
+               C.DT_MEM_HOST, self._stream())
+        return arrs
+
+    def _d_model(self) -> int:
+        if getattr(self, "d_model", None) is None:
+            raise RuntimeError("d_model unknown: construct with from_weights or pass d_model")
+        return self.d_model
+
+    def weights(self) -> dict:
+        """Host copies of Wq, Wk, Wv, Wo, q_norm, k_norm (the param<2>::w members)."""
+        return self._copy_out("dt_attn_layer_get_weights")
+
+    def grads(self) -> dict:
+        """Host copies of the accumulated gradients (the param<2>::grad members)."""
+        return self._copy_out("dt_attn_layer_get_grads")

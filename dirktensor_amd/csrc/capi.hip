@@ -118,27 +118,35 @@ static int ensure_blas(dt_ctx* ctx) {
     return DT_OK;
 }
 
-// Row-major C[M][N] = A[M][K] * W[N][K]^T (y = x W^T). In rocBLAS's column-major
-// terms this is C^T (N x M) = W (N x K, i.e. op(T) of the K x N col-major view) * A^T.
-static int gemm_xwt(dt_ctx* ctx, hipStream_t s, int M, int N, int K, const void* A, int lda, const void* W, int ldw,
-                    float* C, int ldc, bool bf16_in) {
+// Row-major C[M][N] = op(A)[M][K] op(B)[K][N] + beta C, op = transpose when the flag is set (A is then
+// stored [K][M], B [N][K]). In rocBLAS's column-major terms a row-major X is X^T, so this is
+// C^T = op(B)^T op(A)^T: B goes first, each transposed exactly when it is transposed here.
+static int gemm_rm(dt_ctx* ctx, hipStream_t s, bool ta, bool tb, int M, int N, int K, const void* A, int lda,
+                   const void* B, int ldb, float beta, float* C, int ldc, bool bf16_in) {
     DT_TRY(ensure_blas(ctx));
     rocblas_handle h = static_cast<rocblas_handle>(ctx->blas);
     rocblas_set_stream(h, s);
-    const float one = 1.0f, zero = 0.0f;
+    const float one = 1.0f;
+    const rocblas_operation opb = tb ? rocblas_operation_transpose : rocblas_operation_none;
+    const rocblas_operation opa = ta ? rocblas_operation_transpose : rocblas_operation_none;
     rocblas_status st;
     if (!bf16_in) {
-        st = rocblas_sgemm(h, rocblas_operation_transpose, rocblas_operation_none, N, M, K, &one,
-                           static_cast<const float*>(W), ldw, static_cast<const float*>(A), lda, &zero, C, ldc);
+        st = rocblas_sgemm(h, opb, opa, N, M, K, &one, static_cast<const float*>(B), ldb, static_cast<const float*>(A),
+                           lda, &beta, C, ldc);
     } else {
-        st = rocblas_gemm_ex(h, rocblas_operation_transpose, rocblas_operation_none, N, M, K, &one, W,
-                             rocblas_datatype_bf16_r, ldw, A, rocblas_datatype_bf16_r, lda, &zero, C,
-                             rocblas_datatype_f32_r, ldc, C, rocblas_datatype_f32_r, ldc, rocblas_datatype_f32_r,
-                             rocblas_gemm_algo_standard, 0, 0);
+        st = rocblas_gemm_ex(h, opb, opa, N, M, K, &one, B, rocblas_datatype_bf16_r, ldb, A, rocblas_datatype_bf16_r,
+                             lda, &beta, C, rocblas_datatype_f32_r, ldc, C, rocblas_datatype_f32_r, ldc,
+                             rocblas_datatype_f32_r, rocblas_gemm_algo_standard, 0, 0);
     }
-    if (st != rocblas_status_success) return set_error(DT_ERR_BLAS, "rocBLAS GEMM (%d x %d x %d): %s", M, N, K,
-                                                       blas_status_str(st));
+    if (st != rocblas_status_success)
+        return set_error(DT_ERR_BLAS, "rocBLAS GEMM (%d x %d x %d): %s", M, N, K, blas_status_str(st));
     return DT_OK;
+}
+
+// y = x W^T with W stored [N][K] like torch Linear (OlmoAttention.cpp:68,74,80,104)
+static int gemm_xwt(dt_ctx* ctx, hipStream_t s, int M, int N, int K, const void* A, int lda, const void* W, int ldw,
+                    float* C, int ldc, bool bf16_in) {
+    return gemm_rm(ctx, s, false, true, M, N, K, A, lda, W, ldw, 0.0f, C, ldc, bf16_in);
 }
 
 // ---------------- .npy reader (v1/v2/v3, little-endian fp32, C order) ----------------
@@ -203,6 +211,19 @@ struct dt_attn_layer {
     float* q_norm = nullptr;
     float* k_norm = nullptr;
     dt::DeviceBuffer qkv32, qkv16, attn, x16;
+    bool w16_stale = true;  // the bf16 copies lag the fp32 weights (before the first bf16 forward, after step)
+    // forward state kept for backward (OlmoAttention.h:28-38) when save_for_backward is set
+    dt::DeviceBuffer x32;   // the input rows (fp32)
+    dt::DeviceBuffer att32; // fp32 mode: q_rope | k_rope | v, [rows][3*d_model]
+    dt::DeviceBuffer rms;   // q and k rms, 2 x [rows]
+    dt::DeviceBuffer stats; // attention m and l, 2 x [rows][H]
+    int saved_B = 0, saved_T = 0, saved_dtype = -1;  // saved_T == 0: nothing saved
+    // backward workspaces and the accumulated gradients (param<2>::grad, param.h:5-15)
+    dt::DeviceBuffer d_attn32, d16, d_qkv, partial;
+    float* g_qkv = nullptr;  // [3*d_model][d_model]
+    float* g_o = nullptr;    // [d_model][d_model]
+    float* g_qn = nullptr;   // [d_model]
+    float* g_kn = nullptr;
 };
 
 using namespace dt;
@@ -211,7 +232,7 @@ extern "C" {
 
 const char* dt_last_error(void) { return t_err.c_str(); }
 
-int dt_version(void) { return 1; }
+int dt_version(void) { return 2; }
 
 int dt_ctx_create(int device, dt_ctx** out) {
     clear_error();
@@ -499,16 +520,19 @@ int dt_attn_layer_destroy(dt_attn_layer* L) {
     if (L->w_o16) (void)hipFree(L->w_o16);
     if (L->q_norm) (void)hipFree(L->q_norm);
     if (L->k_norm) (void)hipFree(L->k_norm);
-    L->qkv32.release();
-    L->qkv16.release();
-    L->attn.release();
-    L->x16.release();
+    if (L->g_qkv) (void)hipFree(L->g_qkv);
+    if (L->g_o) (void)hipFree(L->g_o);
+    if (L->g_qn) (void)hipFree(L->g_qn);
+    if (L->g_kn) (void)hipFree(L->g_kn);
+    for (dt::DeviceBuffer* b : {&L->qkv32, &L->qkv16, &L->attn, &L->x16, &L->x32, &L->att32, &L->rms, &L->stats,
+                                &L->d_attn32, &L->d16, &L->d_qkv, &L->partial})
+        b->release();
     delete L;
     return DT_OK;
 }
 
 int dt_attn_layer_fwd(dt_attn_layer* L, const float* x, float* out, int B, int T, const int32_t* seq_lens,
-                      int dtype, int mem, void* stream) {
+                      int dtype, int mem, int save_for_backward, void* stream) {
     clear_error();
     if (!x || !out) return set_error(DT_ERR_INVALID_ARG, "x and out must be non-NULL");
     if (B < 1 || T < 1) return set_error(DT_ERR_INVALID_ARG, "B=%d, T=%d must be >= 1", B, T);
@@ -516,6 +540,10 @@ int dt_attn_layer_fwd(dt_attn_layer* L, const float* x, float* out, int B, int T
     if ((int64_t)B * T > 0x7fffffff / 8) return set_error(DT_ERR_UNSUPPORTED, "B*T too large");
     if (dtype != DT_FP32_EXACT && dtype != DT_BF16) return set_error(DT_ERR_INVALID_ARG, "unknown dtype %d", dtype);
     if (mem != DT_MEM_DEVICE && mem != DT_MEM_HOST) return set_error(DT_ERR_INVALID_ARG, "unknown mem %d", mem);
+    if (save_for_backward != 0 && save_for_backward != 1)
+        return set_error(DT_ERR_INVALID_ARG, "save_for_backward must be 0 or 1");
+    if (save_for_backward && seq_lens)
+        return set_error(DT_ERR_UNSUPPORTED, "save_for_backward with seq_lens: the backward covers full sequences only");
     if (mem == DT_MEM_DEVICE && (!aligned16(x) || !aligned16(out)))
         return set_error(DT_ERR_INVALID_ARG, "device x/out must be 16-byte aligned");
     DT_TRY(validate_seq_lens(seq_lens, B, T));
@@ -529,13 +557,27 @@ int dt_attn_layer_fwd(dt_attn_layer* L, const float* x, float* out, int B, int T
     const size_t act = (size_t)rows * dm;
     const float* xd = x;
     float* od = out;
-    if (mem == DT_MEM_HOST) {
+    L->saved_T = 0;  // a failed or inference forward leaves nothing to differentiate
+    if (save_for_backward) {
+        // the reference keeps its own copy of the input (m_act_input_2d, OlmoAttention.cpp:64)
+        DT_TRY(L->x32.ensure(act * 4));
+        DT_HIP_TRY(hipMemcpyAsync(L->x32.ptr, x, act * 4, mem == DT_MEM_HOST ? hipMemcpyHostToDevice
+                                                                              : hipMemcpyDeviceToDevice, s));
+        xd = static_cast<const float*>(L->x32.ptr);
+        DT_TRY(L->rms.ensure((size_t)2 * rows * 4));
+        DT_TRY(L->stats.ensure((size_t)2 * rows * H * 4));
+    } else if (mem == DT_MEM_HOST) {
         DT_TRY(ctx->stage[0].ensure(act * 4));
-        DT_TRY(ctx->stage[1].ensure(act * 4));
         DT_HIP_TRY(hipMemcpyAsync(ctx->stage[0].ptr, x, act * 4, hipMemcpyHostToDevice, s));
         xd = static_cast<const float*>(ctx->stage[0].ptr);
+    }
+    if (mem == DT_MEM_HOST) {
+        DT_TRY(ctx->stage[1].ensure(act * 4));
         od = static_cast<float*>(ctx->stage[1].ptr);
     }
+    float* rms = save_for_backward ? static_cast<float*>(L->rms.ptr) : nullptr;
+    float* st_m = save_for_backward ? static_cast<float*>(L->stats.ptr) : nullptr;
+    float* st_l = save_for_backward ? st_m + (size_t)rows * H : nullptr;
     DT_TRY(L->qkv32.ensure(act * 3 * 4));
     float* qkv = static_cast<float*>(L->qkv32.ptr);
     const float scale = 1.0f / std::sqrt((float)DT_HEAD_DIM);  // OlmoAttention.cpp:91
@@ -545,11 +587,18 @@ int dt_attn_layer_fwd(dt_attn_layer* L, const float* x, float* out, int B, int T
         float* attn = static_cast<float*>(L->attn.ptr);
         // Q|K|V = x [Wq;Wk;Wv]^T in one N = 3*d_model GEMM (OlmoAttention.cpp:68,74,80)
         DT_TRY(gemm_xwt(ctx, s, rows, 3 * dm, dm, xd, dm, L->w_qkv, dm, qkv, 3 * dm, false));
-        // q/k norm + RoPE in place (OlmoAttention.cpp:70,76,87-88)
-        NormRopeArgs na{qkv, qkv + dm, nullptr, L->q_norm, L->k_norm, qkv, qkv + dm, nullptr, nullptr, nullptr,
-                        ctx->rope_cos, ctx->rope_sin, rows, T, H, 3 * dm, 3 * dm, DT_RMS_EPS};
+        // q/k norm + RoPE (OlmoAttention.cpp:70,76,87-88): in place, or into att32 (with V copied beside them)
+        // when the pre-norm projections must survive for the norms' backward
+        float* att = qkv;
+        if (save_for_backward) {
+            DT_TRY(L->att32.ensure(act * 3 * 4));
+            att = static_cast<float*>(L->att32.ptr);
+        }
+        NormRopeArgs na{qkv, qkv + dm, save_for_backward ? qkv + 2 * dm : nullptr, L->q_norm, L->k_norm, att,
+                        att + dm, att + 2 * dm, rms, rms ? rms + rows : nullptr, ctx->rope_cos, ctx->rope_sin, rows, T,
+                        H, 3 * dm, 3 * dm, DT_RMS_EPS};
         DT_TRY(launch_qk_norm_rope(na, 0, s));
-        FlashArgs fa{qkv, qkv + dm, qkv + 2 * dm, attn, nullptr, nullptr, B, T, H, 3 * dm, 3 * dm, 3 * dm, dm,
+        FlashArgs fa{att, att + dm, att + 2 * dm, attn, st_m, st_l, B, T, H, 3 * dm, 3 * dm, 3 * dm, dm,
                      scale, 1, seq_lens ? 1 : 0};
         DT_TRY(run_flash(ctx, fa, seq_lens, DT_FP32_EXACT, s));  // OlmoAttention.cpp:94
         DT_TRY(gemm_xwt(ctx, s, rows, dm, dm, attn, dm, L->w_o, dm, od, dm, false));  // :104
@@ -557,8 +606,12 @@ int dt_attn_layer_fwd(dt_attn_layer* L, const float* x, float* out, int B, int T
         if (!L->w_qkv16) {
             DT_HIP_TRY(hipMalloc(&L->w_qkv16, (size_t)3 * dm * dm * 2));
             DT_HIP_TRY(hipMalloc(&L->w_o16, (size_t)dm * dm * 2));
+            L->w16_stale = true;
+        }
+        if (L->w16_stale) {
             DT_TRY(launch_f32_to_bf16(L->w_qkv, L->w_qkv16, (int64_t)3 * dm * dm, s));
             DT_TRY(launch_f32_to_bf16(L->w_o, L->w_o16, (int64_t)dm * dm, s));
+            L->w16_stale = false;
         }
         DT_TRY(L->x16.ensure(act * 2));
         DT_TRY(L->qkv16.ensure(act * 3 * 2));
@@ -569,9 +622,10 @@ int dt_attn_layer_fwd(dt_attn_layer* L, const float* x, float* out, int B, int T
         DT_TRY(launch_f32_to_bf16(xd, x16, (int64_t)act, s));
         DT_TRY(gemm_xwt(ctx, s, rows, 3 * dm, dm, x16, dm, L->w_qkv16, dm, qkv, 3 * dm, true));
         NormRopeArgs na{qkv, qkv + dm, qkv + 2 * dm, L->q_norm, L->k_norm, qkv16, qkv16 + dm, qkv16 + 2 * dm,
-                        nullptr, nullptr, ctx->rope_cos, ctx->rope_sin, rows, T, H, 3 * dm, 3 * dm, DT_RMS_EPS};
+                        rms, rms ? rms + rows : nullptr, ctx->rope_cos, ctx->rope_sin, rows, T, H, 3 * dm, 3 * dm,
+                        DT_RMS_EPS};
         DT_TRY(launch_qk_norm_rope(na, 1, s));
-        FlashArgs fa{qkv16, qkv16 + dm, qkv16 + 2 * dm, attn16, nullptr, nullptr, B, T, H, 3 * dm, 3 * dm, 3 * dm,
+        FlashArgs fa{qkv16, qkv16 + dm, qkv16 + 2 * dm, attn16, st_m, st_l, B, T, H, 3 * dm, 3 * dm, 3 * dm,
                      dm, scale, 1, seq_lens ? 1 : 0};
         DT_TRY(run_flash(ctx, fa, seq_lens, DT_BF16, s));
         DT_TRY(gemm_xwt(ctx, s, rows, dm, dm, attn16, dm, L->w_o16, dm, od, dm, true));
@@ -580,13 +634,169 @@ int dt_attn_layer_fwd(dt_attn_layer* L, const float* x, float* out, int B, int T
         DT_HIP_TRY(hipMemcpyAsync(out, od, act * 4, hipMemcpyDeviceToHost, s));
         DT_HIP_TRY(hipStreamSynchronize(s));
     }
+    if (save_for_backward) {
+        L->saved_B = B;
+        L->saved_T = T;
+        L->saved_dtype = dtype;
+    }
     return DT_OK;
 }
 
-int dt_attn_layer_bwd(dt_attn_layer*, const float*, float*, int, int, int, void*) {
+static int ensure_grads(dt_attn_layer* L, hipStream_t s) {
+    if (L->g_qkv) return DT_OK;
+    const size_t dm = L->d_model;
+    DT_HIP_TRY(hipMalloc(&L->g_qkv, 3 * dm * dm * 4));
+    DT_HIP_TRY(hipMalloc(&L->g_o, dm * dm * 4));
+    DT_HIP_TRY(hipMalloc(&L->g_qn, dm * 4));
+    DT_HIP_TRY(hipMalloc(&L->g_kn, dm * 4));
+    DT_TRY(launch_fill_zero(L->g_qkv, (int64_t)(3 * dm * dm), s));
+    DT_TRY(launch_fill_zero(L->g_o, (int64_t)(dm * dm), s));
+    DT_TRY(launch_fill_zero(L->g_qn, (int64_t)dm, s));
+    DT_TRY(launch_fill_zero(L->g_kn, (int64_t)dm, s));
+    return DT_OK;
+}
+
+int dt_attn_layer_bwd(dt_attn_layer* L, const float* d_out, float* d_x, int B, int T, int mem, void* stream) {
     clear_error();
-    return set_error(DT_ERR_NOT_IMPLEMENTED,
-                     "OlmoAttention::backward is not implemented on the GPU path (forward-only prefill)");
+    if (!d_out || !d_x) return set_error(DT_ERR_INVALID_ARG, "d_out and d_x must be non-NULL");
+    if (mem != DT_MEM_DEVICE && mem != DT_MEM_HOST) return set_error(DT_ERR_INVALID_ARG, "unknown mem %d", mem);
+    if (mem == DT_MEM_DEVICE && (!aligned16(d_out) || !aligned16(d_x)))
+        return set_error(DT_ERR_INVALID_ARG, "device d_out/d_x must be 16-byte aligned");
+    if (!L) return set_error(DT_ERR_INVALID_ARG, "layer is NULL");
+    if (L->saved_T == 0)
+        return set_error(DT_ERR_INVALID_ARG, "no saved forward: call dt_attn_layer_fwd with save_for_backward = 1 first");
+    if (B != L->saved_B || T != L->saved_T)
+        return set_error(DT_ERR_INVALID_ARG, "B=%d, T=%d differ from the saved forward's B=%d, T=%d", B, T, L->saved_B,
+                         L->saved_T);
+    dt_ctx* ctx = L->ctx;
+    DT_TRY(check_device_binding(ctx));
+    hipStream_t s = static_cast<hipStream_t>(stream);
+    const bool bf = L->saved_dtype == DT_BF16;
+    const int dm = L->d_model, H = L->n_heads, rows = B * T;
+    const size_t act = (size_t)rows * dm;
+    const size_t esz = bf ? 2 : 4;
+    DT_TRY(ensure_grads(L, s));
+
+    const float* gd = d_out;
+    float* dxd = d_x;
+    if (mem == DT_MEM_HOST) {
+        DT_TRY(ctx->stage[0].ensure(act * 4));
+        DT_TRY(ctx->stage[1].ensure(act * 4));
+        DT_HIP_TRY(hipMemcpyAsync(ctx->stage[0].ptr, d_out, act * 4, hipMemcpyHostToDevice, s));
+        gd = static_cast<const float*>(ctx->stage[0].ptr);
+        dxd = static_cast<float*>(ctx->stage[1].ptr);
+    }
+    DT_TRY(L->d_attn32.ensure(act * 4));
+    DT_TRY(L->d_qkv.ensure(act * 3 * esz));
+    const int nblk = norm_rope_bwd_blocks(rows);
+    DT_TRY(L->partial.ensure((size_t)2 * nblk * dm * 4));
+    DT_TRY(ctx->bwd_stats.ensure((size_t)2 * rows * H * 4));
+    float* d_attn = static_cast<float*>(L->d_attn32.ptr);
+    void* dqkv = L->d_qkv.ptr;
+    float* bstats = static_cast<float*>(ctx->bwd_stats.ptr);
+    const float* st_m = static_cast<const float*>(L->stats.ptr);
+    const float* st_l = st_m + (size_t)rows * H;
+    const float* rms = static_cast<const float*>(L->rms.ptr);
+    const float* qkv = static_cast<const float*>(L->qkv32.ptr);
+    const float scale = 1.0f / std::sqrt((float)DT_HEAD_DIM);
+
+    // step 1 (OlmoAttention.cpp:198-217): dWo += d_out^T attn; d_attn = d_out Wo
+    const void *g_in = gd, *wo = L->w_o, *attn = L->attn.ptr;
+    if (bf) {
+        DT_TRY(L->d16.ensure(act * 2));
+        DT_TRY(launch_f32_to_bf16(gd, static_cast<uint16_t*>(L->d16.ptr), (int64_t)act, s));
+        g_in = L->d16.ptr;
+        wo = L->w_o16;
+    }
+    DT_TRY(gemm_rm(ctx, s, true, false, dm, dm, rows, g_in, dm, attn, dm, 1.0f, L->g_o, dm, bf));
+    DT_TRY(gemm_rm(ctx, s, false, false, rows, dm, dm, g_in, dm, wo, dm, 0.0f, d_attn, dm, bf));
+    // step 2 (:219-232): the attention core's backward from the saved m and l
+    const void* d_o = d_attn;
+    if (bf) {  // the d16 copy of d_out has been consumed by the two GEMMs above (stream order)
+        DT_TRY(launch_f32_to_bf16(d_attn, static_cast<uint16_t*>(L->d16.ptr), (int64_t)act, s));
+        d_o = L->d16.ptr;
+    }
+    const char* att = static_cast<const char*>(bf ? L->qkv16.ptr : L->att32.ptr);
+    char* dq = static_cast<char*>(dqkv);
+    FlashBwdArgs ba{att, att + dm * esz, att + 2 * dm * esz, attn, d_o, st_m, st_l, dq, dq + dm * esz,
+                    dq + 2 * dm * esz, bstats, bstats + (size_t)rows * H, B, T, H, 3 * dm, dm, 3 * dm, scale, 1};
+    DT_TRY(bf ? launch_flash_bwd_bf16(ba, s) : launch_flash_bwd_f32(ba, s));
+    // steps 3-4 (:234-244): RoPE backward and the q/k norms' backward, in place on dq | dk
+    NormRopeBwdArgs nb{dq, dq + dm * esz, qkv, qkv + dm, rms, rms + rows, L->q_norm, L->k_norm,
+                       static_cast<float*>(L->partial.ptr), ctx->rope_cos, ctx->rope_sin, rows, T, H, 3 * dm, 3 * dm};
+    DT_TRY(launch_qk_norm_rope_bwd(nb, bf, L->g_qn, L->g_kn, s));
+    // step 5 (:246-309): [dWq;dWk;dWv] += [dq|dk|dv]^T x and d_x = [dq|dk|dv] [Wq;Wk;Wv]
+    const void* xin = bf ? L->x16.ptr : L->x32.ptr;
+    const void* wqkv = bf ? static_cast<const void*>(L->w_qkv16) : static_cast<const void*>(L->w_qkv);
+    DT_TRY(gemm_rm(ctx, s, true, false, 3 * dm, dm, rows, dqkv, 3 * dm, xin, dm, 1.0f, L->g_qkv, dm, bf));
+    DT_TRY(gemm_rm(ctx, s, false, false, rows, dm, 3 * dm, dqkv, 3 * dm, wqkv, dm, 0.0f, dxd, dm, bf));
+    if (mem == DT_MEM_HOST) {
+        DT_HIP_TRY(hipMemcpyAsync(d_x, dxd, act * 4, hipMemcpyDeviceToHost, s));
+        DT_HIP_TRY(hipStreamSynchronize(s));
+    }
+    return DT_OK;
+}
+
+int dt_attn_layer_step(dt_attn_layer* L, float lr, void* stream) {
+    clear_error();
+    if (!L) return set_error(DT_ERR_INVALID_ARG, "layer is NULL");
+    if (!std::isfinite(lr)) return set_error(DT_ERR_INVALID_ARG, "lr must be finite");
+    DT_TRY(check_device_binding(L->ctx));
+    hipStream_t s = static_cast<hipStream_t>(stream);
+    DT_TRY(ensure_grads(L, s));
+    const int64_t dm = L->d_model;
+    DT_TRY(launch_sgd(L->w_qkv, L->g_qkv, lr, 3 * dm * dm, s));  // OlmoAttention.cpp:315-317
+    DT_TRY(launch_sgd(L->w_o, L->g_o, lr, dm * dm, s));          // :318
+    DT_TRY(launch_sgd(L->q_norm, L->g_qn, lr, dm, s));           // :319, RMSNorm.cpp:38-40
+    DT_TRY(launch_sgd(L->k_norm, L->g_kn, lr, dm, s));           // :320
+    L->w16_stale = true;
+    return DT_OK;
+}
+
+int dt_attn_layer_zero_grad(dt_attn_layer* L, void* stream) {
+    clear_error();
+    if (!L) return set_error(DT_ERR_INVALID_ARG, "layer is NULL");
+    DT_TRY(check_device_binding(L->ctx));
+    hipStream_t s = static_cast<hipStream_t>(stream);
+    if (!L->g_qkv) return ensure_grads(L, s);  // allocated zeroed
+    const int64_t dm = L->d_model;
+    DT_TRY(launch_fill_zero(L->g_qkv, 3 * dm * dm, s));  // OlmoAttention.cpp:323-330
+    DT_TRY(launch_fill_zero(L->g_o, dm * dm, s));
+    DT_TRY(launch_fill_zero(L->g_qn, dm, s));
+    DT_TRY(launch_fill_zero(L->g_kn, dm, s));
+    return DT_OK;
+}
+
+// copies the six parameter arrays (grads == 0) or their gradients (grads == 1) out of the layer
+static int copy_params(dt_attn_layer* L, int grads, float* wq, float* wk, float* wv, float* wo, float* qn, float* kn,
+                       int mem, void* stream) {
+    clear_error();
+    if (!L) return set_error(DT_ERR_INVALID_ARG, "layer is NULL");
+    if (mem != DT_MEM_DEVICE && mem != DT_MEM_HOST) return set_error(DT_ERR_INVALID_ARG, "unknown mem %d", mem);
+    DT_TRY(check_device_binding(L->ctx));
+    hipStream_t s = static_cast<hipStream_t>(stream);
+    if (grads) DT_TRY(ensure_grads(L, s));
+    const size_t dm = L->d_model, w2 = dm * dm * 4;
+    const float* src_qkv = grads ? L->g_qkv : L->w_qkv;
+    const float* srcs[6] = {src_qkv, src_qkv + dm * dm, src_qkv + 2 * dm * dm, grads ? L->g_o : L->w_o,
+                            grads ? L->g_qn : L->q_norm, grads ? L->g_kn : L->k_norm};
+    float* dsts[6] = {wq, wk, wv, wo, qn, kn};
+    const size_t bytes[6] = {w2, w2, w2, w2, dm * 4, dm * 4};
+    const hipMemcpyKind kind = mem == DT_MEM_HOST ? hipMemcpyDeviceToHost : hipMemcpyDeviceToDevice;
+    for (int i = 0; i < 6; ++i)
+        if (dsts[i]) DT_HIP_TRY(hipMemcpyAsync(dsts[i], srcs[i], bytes[i], kind, s));
+    if (mem == DT_MEM_HOST) DT_HIP_TRY(hipStreamSynchronize(s));
+    return DT_OK;
+}
+
+int dt_attn_layer_get_weights(dt_attn_layer* L, float* wq, float* wk, float* wv, float* wo, float* q_norm_w,
+                              float* k_norm_w, int mem, void* stream) {
+    return copy_params(L, 0, wq, wk, wv, wo, q_norm_w, k_norm_w, mem, stream);
+}
+
+int dt_attn_layer_get_grads(dt_attn_layer* L, float* d_wq, float* d_wk, float* d_wv, float* d_wo, float* d_q_norm_w,
+                            float* d_k_norm_w, int mem, void* stream) {
+    return copy_params(L, 1, d_wq, d_wk, d_wv, d_wo, d_q_norm_w, d_k_norm_w, mem, stream);
 }
 
 }  // extern "C"

@@ -103,6 +103,28 @@ struct NormRopeArgs {
     float eps;
 };
 int launch_qk_norm_rope(const NormRopeArgs& a, int out_bf16, hipStream_t stream);
+
+// Backward of the fused q/k RMSNorm + RoPE (OlmoAttention.cpp:234-244): dq/dk rows are rewritten in place
+// from d(rope output) to d(pre-norm projection); the norm-weight gradients are accumulated (+=).
+struct NormRopeBwdArgs {
+    void* dq;  // [rows] rows of stride ld_d, fp32 or bf16 (in place)
+    void* dk;
+    const float* q_x;  // saved pre-norm projections, stride ld_x
+    const float* k_x;
+    const float* q_rms;  // saved rms, [rows]
+    const float* k_rms;
+    const float* q_w;
+    const float* k_w;
+    float* partial;  // workspace [2][norm_rope_bwd_blocks(rows)][H*128]
+    const float* rope_cos;
+    const float* rope_sin;
+    int rows, T, H;
+    int ld_d, ld_x;
+};
+int norm_rope_bwd_blocks(int rows);
+int launch_qk_norm_rope_bwd(const NormRopeBwdArgs& a, int bf16, float* grad_q_w, float* grad_k_w, hipStream_t stream);
+int launch_sgd(float* w, const float* g, float lr, int64_t n, hipStream_t stream);  // w -= lr * g
+int launch_fill_zero(float* p, int64_t n, hipStream_t stream);
 int launch_f32_to_bf16(const float* in, uint16_t* out, int64_t n, hipStream_t stream);
 
 }  // namespace dt

@@ -102,8 +102,16 @@ int dt_flash_attn_fwd(dt_ctx* ctx, const void* q, const void* k, const void* v, 
                       int mem, void* stream);
 
 /*
- * Flash attention backward (FlashAttention.h:33-43). Not implemented on the
- * GPU: always returns DT_ERR_NOT_IMPLEMENTED so that callers fail loudly.
+ * Flash attention backward (replaces flash_attention_backward,
+ * FlashAttention.h:33-43 / FlashAttention.cpp:185-359).
+ *   d_o, o, q, k, v : [B, T, H, D] (fp32 in DT_FP32_EXACT, bf16 bits in DT_BF16):
+ *                     the output gradient, the forward's output and its inputs.
+ *   m, l            : the forward's [B, T, H] fp32 statistics (dt_flash_attn_fwd).
+ *   d_q, d_k, d_v   : [B, T, H, D] results, in the same element type.
+ * P = exp(scale q.k - m) / l and dS = P (dP - rowsum(O * dO)) scale, as the
+ * reference; every gradient row is written by one workgroup (no atomics), so
+ * the results are deterministic. Full sequences only (no seq_lens).
+ * Requires D == 128, 1 <= T <= 8192. Uses a context workspace of 8*B*T*H bytes.
  */
 int dt_flash_attn_bwd(dt_ctx* ctx, const void* d_o, const void* o, const float* m, const float* l, const void* q,
                       const void* k, const void* v, void* d_q, void* d_k, void* d_v, int B, int T, int H, int D,
@@ -147,15 +155,40 @@ int dt_attn_layer_destroy(dt_attn_layer* layer);
  * out [B, T, d_model] fp32. dtype selects the attention-core mode and the
  * projection GEMM precision (DT_FP32_EXACT: fp32 GEMMs; DT_BF16: bf16 GEMM
  * inputs with fp32 accumulation). seq_lens as for dt_flash_attn_fwd.
- * Forward-only: the reference's saved activations for backward
- * (OlmoAttention.h:28-38) are not kept.
+ * save_for_backward = 1 keeps what the reference saves for backward
+ * (OlmoAttention.h:28-38: the input, the pre-norm projections and rms, the
+ * rotated q/k, v, the attention output and its m/l) in layer-owned device
+ * buffers; it requires seq_lens == NULL. With 0 nothing is kept (prefill).
  */
 int dt_attn_layer_fwd(dt_attn_layer* layer, const float* x, float* out, int B, int T, const int32_t* seq_lens,
-                      int dtype, int mem, void* stream);
+                      int dtype, int mem, int save_for_backward, void* stream);
 
-/* OlmoAttention::backward / step / zero_grad (OlmoAttention.cpp:193-330):
- * not implemented on the GPU; always DT_ERR_NOT_IMPLEMENTED. */
+/*
+ * OlmoAttention::backward (OlmoAttention.cpp:193-312): d_out [B, T, d_model]
+ * fp32 -> d_x [B, T, d_model] fp32, for the last forward with
+ * save_for_backward = 1 (same B and T; its dtype is used). Accumulates (+=)
+ * the gradients of Wq, Wk, Wv, Wo and the two norm weights in the layer, as
+ * the reference's param<2>::grad (beta = 1 at OlmoAttention.cpp:207-211,
+ * 257-277; RMSNorm.cpp:31).
+ */
 int dt_attn_layer_bwd(dt_attn_layer* layer, const float* d_out, float* d_x, int B, int T, int mem, void* stream);
+
+/* OlmoAttention::step (OlmoAttention.cpp:314-321): w -= lr * grad for all six parameters. */
+int dt_attn_layer_step(dt_attn_layer* layer, float lr, void* stream);
+
+/* OlmoAttention::zero_grad (OlmoAttention.cpp:323-330). */
+int dt_attn_layer_zero_grad(dt_attn_layer* layer, void* stream);
+
+/*
+ * Copies of the layer's parameters / accumulated gradients ([d_model][d_model]
+ * for the four projections, [d_model] for the norm weights; any pointer may be
+ * NULL to skip it). No counterpart function in the reference, where they are
+ * the param<2> members w and grad (param.h:5-15).
+ */
+int dt_attn_layer_get_weights(dt_attn_layer* layer, float* wq, float* wk, float* wv, float* wo, float* q_norm_w,
+                              float* k_norm_w, int mem, void* stream);
+int dt_attn_layer_get_grads(dt_attn_layer* layer, float* d_wq, float* d_wk, float* d_wv, float* d_wo,
+                            float* d_q_norm_w, float* d_k_norm_w, int mem, void* stream);
 
 #ifdef __cplusplus
 }

@@ -2,8 +2,9 @@
 // the HIP path. The constructor reads the same per-layer .npy files
 // (OlmoAttention.cpp:39-53) and keeps the weights on the GPU; forward takes and
 // returns host tensors [batch, seq, d_model] like the reference
-// (OlmoAttention.cpp:56-108), computing in fp32 exact mode. backward, step and
-// zero_grad throw: the GPU path is forward-only.
+// (OlmoAttention.cpp:56-108), computing in fp32 exact mode. As in the
+// reference, forward keeps what backward needs (OlmoAttention.h:28-38), here in
+// device memory; backward, step and zero_grad follow OlmoAttention.cpp:193-330.
 #pragma once
 
 #include <string>
@@ -28,18 +29,26 @@ public:
         const int B = (int)input.shape(0), T = (int)input.shape(1);
         auto out = DT_TENSOR_TEMPLATE<float, 3>::from_shape({input.shape(0), input.shape(1), input.shape(2)});
         dt::throw_if_error(dt_attn_layer_fwd(m_layer, input.data(), out.data(), B, T, nullptr, DT_FP32_EXACT,
-                                             DT_MEM_HOST, nullptr));
+                                             DT_MEM_HOST, 1, nullptr));
         return out;
     }
 
     DT_TENSOR_TEMPLATE<float, 3> backward(const DT_TENSOR_TEMPLATE<float, 3>& d_output) {
-        DT_TENSOR_TEMPLATE<float, 3> d_input;
+        auto d_input = DT_TENSOR_TEMPLATE<float, 3>::from_shape({d_output.shape(0), d_output.shape(1), d_output.shape(2)});
         dt::throw_if_error(dt_attn_layer_bwd(m_layer, d_output.data(), d_input.data(), (int)d_output.shape(0),
                                              (int)d_output.shape(1), DT_MEM_HOST, nullptr));
         return d_input;
     }
-    void step(float) { throw std::runtime_error("OlmoAttention::step: the GPU path is forward-only"); }
-    void zero_grad() { throw std::runtime_error("OlmoAttention::zero_grad: the GPU path is forward-only"); }
+    void step(float lr) {
+        dt::throw_if_error(dt_attn_layer_step(m_layer, lr, nullptr));
+        dt::throw_if_error(dt_attn_layer_get_weights(m_layer, nullptr, nullptr, nullptr, nullptr, nullptr, nullptr,
+                                                     DT_MEM_HOST, nullptr));  // synchronises, like the reference
+    }
+    void zero_grad() {
+        dt::throw_if_error(dt_attn_layer_zero_grad(m_layer, nullptr));
+        dt::throw_if_error(dt_attn_layer_get_grads(m_layer, nullptr, nullptr, nullptr, nullptr, nullptr, nullptr,
+                                                   DT_MEM_HOST, nullptr));
+    }
 
 private:
     dt_attn_layer* m_layer = nullptr;

@@ -3,7 +3,8 @@
 //
 //   dropin_check cpu                       argument errors throw, no GPU needed
 //   dropin_check flash <dir> B T H         reads q/k/v.f32 from dir, writes o/m/l.f32
-//   dropin_check layer <folder> <idx> <dir> B T   reads x.f32, writes out.f32
+//   dropin_check bwd <dir> B T H           reads g/o/q/k/v.f32 and m/l.f32, writes dq/dk/dv.f32
+//   dropin_check layer <folder> <idx> <dir> B T   reads x.f32 and g.f32, writes out.f32 and dx.f32
 #include <cmath>
 #include <cstdio>
 #include <cstdlib>
@@ -53,7 +54,8 @@ int main(int argc, char** argv) {
         ok &= throws([&] { flash_attention_forward(a, b, a, scale); });
         ok &= throws([&] { flash_attention_forward(c, c, c, scale); });
         ok &= throws([&] { flash_attention_forward(big, big, big, scale, true); });
-        ok &= throws([&] { flash_attention_backward(a, a, m3, m3, a, a, a, scale); });
+        ok &= throws([&] { flash_attention_backward(a, b, m3, m3, a, a, a, scale); });
+        ok &= throws([&] { flash_attention_backward(c, c, m3, m3, c, c, c, scale); });
         ok &= throws([&] { OlmoAttention("/nonexistent-folder", 0); });
         a(0, 3, 1, 5) = 2.5f;
         ok &= a.data()[(3 * 2 + 1) * 128 + 5] == 2.5f;
@@ -84,9 +86,35 @@ int main(int argc, char** argv) {
         read_raw(dir + "/x.f32", x);
         auto out = attn.forward(x);
         write_raw(dir + "/out.f32", out);
-        bool ok = throws([&] { attn.backward(out); });
+        auto g = x;
+        read_raw(dir + "/g.f32", g);
+        attn.zero_grad();
+        auto dx = attn.backward(g);
+        write_raw(dir + "/dx.f32", dx);
+        bool ok = throws([&] { attn.backward(dt::tensor<float, 3>::from_shape({B, T + 1, 2048})); });
         std::cout << (ok ? "OK" : "FAIL") << "\n";
         return ok ? 0 : 1;
+    }
+    if (mode == "bwd" && argc == 6) {
+        const std::string dir = argv[2];
+        const size_t B = std::atoi(argv[3]), T = std::atoi(argv[4]), H = std::atoi(argv[5]);
+        auto G = dt::tensor<float, 4>::from_shape({B, T, H, 128});
+        auto O = G, Q = G, K = G, V = G;
+        auto m = dt::tensor<float, 3>::from_shape({B, T, H});
+        auto l = m;
+        read_raw(dir + "/g.f32", G);
+        read_raw(dir + "/o.f32", O);
+        read_raw(dir + "/q.f32", Q);
+        read_raw(dir + "/k.f32", K);
+        read_raw(dir + "/v.f32", V);
+        read_raw(dir + "/m.f32", m);
+        read_raw(dir + "/l.f32", l);
+        FlashAttentionGradients r = flash_attention_backward(G, O, m, l, Q, K, V, scale);
+        write_raw(dir + "/dq.f32", r.d_Q);
+        write_raw(dir + "/dk.f32", r.d_K);
+        write_raw(dir + "/dv.f32", r.d_V);
+        std::cout << "OK\n";
+        return 0;
     }
     return 2;
 }

@@ -34,7 +34,7 @@ def test_every_declared_symbol_is_exported_and_bound():
     for n in names:
         assert hasattr(lib, n), f"{n} declared in the header but not exported"
     assert sorted(C.SIGNATURES) == names, "ctypes signature table and header disagree"
-    assert lib.dt_version() == 1
+    assert lib.dt_version() == 2
 
 
 def flash(**kw):
@@ -73,12 +73,26 @@ def test_flash_seq_lens_validation():
     assert flash(B=300, seq_lens=ctypes.cast(big, ctypes.c_void_p)) == C.DT_ERR_UNSUPPORTED
 
 
-def test_backward_entry_points_fail_loudly():
+def test_flash_bwd_validation():
+    """dt_flash_attn_bwd rejects bad arguments before any HIP call (no device is touched here)."""
     lib = C.lib()
-    assert lib.dt_flash_attn_bwd(None, None, None, None, None, None, None, None, None, None, None, 1, 1, 1, 128,
-                                 0.1, 1, 0, 0, None) == C.DT_ERR_NOT_IMPLEMENTED
-    assert "not implemented" in last_error()
-    assert lib.dt_attn_layer_bwd(None, None, None, 1, 1, 0, None) == C.DT_ERR_NOT_IMPLEMENTED
+    args = [None] + [FAKE] * 10 + [1, 64, 2, 128, 0.1, 1, C.DT_BF16, C.DT_MEM_DEVICE, None]
+    assert lib.dt_flash_attn_bwd(*args) == C.DT_ERR_INVALID_ARG and "ctx is NULL" in last_error()
+    bad = list(args)
+    bad[3] = None  # l
+    assert lib.dt_flash_attn_bwd(*bad) == C.DT_ERR_INVALID_ARG and "non-NULL" in last_error()
+    bad = list(args)
+    bad[14] = 96
+    assert lib.dt_flash_attn_bwd(*bad) == C.DT_ERR_UNSUPPORTED
+    bad = list(args)
+    bad[12] = 9000
+    assert lib.dt_flash_attn_bwd(*bad) == C.DT_ERR_INVALID_ARG
+    bad = list(args)
+    bad[17] = 7
+    assert lib.dt_flash_attn_bwd(*bad) == C.DT_ERR_INVALID_ARG and "dtype" in last_error()
+    bad = list(args)
+    bad[15] = -1.0
+    assert lib.dt_flash_attn_bwd(*bad) == C.DT_ERR_INVALID_ARG and "scale" in last_error()
 
 
 def test_norm_rope_and_layer_validation():
@@ -95,10 +109,23 @@ def test_norm_rope_and_layer_validation():
     bad = list(args)
     bad[10] = 9000
     assert lib.dt_qk_norm_rope_fwd(*bad) == C.DT_ERR_INVALID_ARG
-    assert lib.dt_attn_layer_fwd(None, FAKE, FAKE, 1, 16, None, 0, 0, None) == C.DT_ERR_INVALID_ARG
+    assert lib.dt_attn_layer_fwd(None, FAKE, FAKE, 1, 16, None, 0, 0, 0, None) == C.DT_ERR_INVALID_ARG
     assert "layer is NULL" in last_error()
-    assert lib.dt_attn_layer_fwd(None, FAKE, FAKE, 1, 9000, None, 0, 0, None) == C.DT_ERR_INVALID_ARG
-    assert lib.dt_attn_layer_fwd(None, FAKE, FAKE, 1, 16, None, 3, 0, None) == C.DT_ERR_INVALID_ARG
+    assert lib.dt_attn_layer_fwd(None, FAKE, FAKE, 1, 9000, None, 0, 0, 0, None) == C.DT_ERR_INVALID_ARG
+    assert lib.dt_attn_layer_fwd(None, FAKE, FAKE, 1, 16, None, 3, 0, 0, None) == C.DT_ERR_INVALID_ARG
+    assert lib.dt_attn_layer_fwd(None, FAKE, FAKE, 1, 16, None, 0, 0, 2, None) == C.DT_ERR_INVALID_ARG
+    lens = (ctypes.c_int32 * 1)(16)
+    assert lib.dt_attn_layer_fwd(None, FAKE, FAKE, 1, 16, ctypes.cast(lens, ctypes.c_void_p), 0, 0, 1,
+                                 None) == C.DT_ERR_UNSUPPORTED and "seq_lens" in last_error()
+    # training entry points: argument checks before any device work
+    assert lib.dt_attn_layer_bwd(None, FAKE, FAKE, 1, 16, 0, None) == C.DT_ERR_INVALID_ARG
+    assert "layer is NULL" in last_error()
+    assert lib.dt_attn_layer_bwd(None, None, FAKE, 1, 16, 0, None) == C.DT_ERR_INVALID_ARG
+    assert lib.dt_attn_layer_bwd(None, FAKE, FAKE, 1, 16, 9, None) == C.DT_ERR_INVALID_ARG
+    assert lib.dt_attn_layer_step(None, 0.1, None) == C.DT_ERR_INVALID_ARG
+    assert lib.dt_attn_layer_zero_grad(None, None) == C.DT_ERR_INVALID_ARG
+    assert lib.dt_attn_layer_get_grads(None, None, None, None, None, None, None, 1, None) == C.DT_ERR_INVALID_ARG
+    assert lib.dt_attn_layer_get_weights(None, None, None, None, None, None, None, 1, None) == C.DT_ERR_INVALID_ARG
     h = ctypes.c_void_p()
     assert lib.dt_attn_layer_create(None, FAKE, FAKE, FAKE, FAKE, FAKE, FAKE, 2000, 16, 0,
                                     ctypes.byref(h)) == C.DT_ERR_UNSUPPORTED
