@@ -2,15 +2,29 @@
 """Benchmark of the causal-attention hot path on one MI355X.
 
     python bench.py [--gpus 1] [--steps K] [--warmup W] [--T 4096] [--mode bf16|fp32]
+                    [--workload flash_fwd|flash_bwd|ragged_fwd|layer_fwd|layer_train]
 
-Workload (one "step" = one dt_flash_attn_fwd launch over one batch): causal
-attention at the OLMo-2-1B head shape, B=1, T=4096, H=16, D=128, bf16 Q/K/V/O
-with fp32 accumulation, Q/K/V ~ N(0,1) from seeds 1001-1003, already resident
-in HBM. Prints one JSON line: causal-attention TFLOP/s over the algorithmic
-work 2*B*H*D*T*(T+1) (unmasked pairs only, QK^T and PV, 2 flops per MAC), the
-prefill tokens/s of the attention core, the roofline fraction of the bf16
-MFMA peak, and the CPU baseline: the oracle's restatement of the reference's
-flash_attention_forward (FlashAttention.cpp:24-182) timed on this host.
+Default workload (one "step" = one dt_flash_attn_fwd launch over one batch):
+causal attention at the OLMo-2-1B head shape, B=1, T=4096, H=16, D=128, bf16
+Q/K/V/O with fp32 accumulation, Q/K/V ~ N(0,1) from seeds 1001-1003, already
+resident in HBM. Prints one JSON line: causal-attention TFLOP/s over the
+algorithmic work 2*B*H*D*T*(T+1) (unmasked pairs only, QK^T and PV, 2 flops
+per MAC), the prefill tokens/s of the attention core, the roofline fraction of
+the MFMA peak, and the CPU baseline: the oracle's restatement of the
+reference's flash_attention_forward (FlashAttention.cpp:24-182) timed on this
+host.
+
+Other workloads (each prints one line of the same shape):
+  flash_bwd    one dt_flash_attn_bwd (FlashAttention.cpp:185-359) at the same
+               shape; work 5*B*H*D*T*(T+1) (S, dP, dV, dQ, dK over unmasked pairs)
+  ragged_fwd   a right-padded batch B=8, lengths U[64, 2048] (seed 4001), H=16;
+               work sum_b 2*H*D*L_b*(L_b+1)
+  layer_fwd    OlmoAttention::forward (OlmoAttention.cpp:56-108), x [1, T, 2048]
+               (seed 2001, T=512 by default), seeded weights; work
+               8*T*d^2 (q/k/v/o projections) + 2*H*D*T*(T+1)
+  layer_train  forward with saved state + OlmoAttention::backward + step at the
+               same shape; work 3x the projections' and 3.5x the attention
+               core's forward work
 """
 
 from __future__ import annotations
@@ -114,6 +128,8 @@ def main() -> int:
     ap.add_argument("--warmup", type=int, default=500)
     ap.add_argument("--T", type=int, default=4096)
     ap.add_argument("--mode", choices=["bf16", "fp32"], default="bf16")
+    ap.add_argument("--workload", choices=["flash_fwd", "flash_bwd", "ragged_fwd", "layer_fwd", "layer_train"],
+                    default="flash_fwd")
     ap.add_argument("--cpu-budget", type=float, default=10.0, help="seconds of CPU-baseline timing (0 = skip)")
     ap.add_argument("--copy-mib", type=int, default=0,
                     help="instead of attention, time a plain copy kernel over this many MiB (counter calibration)")
@@ -125,7 +141,6 @@ def main() -> int:
               file=sys.stderr)
         return 2
 
-    import numpy as np
     import torch
 
     if args.copy_mib > 0:
@@ -134,57 +149,32 @@ def main() -> int:
     import dirktensor_amd as dt
     from dirktensor_amd import _capi, synth
 
-    B, T, H, D = 1, args.T, 16, 128
     dev = torch.device("cuda:0")
-    tdt = torch.bfloat16 if args.mode == "bf16" else torch.float32
-    dtype = _capi.DT_BF16 if args.mode == "bf16" else _capi.DT_FP32_EXACT
-    Qn, Kn, Vn = synth.qkv(B, T, H)
-    q, k, v = (torch.from_numpy(x).to(dev).to(tdt) for x in (Qn, Kn, Vn))
-    o = torch.empty_like(q)
-    m = torch.empty((B, T, H), dtype=torch.float32, device=dev)
-    l = torch.empty((B, T, H), dtype=torch.float32, device=dev)
-    ctx = dt.default_context(0)
     stream = torch.cuda.current_stream(dev)
-    sp = stream.cuda_stream
-    fn = _capi.lib().dt_flash_attn_fwd
-    args_c = (ctx.handle, q.data_ptr(), k.data_ptr(), v.data_ptr(), o.data_ptr(), m.data_ptr(), l.data_ptr(),
-              B, T, H, D, SCALE, 1, None, dtype, _capi.DT_MEM_DEVICE, sp)
-
-    def step():
-        rc = fn(*args_c)
-        if rc != 0:
-            _capi.check(rc)
+    ctx = dt.default_context(0)
+    wl = WORKLOADS[args.workload](args, dev, stream, ctx)
 
     for _ in range(args.warmup):
-        step()
+        wl["step"]()
     torch.cuda.synchronize()
-    # events recorded on the stream the kernel is launched on (torch's current stream)
+    # events recorded on the stream the kernels are launched on (torch's current stream)
     ev0 = torch.cuda.Event(enable_timing=True)
     ev1 = torch.cuda.Event(enable_timing=True)
     wall0 = time.perf_counter()
     ev0.record(stream)
     for _ in range(args.steps):
-        step()
+        wl["step"]()
     ev1.record(stream)
     torch.cuda.synchronize()
     wall = time.perf_counter() - wall0
     ms = ev0.elapsed_time(ev1) / args.steps
 
-    flops = algorithmic_flops(B, T, H, D)
-    tflops = flops / (ms * 1e-3) / 1e12
+    tflops = wl["flops"] / (ms * 1e-3) / 1e12
     peak = PEAK_TFLOPS[args.mode]
-
-    # parity of the measured output on two heads against the oracle (fp32 inputs)
-    import oracle
-
-    O_ref, _, _ = oracle.flash_attention_forward(Qn[:, :, :2], Kn[:, :, :2], Vn[:, :, :2], SCALE, True)
-    O_gpu = o[:, :, :2].float().cpu().numpy()
-    parity = float(np.max(np.abs(O_gpu - O_ref)) / np.max(np.abs(O_ref)))
-
-    cpu = cpu_baseline(T, H, D, args.cpu_budget) if args.cpu_budget > 0 else None
-
+    parity = wl["parity"]()
+    cpu = wl["cpu"](args.cpu_budget) if args.cpu_budget > 0 else None
     line = {
-        "metric": "causal attn TFLOP/s + prefill tok/s, OLMo-2-1B shape T=4096 (% of MFMA peak)",
+        "metric": wl["metric"],
         "value": round(tflops, 3),
         "unit": "TFLOP/s",
         "n_gpus": 1,
@@ -195,19 +185,276 @@ def main() -> int:
         "scaling": "weak",
         "vs_baseline": None,
         "dtype": args.mode,
-        "data": "synthetic (Q/K/V ~ N(0,1), seeds 1001-1003)",
-        "config": {"workload": f"causal flash attention forward, B={B} T={T} H={H} D={D}, {args.mode}",
-                   "B": B, "T": T, "H": H, "D": D, "causal": True},
-        "prefill_tok_per_s": round(B * T / (ms * 1e-3), 1),
+        "data": wl["data"],
+        "config": wl["config"],
+        "tok_per_s": round(wl["tokens"] / (ms * 1e-3), 1),
         "pct_of_peak": round(100.0 * tflops / peak, 2),
-        "parity_rel_err_2heads": parity,
+        "parity_rel_err": parity,
         "wall_s_timed_region": round(wall, 4),
         "roofline": {"bound": "mfma", "achieved": round(tflops, 3), "peak": peak, "unit": "TFLOP/s",
-                     "frac": round(tflops / peak, 4), "traffic": load_traffic(args.mode, T)},
+                     "frac": round(tflops / peak, 4), "traffic": wl.get("traffic")},
         "cpu_baseline": cpu,
     }
+    if args.workload == "flash_fwd":
+        line["prefill_tok_per_s"] = line["tok_per_s"]
     print(json.dumps(line), flush=True)
     return 0
+
+
+def _threads(limit: int) -> tuple:
+    try:
+        cores = len(os.sched_getaffinity(0))
+    except AttributeError:  # pragma: no cover
+        cores = os.cpu_count() or 1
+    return max(1, min(limit, cores, 16)), cores
+
+
+def _time_cpu(fn, budget_s: float):
+    import numpy as np
+
+    times = []
+    t_start = time.perf_counter()
+    while len(times) < 2 or (time.perf_counter() - t_start < budget_s and len(times) < 50):
+        t0 = time.perf_counter()
+        fn()
+        times.append(time.perf_counter() - t0)
+    return float(np.median(times)), len(times)
+
+
+def _rel(a, b) -> float:
+    import numpy as np
+
+    a = np.asarray(a, np.float64)
+    b = np.asarray(b, np.float64)
+    return float(np.max(np.abs(a - b)) / max(np.max(np.abs(b)), 1e-30))
+
+
+def wl_flash_fwd(args, dev, stream, ctx):
+    import torch
+
+    from dirktensor_amd import _capi, synth
+
+    B, T, H, D = 1, args.T, 16, 128
+    tdt = torch.bfloat16 if args.mode == "bf16" else torch.float32
+    dtype = _capi.DT_BF16 if args.mode == "bf16" else _capi.DT_FP32_EXACT
+    Qn, Kn, Vn = synth.qkv(B, T, H)
+    q, k, v = (torch.from_numpy(x).to(dev).to(tdt) for x in (Qn, Kn, Vn))
+    o = torch.empty_like(q)
+    m = torch.empty((B, T, H), dtype=torch.float32, device=dev)
+    l = torch.empty((B, T, H), dtype=torch.float32, device=dev)
+    fn = _capi.lib().dt_flash_attn_fwd
+    args_c = (ctx.handle, q.data_ptr(), k.data_ptr(), v.data_ptr(), o.data_ptr(), m.data_ptr(), l.data_ptr(),
+              B, T, H, D, SCALE, 1, None, dtype, _capi.DT_MEM_DEVICE, stream.cuda_stream)
+
+    def step():
+        rc = fn(*args_c)
+        if rc != 0:
+            _capi.check(rc)
+
+    def parity():  # the measured output on two heads against the oracle (fp32 inputs)
+        import oracle
+
+        O_ref, _, _ = oracle.flash_attention_forward(Qn[:, :, :2], Kn[:, :, :2], Vn[:, :, :2], SCALE, True)
+        return _rel(o[:, :, :2].float().cpu().numpy(), O_ref)
+
+    return dict(step=step, flops=algorithmic_flops(B, T, H, D), tokens=B * T, parity=parity,
+                cpu=lambda budget: cpu_baseline(T, H, D, budget),
+                metric="causal attn TFLOP/s + prefill tok/s, OLMo-2-1B shape T=4096 (% of MFMA peak)",
+                data="synthetic (Q/K/V ~ N(0,1), seeds 1001-1003)",
+                config={"workload": f"causal flash attention forward, B={B} T={T} H={H} D={D}, {args.mode}",
+                        "B": B, "T": T, "H": H, "D": D, "causal": True},
+                traffic=load_traffic(args.mode, T))
+
+
+def wl_flash_bwd(args, dev, stream, ctx):
+    import numpy as np
+    import torch
+
+    import oracle
+    from dirktensor_amd import _capi, synth
+
+    B, T, H, D = 1, args.T, 16, 128
+    tdt = torch.bfloat16 if args.mode == "bf16" else torch.float32
+    dtype = _capi.DT_BF16 if args.mode == "bf16" else _capi.DT_FP32_EXACT
+    Qn, Kn, Vn = synth.qkv(B, T, H)
+    Gn = synth.normal(1004, Qn.shape)
+    q, k, v, g = (torch.from_numpy(x).to(dev).to(tdt) for x in (Qn, Kn, Vn, Gn))
+    o = torch.empty_like(q)
+    m = torch.empty((B, T, H), dtype=torch.float32, device=dev)
+    l = torch.empty((B, T, H), dtype=torch.float32, device=dev)
+    _capi.call("dt_flash_attn_fwd", ctx.handle, q.data_ptr(), k.data_ptr(), v.data_ptr(), o.data_ptr(),
+               m.data_ptr(), l.data_ptr(), B, T, H, D, SCALE, 1, None, dtype, _capi.DT_MEM_DEVICE,
+               stream.cuda_stream)
+    dq, dk, dv = (torch.empty_like(q) for _ in range(3))
+    fn = _capi.lib().dt_flash_attn_bwd
+    args_c = (ctx.handle, g.data_ptr(), o.data_ptr(), m.data_ptr(), l.data_ptr(), q.data_ptr(), k.data_ptr(),
+              v.data_ptr(), dq.data_ptr(), dk.data_ptr(), dv.data_ptr(), B, T, H, D, SCALE, 1, dtype,
+              _capi.DT_MEM_DEVICE, stream.cuda_stream)
+
+    def step():
+        rc = fn(*args_c)
+        if rc != 0:
+            _capi.check(rc)
+
+    def parity():  # two heads against the oracle's backward from the same (device) forward statistics
+        hs = slice(0, 2)
+        to = lambda t: t[:, :, hs].float().cpu().numpy()
+        ref = oracle.flash_attention_backward(to(g), to(o), to(m), to(l), to(q), to(k), to(v), SCALE, True)
+        return max(_rel(to(x), r) for x, r in zip((dq, dk, dv), ref))
+
+    def cpu(budget):
+        O, mm, ll = oracle.flash_attention_forward(Qn, Kn, Vn, SCALE, True)
+        threads, cores = _threads(H)
+        med, n = _time_cpu(lambda: oracle.flash_attention_backward(Gn, O, mm, ll, Qn, Kn, Vn, SCALE, True,
+                                                                   nthreads=threads), budget)
+        return {"value": 2.5 * algorithmic_flops(B, T, H, D) / med / 1e12, "unit": "TFLOP/s", "cores": threads,
+                "kind": "port", "sample": f"oracle flash_attention_backward fp32, B=1 T={T} H={H} D={D} causal, "
+                f"full workload x {n} runs (median {med * 1e3:.1f} ms), {threads} threads of {cores} usable"}
+
+    return dict(step=step, flops=5 * B * H * D * T * (T + 1), tokens=B * T, parity=parity, cpu=cpu,
+                metric=f"causal attn backward TFLOP/s, OLMo-2-1B shape T={T} (% of MFMA peak)",
+                data="synthetic (Q/K/V ~ N(0,1) seeds 1001-1003, dO ~ N(0,1) seed 1004)",
+                config={"workload": f"causal flash attention backward, B={B} T={T} H={H} D={D}, {args.mode}",
+                        "B": B, "T": T, "H": H, "D": D, "causal": True})
+
+
+def wl_ragged_fwd(args, dev, stream, ctx):
+    import numpy as np
+    import torch
+
+    import oracle
+    from dirktensor_amd import _capi, synth
+
+    lens = synth.ragged_lengths()
+    B, H, D = len(lens), 16, 128
+    T = int(lens.max())
+    tdt = torch.bfloat16 if args.mode == "bf16" else torch.float32
+    dtype = _capi.DT_BF16 if args.mode == "bf16" else _capi.DT_FP32_EXACT
+    Qn, Kn, Vn = synth.qkv(B, T, H)
+    q, k, v = (torch.from_numpy(x).to(dev).to(tdt) for x in (Qn, Kn, Vn))
+    o = torch.empty_like(q)
+    m = torch.empty((B, T, H), dtype=torch.float32, device=dev)
+    l = torch.empty((B, T, H), dtype=torch.float32, device=dev)
+    lens_c = np.ascontiguousarray(lens, dtype=np.int32)
+    fn = _capi.lib().dt_flash_attn_fwd
+    args_c = (ctx.handle, q.data_ptr(), k.data_ptr(), v.data_ptr(), o.data_ptr(), m.data_ptr(), l.data_ptr(),
+              B, T, H, D, SCALE, 1, lens_c.ctypes.data, dtype, _capi.DT_MEM_DEVICE, stream.cuda_stream)
+
+    def step():
+        rc = fn(*args_c)
+        if rc != 0:
+            _capi.check(rc)
+
+    flops = sum(2 * H * D * int(L) * (int(L) + 1) for L in lens)
+
+    def parity():  # the shortest and the longest sequence, two heads each
+        err = 0.0
+        for b in (int(np.argmin(lens)), int(np.argmax(lens))):
+            L = int(lens[b])
+            O_ref, _, _ = oracle.flash_attention_forward(Qn[b:b + 1, :L, :2], Kn[b:b + 1, :L, :2],
+                                                         Vn[b:b + 1, :L, :2], SCALE, True)
+            err = max(err, _rel(o[b:b + 1, :L, :2].float().cpu().numpy(), O_ref))
+        return err
+
+    def cpu(budget):
+        threads, cores = _threads(H)
+        med, n = _time_cpu(lambda: oracle.flash_attention_ragged(Qn, Kn, Vn, lens, SCALE, nthreads=threads), budget)
+        return {"value": flops / med / 1e12, "unit": "TFLOP/s", "cores": threads, "kind": "port",
+                "sample": f"oracle flash_attention_forward per sequence, B={B} ragged lengths {int(lens.min())}.."
+                f"{T} (seed 4001), x {n} runs (median {med * 1e3:.1f} ms), {threads} threads of {cores} usable"}
+
+    return dict(step=step, flops=flops, tokens=int(lens.sum()), parity=parity, cpu=cpu,
+                metric="ragged causal attn TFLOP/s, B=8 lengths U[64,2048] (% of MFMA peak)",
+                data="synthetic (Q/K/V ~ N(0,1) seeds 1001-1003, lengths seed 4001)",
+                config={"workload": f"causal flash attention forward, right-padded batch B={B} T={T} H={H} "
+                        f"D={D}, {args.mode}", "B": B, "T": T, "H": H, "D": D, "lengths": [int(x) for x in lens]})
+
+
+def _layer_setup(args, dev):
+    import torch
+
+    from dirktensor_amd import OlmoAttention, synth
+
+    T = args.T if args.T != 4096 else 512  # the layer workload is quoted at T = 512
+    w = synth.attention_layer_weights()
+    layer = OlmoAttention.from_weights(w["wq"], w["wk"], w["wv"], w["wo"], w["q_norm"], w["k_norm"])
+    x = synth.layer_input(1, T)
+    xt = torch.from_numpy(x).to(dev)
+    return T, w, layer, x, xt
+
+
+def wl_layer_fwd(args, dev, stream, ctx):
+    import oracle
+
+    T, w, layer, x, xt = _layer_setup(args, dev)
+    d, H, D = 2048, 16, 128
+    box = {}
+
+    def step():
+        box["out"] = layer.forward(xt, mode=args.mode, save_for_backward=False)
+
+    def parity():
+        ref = oracle.attention_layer_forward(x, w["wq"], w["wk"], w["wv"], w["wo"], w["q_norm"], w["k_norm"])
+        return _rel(box["out"].cpu().numpy(), ref)
+
+    def cpu(budget):
+        threads, cores = _threads(16)
+        med, n = _time_cpu(lambda: oracle.attention_layer_forward(x, w["wq"], w["wk"], w["wv"], w["wo"], w["q_norm"],
+                                                                  w["k_norm"], nthreads=threads), budget)
+        return {"value": (8 * T * d * d + algorithmic_flops(1, T, H, D)) / med / 1e12, "unit": "TFLOP/s",
+                "cores": threads, "kind": "port",
+                "sample": f"oracle OlmoAttention::forward fp32, x [1,{T},2048], x {n} runs (median {med * 1e3:.1f} ms), "
+                f"{threads} threads of {cores} usable"}
+
+    return dict(step=step, flops=8 * T * d * d + algorithmic_flops(1, T, H, D), tokens=T, parity=parity, cpu=cpu,
+                metric=f"attention layer forward TFLOP/s + tok/s, OLMo-2-1B layer T={T}",
+                data="synthetic (x ~ N(0,1) seed 2001, W ~ N(0,0.02), norms ~ 1+N(0,0.01))",
+                config={"workload": f"OlmoAttention forward, x [1,{T},2048], {args.mode} core", "B": 1, "T": T,
+                        "d_model": d, "H": H, "D": D})
+
+
+def wl_layer_train(args, dev, stream, ctx):
+    import numpy as np
+    import torch
+
+    import oracle
+    from dirktensor_amd import synth
+
+    T, w, layer, x, xt = _layer_setup(args, dev)
+    d, H, D = 2048, 16, 128
+    g = synth.normal(2002, x.shape)
+    gt = torch.from_numpy(g).to(dev)
+    box = {}
+
+    def step():  # OlmoBlock::step order for one layer: zero_grad, forward, backward, step
+        layer.zero_grad()
+        layer.forward(xt, mode=args.mode)
+        box["dx"] = layer.backward(gt)
+        layer.step(0.0)  # lr 0 keeps the weights (and so the timed work) fixed across steps
+
+    def parity():
+        ref_dx, _ = oracle.attention_layer_backward(x, w["wq"], w["wk"], w["wv"], w["wo"], w["q_norm"], w["k_norm"], g)
+        return _rel(box["dx"].cpu().numpy(), ref_dx)
+
+    flops = 3 * 8 * T * d * d + 7 * algorithmic_flops(1, T, H, D) // 2
+
+    def cpu(budget):
+        threads, cores = _threads(16)
+        med, n = _time_cpu(lambda: oracle.attention_layer_backward(x, w["wq"], w["wk"], w["wv"], w["wo"], w["q_norm"],
+                                                                   w["k_norm"], g, nthreads=threads), budget)
+        return {"value": flops / med / 1e12, "unit": "TFLOP/s", "cores": threads, "kind": "port",
+                "sample": f"oracle OlmoAttention forward + backward fp32, x [1,{T},2048], x {n} runs "
+                f"(median {med * 1e3:.1f} ms), {threads} threads of {cores} usable"}
+
+    return dict(step=step, flops=flops, tokens=T, parity=parity, cpu=cpu,
+                metric=f"attention layer train step TFLOP/s + tok/s, OLMo-2-1B layer T={T}",
+                data="synthetic (x ~ N(0,1) seed 2001, dL/dout ~ N(0,1) seed 2002, seeded weights)",
+                config={"workload": f"OlmoAttention forward + backward + step, x [1,{T},2048], {args.mode}",
+                        "B": 1, "T": T, "d_model": d, "H": H, "D": D})
+
+
+WORKLOADS = {"flash_fwd": wl_flash_fwd, "flash_bwd": wl_flash_bwd, "ragged_fwd": wl_ragged_fwd,
+             "layer_fwd": wl_layer_fwd, "layer_train": wl_layer_train}
 
 
 if __name__ == "__main__":
