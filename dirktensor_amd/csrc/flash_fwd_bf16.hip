@@ -8,7 +8,9 @@
 //     one workgroup per CU walks the items in "snake" order over a list sorted
 //     by causal cost (item k of round j: j*G + w on even rounds, (j+1)*G-1-w on
 //     odd ones), so a workgroup pairs a long query tile with a short one; at
-//     T = 4096, H = 16 every workgroup gets 33 key tiles of work.
+//     T = 4096, H = 16 every workgroup gets 33 key tiles of work. In a ragged
+//     batch the list holds only the tiles that start before their sequence's
+//     end, in the same cost order, followed by the padding tiles.
 //   * A workgroup has 8 waves in two groups of 4. Both groups hold the same 128
 //     queries (32 per wave) and split the key tiles: group g takes 64-key tiles
 //     g, g+2, g+4, ... At the end group 1 hands its partial (max, sum, O) to
@@ -59,6 +61,7 @@
 
 #include "dt_internal.h"
 
+#include <algorithm>
 #include <type_traits>
 #include <utility>
 
@@ -119,11 +122,37 @@ struct Item {
     int b, h, qt;
 };
 
+// Item order of a ragged batch, built on the host: the items that compute (query tiles that start
+// before their sequence's end) sorted by decreasing causal cost, i.e. query tile from the last to the
+// first and, within a tile, the sequences long enough to reach it; then the padding items (tiles past
+// a sequence's end, which only write the empty rows).
+struct RaggedOrder {
+    int n_valid;             // computing items
+    int cum_valid[65];       // cum_valid[j]: computing items in the tiles n_qt-1 .. n_qt-j
+    int cum_pad[65];         // the same for padding items
+    int nb[64];              // nb[qt]: sequences with rows in tile qt
+    uint16_t order[kMaxRaggedBatch];  // sequences by decreasing length (stable)
+};
+
 __device__ __forceinline__ Item decode_item(int k, int n_qt, int BH, int H) {
     Item it;
     it.qt = n_qt - 1 - k / BH;  // items sorted by decreasing causal cost
     const int r = k % BH;
     it.b = r / H;
+    it.h = r % H;
+    return it;
+}
+
+__device__ __forceinline__ Item decode_item_ragged(int k, int n_qt, int H, const RaggedOrder& ro) {
+    const bool pad = k >= ro.n_valid;
+    const int* cum = pad ? ro.cum_pad : ro.cum_valid;
+    const int kk = pad ? k - ro.n_valid : k;
+    int j = 0;
+    while (j + 1 < n_qt && cum[j + 1] <= kk) ++j;
+    Item it;
+    it.qt = n_qt - 1 - j;
+    const int r = kk - cum[j];
+    it.b = ro.order[(pad ? ro.nb[it.qt] : 0) + r / H];
     it.h = r % H;
     return it;
 }
@@ -262,7 +291,7 @@ __device__ __forceinline__ void tile_step(Acc& A, const bf16x8 (&qf)[8], const u
 // complete before any wave passes it.
 __device__ __forceinline__ void stage_barrier() { asm volatile("s_waitcnt vmcnt(0) lgkmcnt(0)\n\ts_barrier" ::: "memory"); }
 
-__global__ __launch_bounds__(kThreads, 1) void flash_fwd_bf16_kernel(FlashArgs a, SeqLens lens) {
+__global__ __launch_bounds__(kThreads, 1) void flash_fwd_bf16_kernel(FlashArgs a, SeqLens lens, RaggedOrder ro) {
     __shared__ __attribute__((aligned(1024))) Stage stage0;
     __shared__ __attribute__((aligned(1024))) Stage stage1;
 
@@ -318,7 +347,7 @@ __global__ __launch_bounds__(kThreads, 1) void flash_fwd_bf16_kernel(FlashArgs a
     for (int round = 0;; ++round) {
         const int k_item = (round & 1) ? (round + 1) * G - 1 - (int)blockIdx.x : round * G + (int)blockIdx.x;
         if (k_item >= n_items) break;
-        const Item itm = decode_item(k_item, n_qt, BH, a.H);
+        const Item itm = a.ragged ? decode_item_ragged(k_item, n_qt, a.H, ro) : decode_item(k_item, n_qt, BH, a.H);
         const int b = itm.b, h = itm.h;
         const int L = a.ragged ? lens.len[b] : T;
         const int q0 = itm.qt * kBM;
@@ -497,7 +526,26 @@ int launch_flash_fwd_bf16(const FlashArgs& a, const SeqLens* lens, hipStream_t s
     const int64_t n_items = (int64_t)((a.T + kBM - 1) / kBM) * a.B * a.H;
     if (n_items > 0x7fffffff) return set_error(DT_ERR_UNSUPPORTED, "too many attention items");
     const int grid = (int)(n_items < g_num_cus[dev] ? n_items : g_num_cus[dev]);
-    hipLaunchKernelGGL(flash_fwd_bf16_kernel, dim3(grid), dim3(kThreads), 0, stream, a, sl);
+    RaggedOrder ro{};
+    if (a.ragged) {
+        const int n_qt = (a.T + kBM - 1) / kBM;  // <= 64: T <= 8192 is checked by the caller
+        int idx[kMaxRaggedBatch];
+        for (int b = 0; b < a.B; ++b) idx[b] = b;
+        std::stable_sort(idx, idx + a.B, [&](int x, int y) { return sl.len[x] > sl.len[y]; });
+        for (int b = 0; b < a.B; ++b) ro.order[b] = (uint16_t)idx[b];
+        for (int qt = 0; qt < n_qt; ++qt) {
+            int nb = 0;
+            for (int b = 0; b < a.B; ++b) nb += sl.len[b] > qt * kBM;
+            ro.nb[qt] = nb;
+        }
+        for (int j = 0; j < n_qt; ++j) {
+            const int qt = n_qt - 1 - j;
+            ro.cum_valid[j + 1] = ro.cum_valid[j] + ro.nb[qt] * a.H;
+            ro.cum_pad[j + 1] = ro.cum_pad[j] + (a.B - ro.nb[qt]) * a.H;
+        }
+        ro.n_valid = ro.cum_valid[n_qt];
+    }
+    hipLaunchKernelGGL(flash_fwd_bf16_kernel, dim3(grid), dim3(kThreads), 0, stream, a, sl, ro);
     DT_HIP_TRY(hipGetLastError());
     return DT_OK;
 }
