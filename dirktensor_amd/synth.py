@@ -100,3 +100,44 @@ def attention_layer_weights(d_model: int = 2048, seed_base: int = 2011, norm_see
 
 def layer_input(B: int = 1, T: int = 512, d_model: int = 2048, seed: int = 2001) -> np.ndarray:
     return normal(seed, (B, T, d_model))
+
+
+MODEL_LAYER_PARAMS = ("self_attn.q_proj", "self_attn.k_proj", "self_attn.v_proj", "self_attn.o_proj",
+                      "self_attn.q_norm", "self_attn.k_norm", "post_attention_layernorm", "mlp.gate_proj",
+                      "mlp.up_proj", "mlp.down_proj", "post_feedforward_layernorm")
+
+
+def model_params(n_layers: int = 16, vocab: int = 100352, hidden: int = 8192, d_model: int = 2048,
+                 seed_base: int = 5100) -> dict:
+    """Seeded OLMo-2 weights keyed by the reference's .npy file stems (OlmoModel.cpp:12-22,
+    OlmoBlock.cpp:5-11, OlmoMlp.cpp:9-24, OlmoAttention.cpp:39-53). Matrices ~ N(0, 0.02) rounded to
+    bf16-representable fp32 (so both modes see the same weights), norm weights ~ 1 + N(0, 0.01); the
+    k-th array in creation order uses seed seed_base + k."""
+    shapes = {"self_attn.q_proj": (d_model, d_model), "self_attn.k_proj": (d_model, d_model),
+              "self_attn.v_proj": (d_model, d_model), "self_attn.o_proj": (d_model, d_model),
+              "self_attn.q_norm": (d_model,), "self_attn.k_norm": (d_model,), "post_attention_layernorm": (d_model,),
+              "mlp.gate_proj": (hidden, d_model), "mlp.up_proj": (hidden, d_model), "mlp.down_proj": (d_model, hidden),
+              "post_feedforward_layernorm": (d_model,)}
+    out = {}
+    k = 0
+
+    def draw(shape):
+        nonlocal k
+        seed = seed_base + k
+        k += 1
+        if len(shape) == 1:
+            return normal(seed, shape, 1.0, 0.01)
+        return round_bf16(normal(seed, shape, 0.0, 0.02))
+
+    out["model.embed_tokens.weight"] = draw((vocab, d_model))
+    for i in range(n_layers):
+        for name in MODEL_LAYER_PARAMS:
+            out[f"model.layers.{i}.{name}.weight"] = draw(shapes[name])
+    out["model.norm.weight"] = draw((d_model,))
+    out["lm_head.weight"] = draw((vocab, d_model))
+    return out
+
+
+def model_tokens(B: int = 1, T: int = 2048, vocab: int = 100352, seed: int = 5001) -> np.ndarray:
+    """Token ids ~ U[0, vocab) for the end-to-end workloads, int32 [B, T]."""
+    return uniform_int(seed, B * T, 0, vocab - 1).astype(np.int32).reshape(B, T)

@@ -50,6 +50,10 @@ def lib() -> ctypes.CDLL:
         l.oracle_apply_rope_backward.argtypes = [_vp, _vp, _i, _i, _i, _i, _vp, _vp]
         l.oracle_rmsnorm_backward.argtypes = [_vp] * 6 + [_i, _i]
         l.oracle_attention_layer_backward.argtypes = [_vp] * 17 + [_i, _i, _i, _i, _f, _i]
+        l.oracle_mlp_forward.argtypes = [_vp] * 5 + [_i, _i, _i, _i, _vp, _vp, _vp]
+        l.oracle_model_forward.argtypes = [_vp] * 6 + [_i] * 6 + [_f, _i]
+        l.oracle_ce_loss.argtypes = [_vp, _vp, _i, _i, _i, _i, _vp, _vp]
+        l.oracle_ce_loss.restype = _f
         _lib = l
     return _lib
 
@@ -216,3 +220,56 @@ def attention_layer_backward(x, wq, wk, wv, wo, q_norm, k_norm, d_out, *, theta:
                                           _p(g["q_norm"]), _p(g["k_norm"]), B, T, H, D, float(eps),
                                           nthreads or default_threads())
     return d_x, g
+
+
+LAYER_PARAMS = ("self_attn.q_proj", "self_attn.k_proj", "self_attn.v_proj", "self_attn.o_proj", "self_attn.q_norm",
+                "self_attn.k_norm", "post_attention_layernorm", "mlp.gate_proj", "mlp.up_proj", "mlp.down_proj",
+                "post_feedforward_layernorm")
+
+
+def mlp_forward(x, w_gate, w_up, w_down, nthreads: int | None = None):
+    """OlmoMlp::forward (OlmoMlp.cpp:26-63) on rows of x [..., dm]."""
+    x = _c32(x)
+    dm = x.shape[-1]
+    rows = x.size // dm
+    hid = w_up.shape[0]
+    out = np.empty(x.shape, np.float32)
+    lib().oracle_mlp_forward(_p(x), _p(_c32(w_gate)), _p(_c32(w_up)), _p(_c32(w_down)), _p(out), rows, dm, hid,
+                             nthreads or default_threads(), None, None, None)
+    return out
+
+
+def model_forward(tokens, params: dict, *, eps: float = 1e-6, nthreads: int | None = None):
+    """OlmoModel::forward (OlmoModel.cpp:25-48): tokens [B, T] -> logits [B, T, V]. ``params`` maps the
+    reference's weight file stems ("model.embed_tokens.weight", "model.layers.{i}.mlp.up_proj.weight",
+    ..., "model.norm.weight", "lm_head.weight") to fp32 arrays."""
+    tok = np.ascontiguousarray(tokens, dtype=np.int32)
+    B, T = tok.shape
+    embed = _c32(params["model.embed_tokens.weight"])
+    V, dm = embed.shape
+    n_layers = sum(1 for k in params if k.endswith(".mlp.up_proj.weight"))
+    hid = params["model.layers.0.mlp.up_proj.weight"].shape[0]
+    keep = [embed]
+    ptrs = (_vp * (n_layers * len(LAYER_PARAMS)))()
+    for i in range(n_layers):
+        for j, name in enumerate(LAYER_PARAMS):
+            a = _c32(params[f"model.layers.{i}.{name}.weight"])
+            keep.append(a)
+            ptrs[i * len(LAYER_PARAMS) + j] = a.ctypes.data
+    fn, lm = _c32(params["model.norm.weight"]), _c32(params["lm_head.weight"])
+    logits = np.empty((B, T, V), np.float32)
+    lib().oracle_model_forward(_p(tok), _p(embed), ctypes.cast(ptrs, _vp), _p(fn), _p(lm), _p(logits), B, T, dm, hid,
+                               V, n_layers, float(eps), nthreads or default_threads())
+    return logits
+
+
+def ce_loss(logits, tokens, ignore_index: int, with_grad: bool = False):
+    """ce_loss (CrossEntropyLoss.cpp:8-43): mean next-token cross entropy, targets tokens[:, 1:], those equal
+    to ignore_index skipped. With ``with_grad`` also main.cpp:62-80's gradient (softmax - onehot) / count."""
+    logits = _c32(logits)
+    tok = np.ascontiguousarray(tokens, dtype=np.int32)
+    B, T, V = logits.shape
+    g = np.empty_like(logits) if with_grad else None
+    cnt = ctypes.c_int(0)
+    loss = lib().oracle_ce_loss(_p(logits), _p(tok), B, T, V, int(ignore_index), _p(g), ctypes.byref(cnt))
+    return (float(loss), g) if with_grad else float(loss)

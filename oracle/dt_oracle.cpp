@@ -21,6 +21,11 @@
 //   oracle_rmsnorm_backward       RMSNorm.cpp:24-36          (c = mean(dy*y), n = y/w recomputed)
 //   oracle_attention_layer_backward OlmoAttention.cpp:193-312 (o_proj, flash, RoPE, norms and
 //                                  q/k/v projection backward; weight gradients accumulated)
+//   oracle_mlp_forward            OlmoMlp.cpp:26-63          (SwiGLU: silu(x Wgate^T) * x Wup^T, Wdown)
+//   oracle_model_forward          OlmoModel.cpp:25-48, OlmoBlock.cpp:13-21 (embedding, post-norm
+//                                  blocks, final norm, LM head OlmoLmHead.cpp:11-28)
+//   oracle_ce_loss                CrossEntropyLoss.cpp:8-43 and main.cpp:62-80 (loss with
+//                                  ignore_index, and the softmax - onehot gradient / count)
 //
 // Parity pins (checked in tests/test_oracle_pins.py): an fp64 full-softmax attention
 // written independently in numpy, torch's scaled_dot_product_attention in fp64,
@@ -164,6 +169,9 @@ int oracle_version(void) { return 1; }
 //   9 rope backward: rotate forwards, not back      (OlmoAttention.cpp:174-182)
 //  10 norm backward: drop the c = mean(dy * y) term (RMSNorm.cpp:26, 35)
 //  11 flash backward: P without the 1 / l           (FlashAttention.cpp:272)
+//  12 mlp: drop the sigmoid from SiLU               (OlmoMlp.cpp:47-52)
+//  13 model: pre-norm blocks instead of post-norm   (OlmoBlock.cpp:13-21)
+//  14 ce: count the ignore_index targets           (CrossEntropyLoss.cpp:28-30)
 void oracle_set_mutation(int m) { g_mutation = m; }
 int oracle_get_mutation(void) { return g_mutation; }
 
@@ -548,6 +556,109 @@ void oracle_attention_layer_backward(const float* x, const float* wq, const floa
     for (size_t i = 0; i < n; ++i) d_x[i] += t1[i];
     oracle_sgemm_nn(rows, dm, dm, dv.data(), dm, wv, dm, t1.data(), dm, nthreads);
     for (size_t i = 0; i < n; ++i) d_x[i] += t1[i];
+}
+
+
+// ------------------------------------------------------------------------------------------------ model
+// Per-layer parameter order of the model functions below (file names of OlmoBlock / OlmoAttention /
+// OlmoMlp, OlmoBlock.cpp:5-11, OlmoAttention.cpp:39-53, OlmoMlp.cpp:9-24):
+//   0 self_attn.q_proj  1 self_attn.k_proj  2 self_attn.v_proj  3 self_attn.o_proj
+//   4 self_attn.q_norm  5 self_attn.k_norm  6 post_attention_layernorm
+//   7 mlp.gate_proj     8 mlp.up_proj       9 mlp.down_proj     10 post_feedforward_layernorm
+constexpr int kLayerParams = 11;
+
+// OlmoMlp::forward, OlmoMlp.cpp:26-63: up = x Wup^T, gate = x Wgate^T, act = gate / (1 + exp(-gate)) * up,
+// out = act Wdown^T. x [rows][dm], Wup/Wgate [hid][dm], Wdown [dm][hid]. gate/up/act (nullable) keep state.
+void oracle_mlp_forward(const float* x, const float* w_gate, const float* w_up, const float* w_down, float* out,
+                        int rows, int dm, int hid, int nthreads, float* gate_out, float* up_out, float* act_out) {
+    std::vector<float> up((size_t)rows * hid), gate((size_t)rows * hid), act((size_t)rows * hid);
+    oracle_sgemm_nt(rows, hid, dm, 1.0f, x, dm, w_up, dm, up.data(), hid, nthreads);
+    oracle_sgemm_nt(rows, hid, dm, 1.0f, x, dm, w_gate, dm, gate.data(), hid, nthreads);
+    for (size_t i = 0; i < act.size(); ++i) {
+        const float g = gate[i];
+        const float silu = (g_mutation == 12) ? g : g / (1.0f + std::exp(-g));
+        act[i] = silu * up[i];
+    }
+    oracle_sgemm_nt(rows, dm, hid, 1.0f, act.data(), hid, w_down, hid, out, dm, nthreads);
+    if (gate_out) std::memcpy(gate_out, gate.data(), gate.size() * sizeof(float));
+    if (up_out) std::memcpy(up_out, up.data(), up.size() * sizeof(float));
+    if (act_out) std::memcpy(act_out, act.data(), act.size() * sizeof(float));
+}
+
+// OlmoModel::forward, OlmoModel.cpp:25-48: embedding rows, n_layers post-norm blocks
+// (OlmoBlock.cpp:13-21: h = x + N_attn(attn(x)); y = h + N_mlp(mlp(h))), final norm, LM head.
+// tokens [B][T]; embed [V][dm]; layers: n_layers * 11 pointers in the order above; lm_head [V][dm];
+// logits [B][T][V]. hid is the MLP width (8192 in the reference).
+void oracle_model_forward(const int32_t* tokens, const float* embed, const float* const* layers,
+                          const float* final_norm, const float* lm_head, float* logits, int B, int T, int dm,
+                          int hid, int V, int n_layers, float eps, int nthreads) {
+    const int rows = B * T, H = dm / 128;
+    const size_t n = (size_t)rows * dm;
+    std::vector<float> x(n), a(n), na(n), h(n), m(n), nm(n);
+    for (int r = 0; r < rows; ++r) std::memcpy(&x[(size_t)r * dm], embed + (int64_t)tokens[r] * dm, dm * sizeof(float));
+    std::vector<float> sin_t((size_t)T * 128), cos_t((size_t)T * 128);
+    oracle_rope_tables(sin_t.data(), cos_t.data(), T, 128, 500000.0f);
+    for (int i = 0; i < n_layers; ++i) {
+        const float* const* p = layers + (size_t)i * kLayerParams;
+        if (g_mutation == 13) {  // planted mistake: pre-norm blocks
+            oracle_rmsnorm_forward(x.data(), p[6], na.data(), nullptr, rows, dm, eps);
+            oracle_attention_layer_forward(na.data(), p[0], p[1], p[2], p[3], p[4], p[5], sin_t.data(), cos_t.data(),
+                                           a.data(), B, T, H, 128, eps, nthreads, nullptr, nullptr, nullptr, nullptr,
+                                           nullptr, nullptr);
+            for (size_t j = 0; j < n; ++j) h[j] = x[j] + a[j];
+            oracle_rmsnorm_forward(h.data(), p[10], nm.data(), nullptr, rows, dm, eps);
+            oracle_mlp_forward(nm.data(), p[7], p[8], p[9], m.data(), rows, dm, hid, nthreads, nullptr, nullptr, nullptr);
+            for (size_t j = 0; j < n; ++j) x[j] = h[j] + m[j];
+            continue;
+        }
+        oracle_attention_layer_forward(x.data(), p[0], p[1], p[2], p[3], p[4], p[5], sin_t.data(), cos_t.data(),
+                                       a.data(), B, T, H, 128, eps, nthreads, nullptr, nullptr, nullptr, nullptr,
+                                       nullptr, nullptr);
+        oracle_rmsnorm_forward(a.data(), p[6], na.data(), nullptr, rows, dm, eps);
+        for (size_t j = 0; j < n; ++j) h[j] = x[j] + na[j];
+        oracle_mlp_forward(h.data(), p[7], p[8], p[9], m.data(), rows, dm, hid, nthreads, nullptr, nullptr, nullptr);
+        oracle_rmsnorm_forward(m.data(), p[10], nm.data(), nullptr, rows, dm, eps);
+        for (size_t j = 0; j < n; ++j) x[j] = h[j] + nm[j];
+    }
+    oracle_rmsnorm_forward(x.data(), final_norm, na.data(), nullptr, rows, dm, eps);
+    oracle_sgemm_nt(rows, V, dm, 1.0f, na.data(), dm, lm_head, dm, logits, V, nthreads);
+}
+
+// ce_loss, CrossEntropyLoss.cpp:8-43, and the gradient main.cpp:62-80 builds from its probs:
+// loss = mean over (b, s < T-1) with tokens[b][s+1] != ignore of log(sum_v exp(l - max)) - (l[target] - max);
+// d_logits (nullable) = (softmax - onehot(target)) / count at (b, s) for those positions, 0 elsewhere
+// (pad targets and the last position). Returns the loss; count is written to *count_out (nullable).
+float oracle_ce_loss(const float* logits, const int32_t* tokens, int B, int T, int V, int ignore_index,
+                     float* d_logits, int* count_out) {
+    double total = 0.0;  // the reference accumulates in float; a double sum keeps the oracle order-robust
+    int count = 0;
+    for (int b = 0; b < B; ++b)
+        for (int s = 0; s < T; ++s) {
+            const float* l = logits + ((int64_t)b * T + s) * V;
+            float* g = d_logits ? d_logits + ((int64_t)b * T + s) * V : nullptr;
+            const bool has_target = s + 1 < T && (g_mutation == 14 || tokens[b * T + s + 1] != ignore_index);
+            if (!has_target) {
+                if (g) std::fill(g, g + V, 0.0f);
+                continue;
+            }
+            float mx = l[0];
+            for (int v = 1; v < V; ++v) mx = std::max(mx, l[v]);
+            float se = 0.0f;
+            for (int v = 0; v < V; ++v) se += std::exp(l[v] - mx);
+            const int tgt = tokens[b * T + s + 1];
+            total += (double)std::log(se) - (double)(l[tgt] - mx);
+            ++count;
+            if (g) {
+                for (int v = 0; v < V; ++v) g[v] = std::exp(l[v] - mx) / se;
+                g[tgt] -= 1.0f;
+            }
+        }
+    if (d_logits && count > 0) {
+        const float inv = 1.0f / (float)count;
+        for (size_t i = 0; i < (size_t)B * T * V; ++i) d_logits[i] *= inv;
+    }
+    if (count_out) *count_out = count;
+    return count > 0 ? (float)(total / count) : 0.0f;
 }
 
 }  // extern "C"

@@ -17,6 +17,9 @@ pinned against things that fix the answer independently of its code:
 * torch.nn.functional.rms_norm in fp64, and RoPE invariants (identity at
   t = 0, pair norms preserved, scores depend only on t1 - t2).
 
+* model: HF's Olmo2ForCausalLM (2 layers) in fp64 for the whole forward,
+  torch's F.silu MLP, and F.cross_entropy(ignore_index) with its autograd
+  gradient for ce_loss and main.cpp's loss gradient;
 * backward: torch autograd in fp64 through scaled_dot_product_attention,
   F.rms_norm, HF's apply_rotary_pos_emb and the whole Olmo2Attention layer
   (d_x and all six weight gradients); central finite differences of a numpy
@@ -350,6 +353,62 @@ def pin_layer_bwd_hf(T=40):
     return bool(ok)
 
 
+# ----------------------------------------------------------------- model pins
+def _small_model(n_layers=2, vocab=300, hidden=512):
+    return synth.model_params(n_layers=n_layers, vocab=vocab, hidden=hidden, seed_base=5900)
+
+
+def pin_mlp_torch():
+    p = _small_model(1)
+    x = synth.normal(3001, (20, 2048))
+    wg, wu, wd = (p[f"model.layers.0.mlp.{n}_proj.weight"] for n in ("gate", "up", "down"))
+    out = oracle.mlp_forward(x, wg, wu, wd)
+    xt, g, u, d = (torch.from_numpy(a).double() for a in (x, wg, wu, wd))
+    ref = (F.silu(xt @ g.T) * (xt @ u.T)) @ d.T
+    return rel(out, ref.numpy()) <= 1e-5
+
+
+def _hf_model(p, n_layers, vocab, hidden):
+    from transformers import Olmo2ForCausalLM
+
+    cfg = hf_config()
+    cfg.num_hidden_layers = n_layers
+    cfg.vocab_size = vocab
+    cfg.intermediate_size = hidden
+    cfg.tie_word_embeddings = False
+    cfg._attn_implementation = "eager"
+    model = Olmo2ForCausalLM(cfg).double().eval()
+    sd = {k: torch.from_numpy(v).double() for k, v in p.items()}
+    missing, unexpected = model.load_state_dict(sd, strict=False)
+    assert not unexpected and all("rotary" in m for m in missing), (missing, unexpected)
+    return model
+
+
+def pin_model_hf():
+    """OlmoModel::forward against HF's Olmo2ForCausalLM (post-norm OLMo-2) in fp64, 2 layers."""
+    n_layers, vocab, hidden, T = 2, 300, 512, 24
+    p = _small_model(n_layers, vocab, hidden)
+    tok = synth.model_tokens(2, T, vocab, seed=5902)
+    logits = oracle.model_forward(tok, p)
+    with torch.no_grad():
+        ref = _hf_model(p, n_layers, vocab, hidden)(torch.from_numpy(tok).long()).logits.numpy()
+    return rel(logits, ref) <= 1e-4
+
+
+def pin_ce_torch():
+    """ce_loss and main.cpp's gradient against F.cross_entropy(ignore_index) and its autograd in fp64."""
+    B, T, V, pad = 3, 17, 50, 7
+    logits = synth.normal(3101, (B, T, V), 0.0, 3.0)
+    tok = synth.model_tokens(B, T, V, seed=3102)
+    tok[1, 9:] = pad  # a right-padded sequence (main.cpp:46-57)
+    tok[2, 4] = pad
+    loss, g = oracle.ce_loss(logits, tok, pad, with_grad=True)
+    lt = torch.from_numpy(logits).double().requires_grad_()
+    ref = F.cross_entropy(lt[:, :-1].reshape(-1, V), torch.from_numpy(tok[:, 1:]).long().reshape(-1), ignore_index=pad)
+    ref.backward()
+    return abs(loss - ref.item()) <= 1e-5 * abs(ref.item()) and rel(g, lt.grad.numpy()) <= 1e-5
+
+
 PINS = {
     "flash_textbook_causal": lambda: pin_flash_textbook(True),
     "flash_textbook_full": lambda: pin_flash_textbook(False),
@@ -371,6 +430,9 @@ PINS = {
     "rope_bwd_autograd": pin_rope_bwd_autograd,
     "rmsnorm_bwd_autograd": pin_rmsnorm_bwd_autograd,
     "layer_bwd_hf": pin_layer_bwd_hf,
+    "mlp_torch": pin_mlp_torch,
+    "model_hf": pin_model_hf,
+    "ce_torch": pin_ce_torch,
 }
 
 
@@ -392,6 +454,9 @@ MUTATIONS = {
     9: ["rope_bwd_adjoint", "rope_bwd_autograd", "layer_bwd_hf"],                            # forward rotation
     10: ["rmsnorm_bwd_autograd", "layer_bwd_hf"],                                            # c term dropped
     11: ["flash_bwd_autograd_causal", "flash_bwd_finite_difference"],                        # 1 / l dropped
+    12: ["mlp_torch", "model_hf"],                                                           # SiLU without sigmoid
+    13: ["model_hf"],                                                                         # pre-norm blocks
+    14: ["ce_torch"],                                                                         # pad targets counted
 }
 
 
