@@ -14,6 +14,7 @@ from .attention import (  # noqa: F401
     flash_attention_forward,
     qk_norm_rope,
 )
+from .model import OlmoModel, ce_loss  # noqa: F401
 from ._capi import DTError, LIB_PATH  # noqa: F401
 
 __all__ = [
@@ -22,6 +23,8 @@ __all__ = [
     "FlashAttentionResult",
     "LIB_PATH",
     "OlmoAttention",
+    "OlmoModel",
+    "ce_loss",
     "default_context",
     "flash_attention_backward",
     "flash_attention_forward",

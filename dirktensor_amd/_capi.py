@@ -57,6 +57,16 @@ SIGNATURES = {
     "dt_attn_layer_zero_grad": (_c_int, [_vp, _vp]),
     "dt_attn_layer_get_weights": (_c_int, [_vp] * 7 + [_c_int, _vp]),
     "dt_attn_layer_get_grads": (_c_int, [_vp] * 7 + [_c_int, _vp]),
+    "dt_model_create": (_c_int, [_vp, _c_int, _c_int, _c_int, _c_int, _c_int, ctypes.POINTER(_vp)]),
+    "dt_model_load": (_c_int, [_vp, ctypes.c_char_p, _c_int, ctypes.POINTER(_vp)]),
+    "dt_model_destroy": (_c_int, [_vp]),
+    "dt_model_set_param": (_c_int, [_vp, ctypes.c_char_p, _vp, ctypes.c_int64, _c_int]),
+    "dt_model_get_param": (_c_int, [_vp, ctypes.c_char_p, _vp, ctypes.c_int64, _c_int, _c_int, _vp]),
+    "dt_model_fwd": (_c_int, [_vp, _vp, _c_int, _c_int, _vp, _c_int, _c_int, _c_int, _vp]),
+    "dt_model_bwd": (_c_int, [_vp, _vp, _c_int, _vp]),
+    "dt_model_step": (_c_int, [_vp, ctypes.c_float, _vp]),
+    "dt_model_zero_grad": (_c_int, [_vp, _vp]),
+    "dt_ce_loss": (_c_int, [_vp, _vp, _vp, _c_int, _c_int, _c_int, _c_int, _vp, _vp, _c_int, _vp]),
 }
 
 _lib = None

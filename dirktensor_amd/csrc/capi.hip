@@ -53,9 +53,9 @@ void DeviceBuffer::release() {
     bytes = 0;
 }
 
-static bool aligned16(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15) == 0; }
+bool aligned16(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15) == 0; }
 
-static int check_device_binding(dt_ctx* ctx) {
+int check_device_binding(dt_ctx* ctx) {
     DT_HIP_TRY(hipSetDevice(ctx->device));
     return DT_OK;
 }
@@ -121,7 +121,7 @@ static int ensure_blas(dt_ctx* ctx) {
 // Row-major C[M][N] = op(A)[M][K] op(B)[K][N] + beta C, op = transpose when the flag is set (A is then
 // stored [K][M], B [N][K]). In rocBLAS's column-major terms a row-major X is X^T, so this is
 // C^T = op(B)^T op(A)^T: B goes first, each transposed exactly when it is transposed here.
-static int gemm_rm(dt_ctx* ctx, hipStream_t s, bool ta, bool tb, int M, int N, int K, const void* A, int lda,
+int gemm_rm(dt_ctx* ctx, hipStream_t s, bool ta, bool tb, int M, int N, int K, const void* A, int lda,
                    const void* B, int ldb, float beta, float* C, int ldc, bool bf16_in) {
     DT_TRY(ensure_blas(ctx));
     rocblas_handle h = static_cast<rocblas_handle>(ctx->blas);
@@ -150,7 +150,7 @@ static int gemm_xwt(dt_ctx* ctx, hipStream_t s, int M, int N, int K, const void*
 }
 
 // ---------------- .npy reader (v1/v2/v3, little-endian fp32, C order) ----------------
-static int read_npy_f32(const std::string& path, std::vector<float>& out, std::vector<size_t>& shape) {
+int read_npy_f32(const std::string& path, std::vector<float>& out, std::vector<size_t>& shape) {
     FILE* f = std::fopen(path.c_str(), "rb");
     if (!f) return set_error(DT_ERR_IO, "cannot open %s", path.c_str());
     unsigned char magic[8];
@@ -201,30 +201,6 @@ static int read_npy_f32(const std::string& path, std::vector<float>& out, std::v
 }  // namespace dt
 
 // ---------------- layer ----------------
-struct dt_attn_layer {
-    dt_ctx* ctx = nullptr;
-    int d_model = 0, n_heads = 0;
-    float* w_qkv = nullptr;      // [3*d_model][d_model] fp32 (q rows, k rows, v rows)
-    float* w_o = nullptr;        // [d_model][d_model]
-    uint16_t* w_qkv16 = nullptr; // bf16 copies, made on first bf16 forward
-    uint16_t* w_o16 = nullptr;
-    float* q_norm = nullptr;
-    float* k_norm = nullptr;
-    dt::DeviceBuffer qkv32, qkv16, attn, x16;
-    bool w16_stale = true;  // the bf16 copies lag the fp32 weights (before the first bf16 forward, after step)
-    // forward state kept for backward (OlmoAttention.h:28-38) when save_for_backward is set
-    dt::DeviceBuffer x32;   // the input rows (fp32)
-    dt::DeviceBuffer att32; // fp32 mode: q_rope | k_rope | v, [rows][3*d_model]
-    dt::DeviceBuffer rms;   // q and k rms, 2 x [rows]
-    dt::DeviceBuffer stats; // attention m and l, 2 x [rows][H]
-    int saved_B = 0, saved_T = 0, saved_dtype = -1;  // saved_T == 0: nothing saved
-    // backward workspaces and the accumulated gradients (param<2>::grad, param.h:5-15)
-    dt::DeviceBuffer d_attn32, d16, d_qkv, partial;
-    float* g_qkv = nullptr;  // [3*d_model][d_model]
-    float* g_o = nullptr;    // [d_model][d_model]
-    float* g_qn = nullptr;   // [d_model]
-    float* g_kn = nullptr;
-};
 
 using namespace dt;
 
@@ -446,6 +422,32 @@ int dt_qk_norm_rope_fwd(dt_ctx* ctx, const float* q_in, const float* k_in, const
     return DT_OK;
 }
 
+}  // extern "C"
+
+int attn_layer_alloc(dt_ctx* ctx, int d_model, int n_heads, dt_attn_layer** out) {
+    dt_attn_layer* L = new dt_attn_layer();
+    L->ctx = ctx;
+    L->d_model = d_model;
+    L->n_heads = n_heads;
+    const size_t wsz = (size_t)d_model * d_model * sizeof(float);
+    hipError_t e = hipMalloc(&L->w_qkv, 3 * wsz);
+    if (e == hipSuccess) e = hipMalloc(&L->w_o, wsz);
+    if (e == hipSuccess) e = hipMalloc(&L->q_norm, d_model * sizeof(float));
+    if (e == hipSuccess) e = hipMalloc(&L->k_norm, d_model * sizeof(float));
+    if (e == hipSuccess) e = hipMemset(L->w_qkv, 0, 3 * wsz);
+    if (e == hipSuccess) e = hipMemset(L->w_o, 0, wsz);
+    if (e == hipSuccess) e = hipMemset(L->q_norm, 0, d_model * sizeof(float));
+    if (e == hipSuccess) e = hipMemset(L->k_norm, 0, d_model * sizeof(float));
+    if (e != hipSuccess) {
+        dt_attn_layer_destroy(L);
+        return set_error(DT_ERR_HIP, "layer allocation: %s", hipGetErrorString(e));
+    }
+    *out = L;
+    return DT_OK;
+}
+
+extern "C" {
+
 int dt_attn_layer_create(dt_ctx* ctx, const float* wq, const float* wk, const float* wv, const float* wo,
                          const float* q_norm_w, const float* k_norm_w, int d_model, int n_heads, int mem,
                          dt_attn_layer** out) {
@@ -458,27 +460,20 @@ int dt_attn_layer_create(dt_ctx* ctx, const float* wq, const float* wk, const fl
     if (mem != DT_MEM_DEVICE && mem != DT_MEM_HOST) return set_error(DT_ERR_INVALID_ARG, "unknown mem %d", mem);
     if (!ctx) return set_error(DT_ERR_INVALID_ARG, "ctx is NULL");
     DT_TRY(check_device_binding(ctx));
-    dt_attn_layer* L = new dt_attn_layer();
-    L->ctx = ctx;
-    L->d_model = d_model;
-    L->n_heads = n_heads;
+    dt_attn_layer* L = nullptr;
+    DT_TRY(attn_layer_alloc(ctx, d_model, n_heads, &L));
     const size_t wsz = (size_t)d_model * d_model * sizeof(float);
     const hipMemcpyKind kind = mem == DT_MEM_HOST ? hipMemcpyHostToDevice : hipMemcpyDeviceToDevice;
-    auto fail = [&](int rc) {
-        dt_attn_layer_destroy(L);
-        return rc;
-    };
-    hipError_t e = hipMalloc(&L->w_qkv, 3 * wsz);
-    if (e == hipSuccess) e = hipMalloc(&L->w_o, wsz);
-    if (e == hipSuccess) e = hipMalloc(&L->q_norm, d_model * sizeof(float));
-    if (e == hipSuccess) e = hipMalloc(&L->k_norm, d_model * sizeof(float));
-    if (e == hipSuccess) e = hipMemcpy(L->w_qkv, wq, wsz, kind);
+    hipError_t e = hipMemcpy(L->w_qkv, wq, wsz, kind);
     if (e == hipSuccess) e = hipMemcpy(reinterpret_cast<char*>(L->w_qkv) + wsz, wk, wsz, kind);
     if (e == hipSuccess) e = hipMemcpy(reinterpret_cast<char*>(L->w_qkv) + 2 * wsz, wv, wsz, kind);
     if (e == hipSuccess) e = hipMemcpy(L->w_o, wo, wsz, kind);
     if (e == hipSuccess) e = hipMemcpy(L->q_norm, q_norm_w, d_model * sizeof(float), kind);
     if (e == hipSuccess) e = hipMemcpy(L->k_norm, k_norm_w, d_model * sizeof(float), kind);
-    if (e != hipSuccess) return fail(set_error(DT_ERR_HIP, "layer weight upload: %s", hipGetErrorString(e)));
+    if (e != hipSuccess) {
+        dt_attn_layer_destroy(L);
+        return set_error(DT_ERR_HIP, "layer weight upload: %s", hipGetErrorString(e));
+    }
     *out = L;
     return DT_OK;
 }
@@ -642,7 +637,9 @@ int dt_attn_layer_fwd(dt_attn_layer* L, const float* x, float* out, int B, int T
     return DT_OK;
 }
 
-static int ensure_grads(dt_attn_layer* L, hipStream_t s) {
+}  // extern "C"
+
+int attn_layer_ensure_grads(dt_attn_layer* L, hipStream_t s) {
     if (L->g_qkv) return DT_OK;
     const size_t dm = L->d_model;
     DT_HIP_TRY(hipMalloc(&L->g_qkv, 3 * dm * dm * 4));
@@ -655,6 +652,8 @@ static int ensure_grads(dt_attn_layer* L, hipStream_t s) {
     DT_TRY(launch_fill_zero(L->g_kn, (int64_t)dm, s));
     return DT_OK;
 }
+
+extern "C" {
 
 int dt_attn_layer_bwd(dt_attn_layer* L, const float* d_out, float* d_x, int B, int T, int mem, void* stream) {
     clear_error();
@@ -675,7 +674,7 @@ int dt_attn_layer_bwd(dt_attn_layer* L, const float* d_out, float* d_x, int B, i
     const int dm = L->d_model, H = L->n_heads, rows = B * T;
     const size_t act = (size_t)rows * dm;
     const size_t esz = bf ? 2 : 4;
-    DT_TRY(ensure_grads(L, s));
+    DT_TRY(attn_layer_ensure_grads(L, s));
 
     const float* gd = d_out;
     float* dxd = d_x;
@@ -743,7 +742,7 @@ int dt_attn_layer_step(dt_attn_layer* L, float lr, void* stream) {
     if (!std::isfinite(lr)) return set_error(DT_ERR_INVALID_ARG, "lr must be finite");
     DT_TRY(check_device_binding(L->ctx));
     hipStream_t s = static_cast<hipStream_t>(stream);
-    DT_TRY(ensure_grads(L, s));
+    DT_TRY(attn_layer_ensure_grads(L, s));
     const int64_t dm = L->d_model;
     DT_TRY(launch_sgd(L->w_qkv, L->g_qkv, lr, 3 * dm * dm, s));  // OlmoAttention.cpp:315-317
     DT_TRY(launch_sgd(L->w_o, L->g_o, lr, dm * dm, s));          // :318
@@ -758,7 +757,7 @@ int dt_attn_layer_zero_grad(dt_attn_layer* L, void* stream) {
     if (!L) return set_error(DT_ERR_INVALID_ARG, "layer is NULL");
     DT_TRY(check_device_binding(L->ctx));
     hipStream_t s = static_cast<hipStream_t>(stream);
-    if (!L->g_qkv) return ensure_grads(L, s);  // allocated zeroed
+    if (!L->g_qkv) return attn_layer_ensure_grads(L, s);  // allocated zeroed
     const int64_t dm = L->d_model;
     DT_TRY(launch_fill_zero(L->g_qkv, 3 * dm * dm, s));  // OlmoAttention.cpp:323-330
     DT_TRY(launch_fill_zero(L->g_o, dm * dm, s));
@@ -775,7 +774,7 @@ static int copy_params(dt_attn_layer* L, int grads, float* wq, float* wk, float*
     if (mem != DT_MEM_DEVICE && mem != DT_MEM_HOST) return set_error(DT_ERR_INVALID_ARG, "unknown mem %d", mem);
     DT_TRY(check_device_binding(L->ctx));
     hipStream_t s = static_cast<hipStream_t>(stream);
-    if (grads) DT_TRY(ensure_grads(L, s));
+    if (grads) DT_TRY(attn_layer_ensure_grads(L, s));
     const size_t dm = L->d_model, w2 = dm * dm * 4;
     const float* src_qkv = grads ? L->g_qkv : L->w_qkv;
     const float* srcs[6] = {src_qkv, src_qkv + dm * dm, src_qkv + 2 * dm * dm, grads ? L->g_o : L->w_o,

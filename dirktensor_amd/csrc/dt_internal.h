@@ -5,6 +5,7 @@
 
 #include <cstdint>
 #include <string>
+#include <vector>
 
 #include "dirktensor_amd.h"  // include/, on the include path
 
@@ -127,6 +128,15 @@ int launch_sgd(float* w, const float* g, float lr, int64_t n, hipStream_t stream
 int launch_fill_zero(float* p, int64_t n, hipStream_t stream);
 int launch_f32_to_bf16(const float* in, uint16_t* out, int64_t n, hipStream_t stream);
 
+// Row-major C[M][N] = op(A)[M][K] op(B)[K][N] + beta C on rocBLAS (fp32, or bf16 inputs with fp32
+// accumulation and output); op = transpose when ta / tb is set.
+int gemm_rm(dt_ctx* ctx, hipStream_t s, bool ta, bool tb, int M, int N, int K, const void* A, int lda,
+            const void* B, int ldb, float beta, float* C, int ldc, bool bf16_in);
+// .npy reader (v1-v3 headers, little-endian fp32, C order)
+int read_npy_f32(const std::string& path, std::vector<float>& out, std::vector<size_t>& shape);
+bool aligned16(const void* p);
+int check_device_binding(dt_ctx* ctx);
+
 }  // namespace dt
 
 // ---- opaque handles ----
@@ -140,3 +150,50 @@ struct dt_ctx {
     dt::DeviceBuffer bwd_stats;  // attention-core backward: delta and lse2, 2 x [B][H][T] fp32
     void* blas = nullptr;        // rocblas_handle, created on first use
 };
+
+// OlmoAttention on the device (OlmoAttention.h:10-42): weights, forward state kept for backward, gradients.
+struct dt_attn_layer {
+    dt_ctx* ctx = nullptr;
+    int d_model = 0, n_heads = 0;
+    float* w_qkv = nullptr;      // [3*d_model][d_model] fp32 (q rows, k rows, v rows)
+    float* w_o = nullptr;        // [d_model][d_model]
+    uint16_t* w_qkv16 = nullptr; // bf16 copies, made on first bf16 forward
+    uint16_t* w_o16 = nullptr;
+    float* q_norm = nullptr;
+    float* k_norm = nullptr;
+    dt::DeviceBuffer qkv32, qkv16, attn, x16;
+    bool w16_stale = true;  // the bf16 copies lag the fp32 weights (before the first bf16 forward, after step)
+    // forward state kept for backward (OlmoAttention.h:28-38) when save_for_backward is set
+    dt::DeviceBuffer x32;   // the input rows (fp32)
+    dt::DeviceBuffer att32; // fp32 mode: q_rope | k_rope | v, [rows][3*d_model]
+    dt::DeviceBuffer rms;   // q and k rms, 2 x [rows]
+    dt::DeviceBuffer stats; // attention m and l, 2 x [rows][H]
+    int saved_B = 0, saved_T = 0, saved_dtype = -1;  // saved_T == 0: nothing saved
+    // backward workspaces and the accumulated gradients (param<2>::grad, param.h:5-15)
+    dt::DeviceBuffer d_attn32, d16, d_qkv, partial;
+    float* g_qkv = nullptr;  // [3*d_model][d_model]
+    float* g_o = nullptr;    // [d_model][d_model]
+    float* g_qn = nullptr;   // [d_model]
+    float* g_kn = nullptr;
+};
+
+// zero-initialised attention layer (weights set afterwards), and its gradient buffers (allocated zeroed)
+int attn_layer_alloc(dt_ctx* ctx, int d_model, int n_heads, dt_attn_layer** out);
+int attn_layer_ensure_grads(dt_attn_layer* L, hipStream_t s);
+
+namespace dt {
+// model kernels (model_kernels.hip)
+int launch_embed_gather(const int32_t* tok, const float* E, float* x, int rows, int dm, hipStream_t s);
+int launch_add(const float* a, const float* b, float* out, int64_t n, hipStream_t s);  // n % 4 == 0
+int launch_rmsnorm_rows(const float* a, const float* w, const float* res, float* out, uint16_t* out16, float* y_save,
+                        float* rms_save, int rows, int dm, float eps, hipStream_t s);
+int launch_swiglu(const float* gu, void* act, int rows, int hid, int bf16, hipStream_t s);
+int launch_ce_loss(const float* logits, const int32_t* target, float* term, float* grad, float* loss, int rows, int V,
+                   int count, hipStream_t s);
+int rmsnorm_bwd_blocks(int rows);
+int launch_rmsnorm_bwd(const float* dy, const float* y, const float* rms, const float* w, const float* dx_add,
+                       float* dx, float* partial, float* grad_w, int rows, int dm, hipStream_t s);
+int launch_swiglu_bwd(const float* d_act, const float* gu, void* d_gu, int rows, int hid, int bf16, hipStream_t s);
+int launch_embed_bwd(const float* dx, const int32_t* uniq, const int32_t* start, const int32_t* pos, int n_uniq,
+                     float* g_embed, int dm, hipStream_t s);
+}  // namespace dt

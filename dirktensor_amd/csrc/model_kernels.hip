@@ -1,0 +1,351 @@
+// Element-wise and row kernels of the OLMo-2 model around the attention layer, for gfx950.
+//
+//   embed_gather        OlmoModel.cpp:29-38: x[b, t] = E[token[b, t]]
+//   rmsnorm_rows        RMSNorm::forward (RMSNorm.cpp:15-22) on d_model rows, optionally added to a
+//                       residual (the post-norm blocks, OlmoBlock.cpp:13-21: h = x + N(attn(x))),
+//                       keeping the output y and rms the norm's backward needs (RMSNorm.h:22-23)
+//   swiglu              OlmoMlp.cpp:44-53: act = gate / (1 + exp(-gate)) * up, from the [gate | up]
+//                       rows of the concatenated projection
+//   ce_rows / ce_reduce ce_loss (CrossEntropyLoss.cpp:8-43) and the gradient main.cpp:62-80 builds
+//   rmsnorm_bwd_rows    RMSNorm::backward (RMSNorm.cpp:24-36) with the weight gradient reduced
+//                       deterministically through per-workgroup partial sums
+//   swiglu_bwd          OlmoMlp.cpp (backward): d_up = d_act * silu(gate),
+//                       d_gate = d_act * up * sig * (1 + gate * (1 - sig))
+//   embed_bwd           OlmoModel.cpp:60-66: E_grad[token] += dx rows, summed per distinct token in
+//                       position order (no atomics)
+// All are HBM bound; one workgroup of 256 threads per row unless noted.
+
+#include "dt_internal.h"
+
+namespace dt {
+namespace {
+
+typedef __bf16 bf16x2 __attribute__((ext_vector_type(2)));
+typedef float floatx2 __attribute__((ext_vector_type(2)));
+
+__device__ __forceinline__ uint32_t pack_bf16x2(float lo, float hi) {
+    bf16x2 r = __builtin_convertvector((floatx2){lo, hi}, bf16x2);
+    return __builtin_bit_cast(uint32_t, r);
+}
+
+// sum over the 256 threads of a workgroup (4 waves)
+__device__ __forceinline__ float block_sum(float v, float* red) {
+#pragma unroll
+    for (int off = 32; off >= 1; off >>= 1) v += __shfl_xor(v, off, 64);
+    __syncthreads();  // red may still be read by a previous call
+    if ((threadIdx.x & 63) == 0) red[threadIdx.x >> 6] = v;
+    __syncthreads();
+    return red[0] + red[1] + red[2] + red[3];
+}
+
+__global__ __launch_bounds__(256) void embed_gather_kernel(const int32_t* tok, const float* E, float* x, int dm) {
+    const int64_t row = blockIdx.x;
+    const float4* src = reinterpret_cast<const float4*>(E + (int64_t)tok[row] * dm);
+    float4* dst = reinterpret_cast<float4*>(x + row * dm);
+    for (int i = threadIdx.x; i < dm / 4; i += 256) dst[i] = src[i];
+}
+
+// out = res + (a / rms) * w (res may be null); y_save = (a / rms) * w, rms_save = rms (either may be null);
+// out16 (nullable) receives a bf16 copy of out
+__global__ __launch_bounds__(256) void rmsnorm_rows_kernel(const float* a, const float* w, const float* res, float* out,
+                                                           uint16_t* out16, float* y_save, float* rms_save, int dm,
+                                                           float eps) {
+    __shared__ float red[4];
+    const int64_t row = blockIdx.x;
+    const float* ar = a + row * dm;
+    float ss = 0.0f;
+    for (int i = 4 * threadIdx.x; i < dm; i += 1024) {
+        const float4 v = *reinterpret_cast<const float4*>(ar + i);
+        ss += v.x * v.x + v.y * v.y + v.z * v.z + v.w * v.w;
+    }
+    ss = block_sum(ss, red);
+    const float rms = sqrtf(ss / (float)dm + eps);
+    if (rms_save && threadIdx.x == 0) rms_save[row] = rms;
+    for (int i = 4 * threadIdx.x; i < dm; i += 1024) {
+        const float4 v = *reinterpret_cast<const float4*>(ar + i);
+        const float4 wv = *reinterpret_cast<const float4*>(w + i);
+        const float4 y = make_float4((v.x / rms) * wv.x, (v.y / rms) * wv.y, (v.z / rms) * wv.z, (v.w / rms) * wv.w);
+        if (y_save) *reinterpret_cast<float4*>(y_save + row * dm + i) = y;
+        float4 o = y;
+        if (res) {
+            const float4 r = *reinterpret_cast<const float4*>(res + row * dm + i);
+            o = make_float4(r.x + y.x, r.y + y.y, r.z + y.z, r.w + y.w);
+        }
+        *reinterpret_cast<float4*>(out + row * dm + i) = o;
+        if (out16) {
+            uint2 p;
+            p.x = pack_bf16x2(o.x, o.y);
+            p.y = pack_bf16x2(o.z, o.w);
+            *reinterpret_cast<uint2*>(out16 + row * dm + i) = p;
+        }
+    }
+}
+
+// act[r][i] = silu(gu[r][i]) * gu[r][hid + i]; fp32 or bf16 output (grid-stride over rows * hid / 4)
+template <bool kBF16>
+__global__ __launch_bounds__(256) void swiglu_kernel(const float* gu, void* act, int64_t rows, int hid) {
+    const int64_t n4 = rows * (hid / 4);
+    for (int64_t q = (int64_t)blockIdx.x * 256 + threadIdx.x; q < n4; q += (int64_t)gridDim.x * 256) {
+        const int64_t r = q / (hid / 4);
+        const int i = (int)(q - r * (hid / 4)) * 4;
+        const float4 g = *reinterpret_cast<const float4*>(gu + r * 2 * hid + i);
+        const float4 u = *reinterpret_cast<const float4*>(gu + r * 2 * hid + hid + i);
+        const float4 o = make_float4(g.x / (1.0f + expf(-g.x)) * u.x, g.y / (1.0f + expf(-g.y)) * u.y,
+                                     g.z / (1.0f + expf(-g.z)) * u.z, g.w / (1.0f + expf(-g.w)) * u.w);
+        if constexpr (kBF16) {
+            uint2 p;
+            p.x = pack_bf16x2(o.x, o.y);
+            p.y = pack_bf16x2(o.z, o.w);
+            *reinterpret_cast<uint2*>(static_cast<uint16_t*>(act) + r * hid + i) = p;
+        } else {
+            *reinterpret_cast<float4*>(static_cast<float*>(act) + r * hid + i) = o;
+        }
+    }
+}
+
+// One row of logits: target[row] >= 0 is the next token (a loss term), -1 none (no loss, zero gradient).
+// term[row] = log(sum exp(l - max)) - (l[target] - max); grad row (nullable) = (softmax - onehot) * inv_count.
+__global__ __launch_bounds__(256) void ce_rows_kernel(const float* logits, const int32_t* target, float* term,
+                                                      float* grad, int V, float inv_count) {
+    __shared__ float red_m[4], red_s[4];
+    const int64_t row = blockIdx.x;
+    const int tgt = target[row];
+    const float* l = logits + row * V;
+    float* g = grad ? grad + row * V : nullptr;
+    if (tgt < 0) {
+        if (threadIdx.x == 0) term[row] = 0.0f;
+        if (g)
+            for (int i = threadIdx.x; i < V; i += 256) g[i] = 0.0f;
+        return;
+    }
+    // online (max, sum of exp) per thread, then combined over the workgroup
+    float m = -__builtin_huge_valf(), s = 0.0f;
+    for (int i = threadIdx.x; i < V; i += 256) {
+        const float x = l[i];
+        if (x > m) {
+            s = s * expf(m - x) + 1.0f;
+            m = x;
+        } else {
+            s += expf(x - m);
+        }
+    }
+#pragma unroll
+    for (int off = 32; off >= 1; off >>= 1) {
+        const float m2 = __shfl_xor(m, off, 64), s2 = __shfl_xor(s, off, 64);
+        const float mm = fmaxf(m, m2);
+        s = (m == -__builtin_huge_valf() ? 0.0f : s * expf(m - mm)) + (m2 == -__builtin_huge_valf() ? 0.0f : s2 * expf(m2 - mm));
+        m = mm;
+    }
+    if ((threadIdx.x & 63) == 0) {
+        red_m[threadIdx.x >> 6] = m;
+        red_s[threadIdx.x >> 6] = s;
+    }
+    __syncthreads();
+    float mx = red_m[0];
+    for (int k = 1; k < 4; ++k) mx = fmaxf(mx, red_m[k]);
+    float se = 0.0f;
+    for (int k = 0; k < 4; ++k) se += red_s[k] * expf(red_m[k] - mx);
+    if (threadIdx.x == 0) term[row] = logf(se) - (l[tgt] - mx);
+    if (g) {
+        const float inv = 1.0f / se;
+        for (int i = threadIdx.x; i < V; i += 256) {
+            float p = expf(l[i] - mx) * inv;
+            if (i == tgt) p -= 1.0f;
+            g[i] = p * inv_count;
+        }
+    }
+}
+
+// loss = sum of the terms (fixed order, fp64) / count, one workgroup
+__global__ __launch_bounds__(256) void ce_reduce_kernel(const float* term, int64_t rows, float inv_count, float* loss) {
+    __shared__ double red[256];
+    double acc = 0.0;
+    for (int64_t i = threadIdx.x; i < rows; i += 256) acc += term[i];
+    red[threadIdx.x] = acc;
+    __syncthreads();
+    for (int w = 128; w >= 1; w >>= 1) {
+        if ((int)threadIdx.x < w) red[threadIdx.x] += red[threadIdx.x + w];
+        __syncthreads();
+    }
+    if (threadIdx.x == 0) loss[0] = (float)(red[0] * (double)inv_count);
+}
+
+// RMSNorm::backward for kRowsPerBlock rows per workgroup: c = mean(dy * y), n = y / w,
+// dx = (w * dy - n * c) / rms; this workgroup's column sums of dy * n go to partial[blockIdx.x][dm].
+// dx_add (nullable) is added to dx (the residual branch of the block's backward, OlmoBlock.cpp:28,32).
+constexpr int kRowsPerBlock = 16;
+__global__ __launch_bounds__(256) void rmsnorm_bwd_rows_kernel(const float* dy, const float* y, const float* rms,
+                                                               const float* w, const float* dx_add, float* dx,
+                                                               float* partial, int64_t rows, int dm) {
+    __shared__ float red[4];
+    __shared__ float cs[kRowsPerBlock];
+    const int64_t r0 = (int64_t)blockIdx.x * kRowsPerBlock;
+    const int nr = (int)min((int64_t)kRowsPerBlock, rows - r0);
+    for (int k = 0; k < nr; ++k) {
+        const int64_t row = r0 + k;
+        float acc = 0.0f;
+        for (int i = 4 * threadIdx.x; i < dm; i += 1024) {
+            const float4 g = *reinterpret_cast<const float4*>(dy + row * dm + i);
+            const float4 v = *reinterpret_cast<const float4*>(y + row * dm + i);
+            acc += g.x * v.x + g.y * v.y + g.z * v.z + g.w * v.w;
+        }
+        acc = block_sum(acc, red);
+        if (threadIdx.x == 0) cs[k] = acc / (float)dm;
+    }
+    __syncthreads();
+    for (int i = 4 * threadIdx.x; i < dm; i += 1024) {
+        const float4 wv = *reinterpret_cast<const float4*>(w + i);
+        float4 p = make_float4(0.f, 0.f, 0.f, 0.f);
+        for (int k = 0; k < nr; ++k) {
+            const int64_t row = r0 + k;
+            const float c = cs[k], inv = 1.0f / rms[row];
+            const float4 g = *reinterpret_cast<const float4*>(dy + row * dm + i);
+            const float4 v = *reinterpret_cast<const float4*>(y + row * dm + i);
+            const float4 n = make_float4(v.x / wv.x, v.y / wv.y, v.z / wv.z, v.w / wv.w);
+            float4 o = make_float4((wv.x * g.x - n.x * c) * inv, (wv.y * g.y - n.y * c) * inv,
+                                   (wv.z * g.z - n.z * c) * inv, (wv.w * g.w - n.w * c) * inv);
+            if (dx_add) {
+                const float4 e = *reinterpret_cast<const float4*>(dx_add + row * dm + i);
+                o = make_float4(o.x + e.x, o.y + e.y, o.z + e.z, o.w + e.w);
+            }
+            *reinterpret_cast<float4*>(dx + row * dm + i) = o;
+            p = make_float4(p.x + g.x * n.x, p.y + g.y * n.y, p.z + g.z * n.z, p.w + g.w * n.w);
+        }
+        *reinterpret_cast<float4*>(partial + (int64_t)blockIdx.x * dm + i) = p;
+    }
+}
+
+// grad[j] += sum over blocks of partial[b][j], in block order
+__global__ __launch_bounds__(256) void col_reduce_kernel(const float* partial, int nblk, int dm, float* grad) {
+    const int j = blockIdx.x * 256 + threadIdx.x;
+    if (j >= dm) return;
+    float s = 0.0f;
+    for (int b = 0; b < nblk; ++b) s += partial[(int64_t)b * dm + j];
+    grad[j] += s;
+}
+
+// from d_act and the saved [gate | up] rows: d_gu = [d_gate | d_up] (fp32 or bf16 output)
+template <bool kBF16>
+__global__ __launch_bounds__(256) void swiglu_bwd_kernel(const float* d_act, const float* gu, void* d_gu, int64_t rows,
+                                                         int hid) {
+    const int64_t n = rows * hid;
+    for (int64_t q = (int64_t)blockIdx.x * 256 + threadIdx.x; q < n; q += (int64_t)gridDim.x * 256) {
+        const int64_t r = q / hid;
+        const int i = (int)(q - r * hid);
+        const float da = d_act[q];
+        const float gate = gu[r * 2 * hid + i], up = gu[r * 2 * hid + hid + i];
+        const float sig = 1.0f / (1.0f + expf(-gate));
+        const float silu = gate * sig;
+        const float d_up = da * silu;
+        const float d_gate = da * up * sig * (1.0f + gate * (1.0f - sig));
+        if constexpr (kBF16) {
+            uint16_t* o = static_cast<uint16_t*>(d_gu);
+            const bf16x2 v = __builtin_convertvector((floatx2){d_gate, d_up}, bf16x2);
+            o[r * 2 * hid + i] = __builtin_bit_cast(uint32_t, v) & 0xffffu;
+            o[r * 2 * hid + hid + i] = __builtin_bit_cast(uint32_t, v) >> 16;
+        } else {
+            float* o = static_cast<float*>(d_gu);
+            o[r * 2 * hid + i] = d_gate;
+            o[r * 2 * hid + hid + i] = d_up;
+        }
+    }
+}
+
+// one workgroup per distinct token: E_grad[tok] += sum of dx rows pos[start[u]] .. pos[start[u+1]-1], in order
+__global__ __launch_bounds__(256) void embed_bwd_kernel(const float* dx, const int32_t* uniq, const int32_t* start,
+                                                        const int32_t* pos, float* g_embed, int dm) {
+    const int u = blockIdx.x;
+    const int64_t tok = uniq[u];
+    for (int i = 4 * threadIdx.x; i < dm; i += 1024) {
+        float4 acc = *reinterpret_cast<const float4*>(g_embed + tok * dm + i);
+        for (int k = start[u]; k < start[u + 1]; ++k) {
+            const float4 v = *reinterpret_cast<const float4*>(dx + (int64_t)pos[k] * dm + i);
+            acc = make_float4(acc.x + v.x, acc.y + v.y, acc.z + v.z, acc.w + v.w);
+        }
+        *reinterpret_cast<float4*>(g_embed + tok * dm + i) = acc;
+    }
+}
+
+// out = a + b (the block's residual gradient, OlmoBlock.cpp:32)
+__global__ __launch_bounds__(256) void add_kernel(const float* a, const float* b, float* out, int64_t n4) {
+    for (int64_t i = (int64_t)blockIdx.x * 256 + threadIdx.x; i < n4; i += (int64_t)gridDim.x * 256) {
+        const float4 x = reinterpret_cast<const float4*>(a)[i], y = reinterpret_cast<const float4*>(b)[i];
+        reinterpret_cast<float4*>(out)[i] = make_float4(x.x + y.x, x.y + y.y, x.z + y.z, x.w + y.w);
+    }
+}
+
+unsigned grid_for(int64_t n) {
+    int64_t b = (n + 255) / 256;
+    return (unsigned)(b < 1 ? 1 : (b > 16384 ? 16384 : b));
+}
+
+}  // namespace
+
+int launch_add(const float* a, const float* b, float* out, int64_t n, hipStream_t s) {
+    hipLaunchKernelGGL(add_kernel, dim3(grid_for(n / 4)), dim3(256), 0, s, a, b, out, n / 4);
+    DT_HIP_TRY(hipGetLastError());
+    return DT_OK;
+}
+
+int launch_embed_gather(const int32_t* tok, const float* E, float* x, int rows, int dm, hipStream_t s) {
+    hipLaunchKernelGGL(embed_gather_kernel, dim3(rows), dim3(256), 0, s, tok, E, x, dm);
+    DT_HIP_TRY(hipGetLastError());
+    return DT_OK;
+}
+
+int launch_rmsnorm_rows(const float* a, const float* w, const float* res, float* out, uint16_t* out16, float* y_save,
+                        float* rms_save, int rows, int dm, float eps, hipStream_t s) {
+    hipLaunchKernelGGL(rmsnorm_rows_kernel, dim3(rows), dim3(256), 0, s, a, w, res, out, out16, y_save, rms_save, dm,
+                       eps);
+    DT_HIP_TRY(hipGetLastError());
+    return DT_OK;
+}
+
+int launch_swiglu(const float* gu, void* act, int rows, int hid, int bf16, hipStream_t s) {
+    const unsigned g = grid_for((int64_t)rows * hid / 4);
+    if (bf16) hipLaunchKernelGGL(swiglu_kernel<true>, dim3(g), dim3(256), 0, s, gu, act, (int64_t)rows, hid);
+    else hipLaunchKernelGGL(swiglu_kernel<false>, dim3(g), dim3(256), 0, s, gu, act, (int64_t)rows, hid);
+    DT_HIP_TRY(hipGetLastError());
+    return DT_OK;
+}
+
+int launch_ce_loss(const float* logits, const int32_t* target, float* term, float* grad, float* loss, int rows, int V,
+                   int count, hipStream_t s) {
+    const float inv = count > 0 ? 1.0f / (float)count : 0.0f;
+    hipLaunchKernelGGL(ce_rows_kernel, dim3(rows), dim3(256), 0, s, logits, target, term, grad, V, inv);
+    DT_HIP_TRY(hipGetLastError());
+    hipLaunchKernelGGL(ce_reduce_kernel, dim3(1), dim3(256), 0, s, term, (int64_t)rows, inv, loss);
+    DT_HIP_TRY(hipGetLastError());
+    return DT_OK;
+}
+
+int rmsnorm_bwd_blocks(int rows) { return (rows + kRowsPerBlock - 1) / kRowsPerBlock; }
+
+int launch_rmsnorm_bwd(const float* dy, const float* y, const float* rms, const float* w, const float* dx_add,
+                       float* dx, float* partial, float* grad_w, int rows, int dm, hipStream_t s) {
+    const int nblk = rmsnorm_bwd_blocks(rows);
+    hipLaunchKernelGGL(rmsnorm_bwd_rows_kernel, dim3(nblk), dim3(256), 0, s, dy, y, rms, w, dx_add, dx, partial,
+                       (int64_t)rows, dm);
+    DT_HIP_TRY(hipGetLastError());
+    hipLaunchKernelGGL(col_reduce_kernel, dim3((dm + 255) / 256), dim3(256), 0, s, partial, nblk, dm, grad_w);
+    DT_HIP_TRY(hipGetLastError());
+    return DT_OK;
+}
+
+int launch_swiglu_bwd(const float* d_act, const float* gu, void* d_gu, int rows, int hid, int bf16, hipStream_t s) {
+    const unsigned g = grid_for((int64_t)rows * hid);
+    if (bf16) hipLaunchKernelGGL(swiglu_bwd_kernel<true>, dim3(g), dim3(256), 0, s, d_act, gu, d_gu, (int64_t)rows, hid);
+    else hipLaunchKernelGGL(swiglu_bwd_kernel<false>, dim3(g), dim3(256), 0, s, d_act, gu, d_gu, (int64_t)rows, hid);
+    DT_HIP_TRY(hipGetLastError());
+    return DT_OK;
+}
+
+int launch_embed_bwd(const float* dx, const int32_t* uniq, const int32_t* start, const int32_t* pos, int n_uniq,
+                     float* g_embed, int dm, hipStream_t s) {
+    if (n_uniq == 0) return DT_OK;
+    hipLaunchKernelGGL(embed_bwd_kernel, dim3(n_uniq), dim3(256), 0, s, dx, uniq, start, pos, g_embed, dm);
+    DT_HIP_TRY(hipGetLastError());
+    return DT_OK;
+}
+
+}  // namespace dt

@@ -190,6 +190,59 @@ int dt_attn_layer_get_weights(dt_attn_layer* layer, float* wq, float* wk, float*
 int dt_attn_layer_get_grads(dt_attn_layer* layer, float* d_wq, float* d_wk, float* d_wv, float* d_wo,
                             float* d_q_norm_w, float* d_k_norm_w, int mem, void* stream);
 
+/*
+ * OLMo-2 model (replaces class OlmoModel, OlmoModel.h:14-34, with its OlmoBlock,
+ * OlmoMlp, RMSNorm and OlmoLmHead members). Parameters are named by the
+ * reference's .npy file stems without the extension: "model.embed_tokens.weight",
+ * "model.layers.{i}.self_attn.{q,k,v,o}_proj.weight",
+ * "model.layers.{i}.self_attn.{q,k}_norm.weight",
+ * "model.layers.{i}.post_attention_layernorm.weight",
+ * "model.layers.{i}.mlp.{gate,up,down}_proj.weight",
+ * "model.layers.{i}.post_feedforward_layernorm.weight", "model.norm.weight",
+ * "lm_head.weight" (shapes [out][in] as in the files).
+ *
+ * dt_model_create makes a zero-initialised model of the given sizes (d_model =
+ * n_heads * 128); dt_model_set_param / dt_model_get_param copy one parameter
+ * (or, with grad = 1, its accumulated gradient) in or out. dt_model_load is
+ * the OlmoModel(folder) constructor (OlmoModel.cpp:12-23): it reads every
+ * "{folder}/{name}.npy" for n_layers blocks (the reference's n_layers = 16,
+ * model_config.h:7).
+ */
+typedef struct dt_model dt_model;
+int dt_model_create(dt_ctx* ctx, int n_layers, int d_model, int n_heads, int hidden, int vocab, dt_model** out);
+int dt_model_load(dt_ctx* ctx, const char* folder, int n_layers, dt_model** out);
+int dt_model_destroy(dt_model* model);
+int dt_model_set_param(dt_model* model, const char* name, const float* data, int64_t count, int mem);
+int dt_model_get_param(dt_model* model, const char* name, float* out, int64_t count, int grad, int mem,
+                       void* stream);
+
+/*
+ * OlmoModel::forward (OlmoModel.cpp:25-48): tokens [B, T] (a host array, like
+ * seq_lens; every id in [0, vocab)) -> logits [B, T, vocab] fp32. dtype selects
+ * the attention-core mode and the GEMM precision as for dt_attn_layer_fwd.
+ * save_for_backward = 1 keeps each block's state for dt_model_bwd.
+ */
+int dt_model_fwd(dt_model* model, const int32_t* tokens, int B, int T, float* logits, int dtype, int mem,
+                 int save_for_backward, void* stream);
+
+/* OlmoModel::backward (OlmoModel.cpp:50-67) for the last saved forward: d_logits
+ * [B, T, vocab] fp32; accumulates (+=) every parameter's gradient. */
+int dt_model_bwd(dt_model* model, const float* d_logits, int mem, void* stream);
+
+/* OlmoModel::step / zero_grad (OlmoModel.cpp:69-83): w -= lr * grad; grads = 0. */
+int dt_model_step(dt_model* model, float lr, void* stream);
+int dt_model_zero_grad(dt_model* model, void* stream);
+
+/*
+ * ce_loss (CrossEntropyLoss.cpp:8-43): the mean next-token cross entropy of
+ * logits [B, T, V] against tokens[b][s+1] (a host array), skipping targets equal
+ * to ignore_index; *loss is written to host memory. d_logits (nullable)
+ * receives the gradient main.cpp:62-80 builds from it: (softmax - onehot) /
+ * count at the positions with a target, 0 elsewhere.
+ */
+int dt_ce_loss(dt_ctx* ctx, const float* logits, const int32_t* tokens, int B, int T, int V, int ignore_index,
+               float* loss, float* d_logits, int mem, void* stream);
+
 #ifdef __cplusplus
 }
 #endif
