@@ -67,8 +67,6 @@ struct dt_model {
     float* g_final = nullptr;
     float* g_lm = nullptr;
     DeviceBuffer d16, dx, dh, da, dxa, dm_, d_act, d_gu, partial, csr;
-    // loss workspace
-    DeviceBuffer target, term, loss;
 };
 
 namespace {
@@ -257,8 +255,7 @@ int dt_model_destroy(dt_model* M) {
             b->release();
     }
     for (DeviceBuffer* b : {&M->tok, &M->x, &M->x2, &M->yf, &M->yf16, &M->rmsf, &M->logits, &M->d16, &M->dx, &M->dh,
-                            &M->da, &M->dxa, &M->dm_, &M->d_act, &M->d_gu, &M->partial, &M->csr, &M->target, &M->term,
-                            &M->loss})
+                            &M->da, &M->dxa, &M->dm_, &M->d_act, &M->d_gu, &M->partial, &M->csr})
         b->release();
     delete M;
     return DT_OK;
@@ -360,7 +357,7 @@ int dt_model_fwd(dt_model* M, const int32_t* tokens, int B, int T, float* logits
     M->saved_T = 0;
     if (bf) DT_TRY(refresh_bf16(M, s));
 
-    // embedding (OlmoModel.cpp:29-38); the token array is staged through pinned-free host memory
+    // embedding (OlmoModel.cpp:29-38)
     DT_TRY(M->tok.ensure(rows * 4));
     DT_HIP_TRY(hipMemcpyAsync(M->tok.ptr, tokens, rows * 4, hipMemcpyHostToDevice, s));
     DT_TRY(M->x.ensure(act * 4));
@@ -477,7 +474,7 @@ int dt_model_bwd(dt_model* M, const float* d_logits, int mem, void* stream) {
     float* partial = static_cast<float*>(M->partial.ptr);
     uint16_t* d16 = static_cast<uint16_t*>(M->d16.ptr);
 
-    // LM head (OlmoLmHead.cpp:30-61): dW += d_logits^T y; d_y = d_logits W
+    // LM head (OlmoLmHead.cpp:30-62): dW += d_logits^T y; d_y = d_logits W
     float* d_yf = da;
     if (bf) {
         DT_TRY(launch_f32_to_bf16(gl, d16, (int64_t)rows * V, s));
@@ -487,11 +484,10 @@ int dt_model_bwd(dt_model* M, const float* d_logits, int mem, void* stream) {
         DT_TRY(gemm_rm(ctx, s, true, false, V, dm, rows, gl, V, M->yf.ptr, dm, 1.0f, M->g_lm, dm, false));
         DT_TRY(gemm_rm(ctx, s, false, false, rows, dm, V, gl, V, M->lm_head, dm, 0.0f, d_yf, dm, false));
     }
-    // final norm (OlmoModel.cpp:52): RMSNorm::backward, y recomputed here from the saved final stream
-    // (the forward kept yf, rms), x = the final residual stream
+    // final norm (OlmoModel.cpp:52): RMSNorm::backward from the saved output y and rms
     DT_TRY(launch_rmsnorm_bwd(d_yf, static_cast<const float*>(M->yf.ptr), static_cast<const float*>(M->rmsf.ptr),
                               M->final_norm, nullptr, dx, partial, M->g_final, rows, dm, s));
-    // blocks in reverse (OlmoBlock.cpp:24-33)
+    // blocks in reverse (OlmoBlock.cpp:23-30)
     for (int li = M->n_layers - 1; li >= 0; --li) {
         ModelLayer& Ly = M->L[li];
         // d_m = N_pf.backward(d_x)
@@ -519,7 +515,7 @@ int dt_model_bwd(dt_model* M, const float* d_logits, int mem, void* stream) {
         DT_TRY(dt_attn_layer_bwd(Ly.attn, da, dxa, B, T, DT_MEM_DEVICE, stream));
         DT_TRY(launch_add(dxa, dh, dx, (int64_t)act, s));
     }
-    // embedding (OlmoModel.cpp:60-66): per distinct token, its positions in order (CSR built here)
+    // embedding (OlmoModel.cpp:57-66): per distinct token, its positions in order (CSR built here)
     std::vector<int32_t> order(rows);
     for (int i = 0; i < rows; ++i) order[i] = i;
     const std::vector<int32_t>& tk = M->saved_tokens;
@@ -556,7 +552,7 @@ int dt_model_step(dt_model* M, float lr, void* stream) {
     // OlmoModel.cpp:69-75
     DT_TRY(launch_sgd(M->embed, M->g_embed, lr, V * dm, s));
     for (ModelLayer& Ly : M->L) {
-        DT_TRY(dt_attn_layer_step(Ly.attn, lr, stream));  // OlmoBlock.cpp:36-41
+        DT_TRY(dt_attn_layer_step(Ly.attn, lr, stream));  // OlmoBlock.cpp:32-37
         DT_TRY(launch_sgd(Ly.w_pa, Ly.g_pa, lr, dm, s));
         DT_TRY(launch_sgd(Ly.w_gu, Ly.g_gu, lr, 2 * hid * dm, s));
         DT_TRY(launch_sgd(Ly.w_down, Ly.g_down, lr, dm * hid, s));

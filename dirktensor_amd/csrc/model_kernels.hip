@@ -11,7 +11,7 @@
 //                       deterministically through per-workgroup partial sums
 //   swiglu_bwd          OlmoMlp.cpp (backward): d_up = d_act * silu(gate),
 //                       d_gate = d_act * up * sig * (1 + gate * (1 - sig))
-//   embed_bwd           OlmoModel.cpp:60-66: E_grad[token] += dx rows, summed per distinct token in
+//   embed_bwd           OlmoModel.cpp:57-66: E_grad[token] += dx rows, summed per distinct token in
 //                       position order (no atomics)
 // All are HBM bound; one workgroup of 256 threads per row unless noted.
 

@@ -54,6 +54,7 @@ def lib() -> ctypes.CDLL:
         l.oracle_model_forward.argtypes = [_vp] * 6 + [_i] * 6 + [_f, _i]
         l.oracle_ce_loss.argtypes = [_vp, _vp, _i, _i, _i, _i, _vp, _vp]
         l.oracle_ce_loss.restype = _f
+        l.oracle_model_backward.argtypes = [_vp] * 10 + [_i] * 6 + [_f, _i]
         _lib = l
     return _lib
 
@@ -273,3 +274,30 @@ def ce_loss(logits, tokens, ignore_index: int, with_grad: bool = False):
     cnt = ctypes.c_int(0)
     loss = lib().oracle_ce_loss(_p(logits), _p(tok), B, T, V, int(ignore_index), _p(g), ctypes.byref(cnt))
     return (float(loss), g) if with_grad else float(loss)
+
+
+def _layer_ptrs(arrays: dict, n_layers: int):
+    ptrs = (_vp * (n_layers * len(LAYER_PARAMS)))()
+    for i in range(n_layers):
+        for j, name in enumerate(LAYER_PARAMS):
+            ptrs[i * len(LAYER_PARAMS) + j] = arrays[f"model.layers.{i}.{name}.weight"].ctypes.data
+    return ptrs
+
+
+def model_backward(tokens, params: dict, d_logits, *, eps: float = 1e-6, nthreads: int | None = None) -> dict:
+    """OlmoModel::backward (OlmoModel.cpp:50-67) after a forward on ``tokens``: the gradient of every parameter
+    (accumulated from zero), keyed like ``params``."""
+    tok = np.ascontiguousarray(tokens, dtype=np.int32)
+    B, T = tok.shape
+    p = {k: _c32(v) for k, v in params.items()}
+    V, dm = p["model.embed_tokens.weight"].shape
+    n_layers = sum(1 for k in p if k.endswith(".mlp.up_proj.weight"))
+    hid = p["model.layers.0.mlp.up_proj.weight"].shape[0]
+    g = {k: np.zeros_like(v) for k, v in p.items()}
+    dl = _c32(d_logits)
+    lib().oracle_model_backward(_p(tok), _p(p["model.embed_tokens.weight"]), ctypes.cast(_layer_ptrs(p, n_layers), _vp),
+                                _p(p["model.norm.weight"]), _p(p["lm_head.weight"]), _p(dl),
+                                _p(g["model.embed_tokens.weight"]), ctypes.cast(_layer_ptrs(g, n_layers), _vp),
+                                _p(g["model.norm.weight"]), _p(g["lm_head.weight"]), B, T, dm, hid, V, n_layers,
+                                float(eps), nthreads or default_threads())
+    return g

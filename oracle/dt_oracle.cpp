@@ -26,6 +26,8 @@
 //                                  blocks, final norm, LM head OlmoLmHead.cpp:11-28)
 //   oracle_ce_loss                CrossEntropyLoss.cpp:8-43 and main.cpp:62-80 (loss with
 //                                  ignore_index, and the softmax - onehot gradient / count)
+//   oracle_model_backward         OlmoModel.cpp:50-67, OlmoBlock.cpp:23-30, OlmoMlp.cpp (backward),
+//                                  OlmoLmHead.cpp:30-62 (all parameter gradients)
 //
 // Parity pins (checked in tests/test_oracle_pins.py): an fp64 full-softmax attention
 // written independently in numpy, torch's scaled_dot_product_attention in fp64,
@@ -659,6 +661,78 @@ float oracle_ce_loss(const float* logits, const int32_t* tokens, int B, int T, i
     }
     if (count_out) *count_out = count;
     return count > 0 ? (float)(total / count) : 0.0f;
+}
+
+
+// OlmoModel::backward, OlmoModel.cpp:50-67, after a forward on tokens (recomputed here, keeping what the
+// reference's layers save). d_logits [B][T][V]. grads: the same pointer layout as the parameters
+// (embed, n_layers * 11 in the order above, final_norm, lm_head), accumulated (+=).
+//   LM head (OlmoLmHead.cpp:30-62): dW += d^T y_final, d_y = d W
+//   final norm, then per block in reverse (OlmoBlock.cpp:23-30): d_m = N_pf'(d), MLP backward
+//   (OlmoMlp.cpp:65-160: dWdown += d_m^T act, d_act = d_m Wdown, d_up = d_act silu(gate),
+//   d_gate = d_act up sig (1 + gate (1 - sig)), dWgate += d_gate^T h, dWup += d_up^T h,
+//   d_h = d_gate Wgate + d_up Wup + d), d_a = N_pa'(d_h), d = attn'(d_a) + d_h
+//   embedding (OlmoModel.cpp:57-66): grad[token] += d rows
+void oracle_model_backward(const int32_t* tokens, const float* embed, const float* const* layers,
+                           const float* final_norm, const float* lm_head, const float* d_logits, float* g_embed,
+                           float* const* g_layers, float* g_final_norm, float* g_lm_head, int B, int T, int dm,
+                           int hid, int V, int n_layers, float eps, int nthreads) {
+    const int rows = B * T, H = dm / 128;
+    const size_t n = (size_t)rows * dm, nh = (size_t)rows * hid;
+    std::vector<float> sin_t((size_t)T * 128), cos_t((size_t)T * 128);
+    oracle_rope_tables(sin_t.data(), cos_t.data(), T, 128, 500000.0f);
+    // forward with saved state
+    std::vector<std::vector<float>> xin(n_layers, std::vector<float>(n)), ypa(n_layers, std::vector<float>(n)),
+        h(n_layers, std::vector<float>(n)), ypf(n_layers, std::vector<float>(n)), gate(n_layers, std::vector<float>(nh)),
+        up(n_layers, std::vector<float>(nh)), act(n_layers, std::vector<float>(nh));
+    std::vector<std::vector<float>> rpa(n_layers, std::vector<float>(rows)), rpf(n_layers, std::vector<float>(rows));
+    std::vector<float> x(n), a(n), m(n), yf(n), rf(rows);
+    for (int r = 0; r < rows; ++r) std::memcpy(&x[(size_t)r * dm], embed + (int64_t)tokens[r] * dm, dm * sizeof(float));
+    for (int i = 0; i < n_layers; ++i) {
+        const float* const* p = layers + (size_t)i * kLayerParams;
+        xin[i] = x;
+        oracle_attention_layer_forward(x.data(), p[0], p[1], p[2], p[3], p[4], p[5], sin_t.data(), cos_t.data(),
+                                       a.data(), B, T, H, 128, eps, nthreads, nullptr, nullptr, nullptr, nullptr,
+                                       nullptr, nullptr);
+        oracle_rmsnorm_forward(a.data(), p[6], ypa[i].data(), rpa[i].data(), rows, dm, eps);
+        for (size_t j = 0; j < n; ++j) h[i][j] = x[j] + ypa[i][j];
+        oracle_mlp_forward(h[i].data(), p[7], p[8], p[9], m.data(), rows, dm, hid, nthreads, gate[i].data(),
+                           up[i].data(), act[i].data());
+        oracle_rmsnorm_forward(m.data(), p[10], ypf[i].data(), rpf[i].data(), rows, dm, eps);
+        for (size_t j = 0; j < n; ++j) x[j] = h[i][j] + ypf[i][j];
+    }
+    oracle_rmsnorm_forward(x.data(), final_norm, yf.data(), rf.data(), rows, dm, eps);
+    // LM head and final norm
+    oracle_sgemm_tn_acc(V, dm, rows, d_logits, V, yf.data(), dm, g_lm_head, dm, nthreads);
+    std::vector<float> dy(n), d(n), dmo(n), dh(n), da(n), dxa(n), d_act(nh), d_gate(nh), d_up(nh), t1(n);
+    oracle_sgemm_nn(rows, dm, V, d_logits, V, lm_head, dm, dy.data(), dm, nthreads);
+    oracle_rmsnorm_backward(dy.data(), yf.data(), rf.data(), final_norm, d.data(), g_final_norm, rows, dm);
+    for (int i = n_layers - 1; i >= 0; --i) {
+        const float* const* p = layers + (size_t)i * kLayerParams;
+        float* const* g = g_layers + (size_t)i * kLayerParams;
+        oracle_rmsnorm_backward(d.data(), ypf[i].data(), rpf[i].data(), p[10], dmo.data(), g[10], rows, dm);
+        oracle_sgemm_tn_acc(dm, hid, rows, dmo.data(), dm, act[i].data(), hid, g[9], hid, nthreads);
+        oracle_sgemm_nn(rows, hid, dm, dmo.data(), dm, p[9], hid, d_act.data(), hid, nthreads);
+        for (size_t j = 0; j < nh; ++j) {
+            const float ga = gate[i][j], sig = 1.0f / (1.0f + std::exp(-ga));
+            d_up[j] = d_act[j] * (ga * sig);
+            d_gate[j] = d_act[j] * up[i][j] * sig * (1.0f + ga * (1.0f - sig));
+        }
+        oracle_sgemm_tn_acc(hid, dm, rows, d_gate.data(), hid, h[i].data(), dm, g[7], dm, nthreads);
+        oracle_sgemm_tn_acc(hid, dm, rows, d_up.data(), hid, h[i].data(), dm, g[8], dm, nthreads);
+        oracle_sgemm_nn(rows, dm, hid, d_gate.data(), hid, p[7], dm, dh.data(), dm, nthreads);
+        oracle_sgemm_nn(rows, dm, hid, d_up.data(), hid, p[8], dm, t1.data(), dm, nthreads);
+        for (size_t j = 0; j < n; ++j) dh[j] += t1[j] + d[j];
+        oracle_rmsnorm_backward(dh.data(), ypa[i].data(), rpa[i].data(), p[6], da.data(), g[6], rows, dm);
+        oracle_attention_layer_backward(xin[i].data(), p[0], p[1], p[2], p[3], p[4], p[5], sin_t.data(),
+                                        cos_t.data(), da.data(), dxa.data(), g[0], g[1], g[2], g[3], g[4], g[5], B, T,
+                                        H, 128, eps, nthreads);
+        for (size_t j = 0; j < n; ++j) d[j] = dxa[j] + dh[j];
+    }
+    for (int r = 0; r < rows; ++r) {
+        float* dst = g_embed + (int64_t)tokens[r] * dm;
+        for (int c = 0; c < dm; ++c) dst[c] += d[(size_t)r * dm + c];
+    }
 }
 
 }  // extern "C"

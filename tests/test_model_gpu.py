@@ -74,3 +74,52 @@ def test_model_loss_full_vocab_shape(gpu):
     tok = synth.model_tokens(1, 12, V, seed=6302)
     ref = oracle.ce_loss(logits, tok, 100277)
     assert abs(ce_loss(torch.from_numpy(logits).to(gpu), tok, 100277) - ref) <= 1e-5 * abs(ref)
+
+
+@pytest.mark.parametrize("mode,tol", [("fp32", TOL_FP32), ("bf16", TOL_BF16)])
+def test_model_backward(gpu, params, mode, tol):
+    """OlmoModel::backward (OlmoModel.cpp:50-67): every parameter gradient against the oracle."""
+    B, T = 1, 48
+    tok = synth.model_tokens(B, T, VOCAB, seed=6401)
+    G = synth.normal(6402, (B, T, VOCAB), 0.0, 1e-3)
+    ref = oracle.model_backward(tok, params, G)
+    model = OlmoModel.from_params(params)
+    model.forward(tok, mode=mode)
+    model.backward(torch.from_numpy(G).to(gpu))
+    errs = {k: rel_err(model.grad(k), ref[k]) for k in params}
+    worst = sorted(errs.items(), key=lambda kv: -kv[1])[:4]
+    print(f"model backward {mode}: worst " + ", ".join(f"{k} {v:.2e}" for k, v in worst))
+    assert max(errs.values()) <= tol, worst
+
+
+def test_train_step_like_main_cpp(gpu, params):
+    """main.cpp:59-91: forward, ce_loss, its gradient, backward, step(1e-4), zero_grad, forward again; a
+    right-padded batch (pad = the ignore index). Losses and updated weights against the oracle."""
+    B, T, lr = 2, 40, 1e-4
+    tok = synth.model_tokens(B, T, VOCAB, seed=6501)
+    tok[1, 30:] = PAD
+    model = OlmoModel.from_params(params)
+    logits = model.forward(tok, mode="fp32")
+    loss1, g = ce_loss(logits, tok, PAD, with_grad=True)
+    ref_logits = oracle.model_forward(tok, params)
+    ref_loss1, ref_g = oracle.ce_loss(ref_logits, tok, PAD, with_grad=True)
+    assert abs(loss1 - ref_loss1) <= 1e-4 * abs(ref_loss1)
+    model.backward(g)
+    grads = {k: model.grad(k) for k in params}
+    ref_grads = oracle.model_backward(tok, params, ref_g)
+    for k in params:
+        assert rel_err(grads[k], ref_grads[k]) <= TOL_FP32, k
+    before = {k: model.param(k) for k in ("lm_head.weight", "model.layers.1.mlp.down_proj.weight",
+                                          "model.layers.0.self_attn.q_norm.weight", "model.embed_tokens.weight")}
+    model.step(lr)
+    for k, w in before.items():
+        expect = w - np.float32(lr) * grads[k]
+        assert np.array_equal(model.param(k), expect), k
+    model.zero_grad()
+    assert all(np.count_nonzero(model.grad(k)) == 0 for k in ("lm_head.weight", "model.layers.0.mlp.up_proj.weight"))
+    loss2 = ce_loss(model.forward(tok, mode="fp32"), tok, PAD)
+    updated = {k: model.param(k) for k in params}
+    ref_loss2 = oracle.ce_loss(oracle.model_forward(tok, updated), tok, PAD)
+    print(f"loss {loss1:.6f} -> {loss2:.6f} (oracle {ref_loss1:.6f} -> {ref_loss2:.6f})")
+    assert abs(loss2 - ref_loss2) <= 1e-4 * abs(ref_loss2)
+    assert loss2 < loss1

@@ -395,6 +395,19 @@ def pin_model_hf():
     return rel(logits, ref) <= 1e-4
 
 
+def pin_model_bwd_hf():
+    """OlmoModel::backward: every parameter gradient against torch autograd through HF's Olmo2ForCausalLM."""
+    n_layers, vocab, hidden, T = 2, 300, 512, 16
+    p = _small_model(n_layers, vocab, hidden)
+    tok = synth.model_tokens(1, T, vocab, seed=5903)
+    G = synth.normal(5904, (1, T, vocab))
+    grads = oracle.model_backward(tok, p, G)
+    model = _hf_model(p, n_layers, vocab, hidden)
+    (model(torch.from_numpy(tok).long()).logits * torch.from_numpy(G).double()).sum().backward()
+    named = dict(model.named_parameters())
+    return all(rel(grads[k], named[k].grad.numpy()) <= 1e-4 for k in p)
+
+
 def pin_ce_torch():
     """ce_loss and main.cpp's gradient against F.cross_entropy(ignore_index) and its autograd in fp64."""
     B, T, V, pad = 3, 17, 50, 7
@@ -432,6 +445,7 @@ PINS = {
     "layer_bwd_hf": pin_layer_bwd_hf,
     "mlp_torch": pin_mlp_torch,
     "model_hf": pin_model_hf,
+    "model_bwd_hf": pin_model_bwd_hf,
     "ce_torch": pin_ce_torch,
 }
 
@@ -454,7 +468,7 @@ MUTATIONS = {
     9: ["rope_bwd_adjoint", "rope_bwd_autograd", "layer_bwd_hf"],                            # forward rotation
     10: ["rmsnorm_bwd_autograd", "layer_bwd_hf"],                                            # c term dropped
     11: ["flash_bwd_autograd_causal", "flash_bwd_finite_difference"],                        # 1 / l dropped
-    12: ["mlp_torch", "model_hf"],                                                           # SiLU without sigmoid
+    12: ["mlp_torch", "model_hf", "model_bwd_hf"],                                           # SiLU without sigmoid
     13: ["model_hf"],                                                                         # pre-norm blocks
     14: ["ce_torch"],                                                                         # pad targets counted
 }
