@@ -25,6 +25,11 @@ Other workloads (each prints one line of the same shape):
   layer_train  forward with saved state + OlmoAttention::backward + step at the
                same shape; work 3x the projections' and 3.5x the attention
                core's forward work
+  model_fwd    OlmoModel::forward end to end (OlmoModel.cpp:25-48): 16 layers,
+               d_model 2048, MLP 8192, vocab 100352, tokens [1, 2048] (seed
+               5001); work 16*(8*T*d^2 + 6*T*d*8192 + attention) + 2*T*d*V
+  model_train  main.cpp's step for one batch: forward, ce_loss and its
+               gradient, OlmoModel::backward, step
 """
 
 from __future__ import annotations
@@ -128,8 +133,8 @@ def main() -> int:
     ap.add_argument("--warmup", type=int, default=500)
     ap.add_argument("--T", type=int, default=4096)
     ap.add_argument("--mode", choices=["bf16", "fp32"], default="bf16")
-    ap.add_argument("--workload", choices=["flash_fwd", "flash_bwd", "ragged_fwd", "layer_fwd", "layer_train"],
-                    default="flash_fwd")
+    ap.add_argument("--workload", choices=["flash_fwd", "flash_bwd", "ragged_fwd", "layer_fwd", "layer_train",
+                                           "model_fwd", "model_train"], default="flash_fwd")
     ap.add_argument("--cpu-budget", type=float, default=10.0, help="seconds of CPU-baseline timing (0 = skip)")
     ap.add_argument("--copy-mib", type=int, default=0,
                     help="instead of attention, time a plain copy kernel over this many MiB (counter calibration)")
@@ -453,8 +458,125 @@ def wl_layer_train(args, dev, stream, ctx):
                         "B": 1, "T": T, "d_model": d, "H": H, "D": D})
 
 
+def _model_setup(args, dev, n_layers=16, vocab=100352, hidden=8192, d=2048):
+    """The end-to-end model at the OLMo-2-1B shape with weights drawn on the device (seeded torch.Generator:
+    matrices ~ N(0, 0.02) rounded to bf16, norm weights ~ 1 + N(0, 0.01)); host copies for the oracle."""
+    import ctypes
+
+    import torch
+
+    import dirktensor_amd as dt
+    from dirktensor_amd import OlmoModel, _capi, synth
+
+    gen = torch.Generator(device=dev)
+    gen.manual_seed(5100)
+    ctx = dt.default_context(0)
+    h = ctypes.c_void_p()
+    _capi.call("dt_model_create", ctx.handle, n_layers, d, d // 128, hidden, vocab, ctypes.byref(h))
+    model = OlmoModel(ctx=ctx, _handle=h, _dims=(n_layers, d, hidden, vocab))
+    shapes = {"self_attn.q_proj": (d, d), "self_attn.k_proj": (d, d), "self_attn.v_proj": (d, d),
+              "self_attn.o_proj": (d, d), "self_attn.q_norm": (d,), "self_attn.k_norm": (d,),
+              "post_attention_layernorm": (d,), "mlp.gate_proj": (hidden, d), "mlp.up_proj": (hidden, d),
+              "mlp.down_proj": (d, hidden), "post_feedforward_layernorm": (d,)}
+    names = [("model.embed_tokens.weight", (vocab, d))]
+    for i in range(n_layers):
+        names += [(f"model.layers.{i}.{n}.weight", shp) for n, shp in shapes.items()]
+    names += [("model.norm.weight", (d,)), ("lm_head.weight", (vocab, d))]
+    host = {}
+    for name, shp in names:
+        if len(shp) == 1:
+            w = 1.0 + 0.01 * torch.randn(shp, generator=gen, device=dev)
+        else:
+            w = (0.02 * torch.randn(shp, generator=gen, device=dev)).bfloat16().float()
+        torch.cuda.synchronize()
+        _capi.call("dt_model_set_param", model.handle, name.encode(), w.data_ptr(), w.numel(), _capi.DT_MEM_DEVICE)
+        host[name] = w.cpu().numpy()
+        del w
+    T = args.T if args.T != 4096 else 2048  # the end-to-end workload is quoted at T = 2048
+    tok = synth.model_tokens(1, T, vocab)
+    return model, host, tok, T
+
+
+def _model_flops(T, n_layers=16, vocab=100352, hidden=8192, d=2048, H=16, D=128):
+    gemm = n_layers * (8 * T * d * d + 6 * T * d * hidden) + 2 * T * d * vocab
+    attn = n_layers * algorithmic_flops(1, T, H, D)
+    return gemm, attn
+
+
+def wl_model_fwd(args, dev, stream, ctx):
+    import torch
+
+    import oracle
+
+    model, host, tok, T = _model_setup(args, dev)
+    logits = torch.empty((1, T, model.vocab), dtype=torch.float32, device=dev)
+    gemm, attn = _model_flops(T)
+    box = {}
+
+    def step():
+        model.forward(tok, mode=args.mode, save_for_backward=False, out=logits)
+
+    def run_oracle():  # one full forward on the host; its time is the CPU baseline's sample
+        threads, _ = _threads(16)
+        t0 = time.perf_counter()
+        box["ref"] = oracle.model_forward(tok, host, nthreads=threads)
+        box["cpu_s"] = time.perf_counter() - t0
+
+    def parity():
+        if "ref" not in box:
+            run_oracle()
+        return _rel(logits.cpu().numpy(), box["ref"])
+
+    def cpu(budget):
+        threads, cores = _threads(16)
+        if "cpu_s" not in box:
+            run_oracle()
+        sec = box["cpu_s"]
+        return {"value": (gemm + attn) / sec / 1e12, "unit": "TFLOP/s", "cores": threads, "kind": "port",
+                "sample": f"oracle OlmoModel::forward fp32, 16 layers, tokens [1,{T}], vocab 100352, one full run "
+                f"({sec:.1f} s), {threads} threads of {cores} usable"}
+
+    return dict(step=step, flops=gemm + attn, tokens=T, parity=parity, cpu=cpu,
+                metric=f"end-to-end prefill tok/s + TFLOP/s, OLMo-2-1B (16 layers, vocab 100352) T={T}",
+                data="synthetic (tokens ~ U[0,100352) seed 5001; weights drawn on the device, torch.Generator seed "
+                     "5100: matrices N(0,0.02) rounded to bf16, norms 1+N(0,0.01))",
+                config={"workload": f"OlmoModel forward, tokens [1,{T}], {args.mode}", "B": 1, "T": T,
+                        "n_layers": 16, "d_model": 2048, "vocab": 100352, "hidden": 8192})
+
+
+def wl_model_train(args, dev, stream, ctx):
+    import torch
+
+    from dirktensor_amd import ce_loss
+
+    model, host, tok, T = _model_setup(args, dev)
+    logits = torch.empty((1, T, model.vocab), dtype=torch.float32, device=dev)
+    gemm, attn = _model_flops(T)
+    box = {}
+
+    def step():  # main.cpp:59-91 for one batch: forward, loss and its gradient, backward, step
+        model.zero_grad()
+        model.forward(tok, mode=args.mode, save_for_backward=True, out=logits)
+        box["loss"], g = ce_loss(logits, tok, 100277, with_grad=True)
+        model.backward(g)
+        model.step(0.0)  # lr 0 keeps the weights (and so the timed work) fixed across steps
+
+    def parity():
+        import oracle
+
+        ref = oracle.ce_loss(oracle.model_forward(tok, host, nthreads=_threads(16)[0]), tok, 100277)
+        return abs(box["loss"] - ref) / abs(ref)
+
+    return dict(step=step, flops=3 * gemm + 7 * attn // 2, tokens=T, parity=parity, cpu=lambda budget: None,
+                metric=f"end-to-end train step tok/s + TFLOP/s, OLMo-2-1B (16 layers, vocab 100352) T={T}",
+                data="synthetic (as the model_fwd workload)",
+                config={"workload": f"OlmoModel forward + ce_loss + backward + step, tokens [1,{T}], {args.mode}",
+                        "B": 1, "T": T, "n_layers": 16, "d_model": 2048, "vocab": 100352, "hidden": 8192})
+
+
 WORKLOADS = {"flash_fwd": wl_flash_fwd, "flash_bwd": wl_flash_bwd, "ragged_fwd": wl_ragged_fwd,
-             "layer_fwd": wl_layer_fwd, "layer_train": wl_layer_train}
+             "layer_fwd": wl_layer_fwd, "layer_train": wl_layer_train, "model_fwd": wl_model_fwd,
+             "model_train": wl_model_train}
 
 
 if __name__ == "__main__":
