@@ -56,7 +56,6 @@ typedef float floatx2 __attribute__((ext_vector_type(2)));
 typedef short shortx4 __attribute__((ext_vector_type(4)));
 typedef short shortx8 __attribute__((ext_vector_type(8)));
 typedef __attribute__((address_space(3))) shortx4 lds_shortx4;
-typedef __attribute__((address_space(3))) void lds_void;
 
 constexpr int kD = 128;
 constexpr int kTile = 64;                      // rows per streamed tile
@@ -145,18 +144,34 @@ __device__ __forceinline__ void dma_offsets(uint32_t (&voff)[4], int lane, int w
 #pragma unroll
     for (int i = 0; i < 4; ++i) voff[i] = (uint32_t)(((16 * i + 4 * wave + rlo) * ld + 8 * chunk) * 2);
 }
+// LDS DMA issued through inline assembly: the compiler does not track these loads, so it does not wait
+// for them before reading the other LDS stage (it cannot prove the two stages apart and otherwise
+// stalls every other step on the DMA just issued). stage_barrier() waits for them explicitly before any
+// wave reads the stage they fill. M0 holds the wave-uniform LDS destination; lane i writes 16 (or 4)
+// bytes at M0 + 16*i (4*i).
+__device__ __forceinline__ uint32_t lds_addr(const void* p) {
+    return (uint32_t)(uintptr_t)(const __attribute__((address_space(3))) void*)p;
+}
+__device__ __forceinline__ void dma16(uint32_t lds, uint32_t voff, __amdgpu_buffer_rsrc_t r) {
+    asm volatile("s_mov_b32 m0, %0\n\tbuffer_load_dwordx4 %1, %2, 0 offen lds" ::"s"(lds), "v"(voff), "s"(r)
+                 : "memory", "m0");
+}
+__device__ __forceinline__ void dma4(uint32_t lds, uint32_t voff, __amdgpu_buffer_rsrc_t r) {
+    asm volatile("s_mov_b32 m0, %0\n\tbuffer_load_dword %1, %2, 0 offen lds" ::"s"(lds), "v"(voff), "s"(r)
+                 : "memory", "m0");
+}
 // rows r0 .. T-1 of a [T][ld] bf16 tensor -> one LDS tile (rows past T arrive as zeros)
 __device__ __forceinline__ void dma_tile(uint8_t* tile, const uint16_t* base, int r0, int T, int ld,
                                          const uint32_t (&voff)[4], int wave) {
     const __amdgpu_buffer_rsrc_t r = make_rsrc(base + (int64_t)r0 * ld, (uint32_t)(T - r0) * (uint32_t)ld * 2u);
+    const uint32_t l0 = __builtin_amdgcn_readfirstlane(lds_addr(tile + wave * 1024));
 #pragma unroll
-    for (int i = 0; i < 4; ++i)
-        __builtin_amdgcn_raw_ptr_buffer_load_lds(r, (lds_void*)(tile + (4 * i + wave) * 1024), 16, voff[i], 0, 0, 0);
+    for (int i = 0; i < 4; ++i) dma16(l0 + 4096 * i, voff[i], r);
 }
 // 64 floats t0 .. t0+63 of a [T] row -> LDS (one wave; entries past T arrive as zeros)
 __device__ __forceinline__ void dma_stats(float* dst, const float* base, int t0, int T, int lane) {
     const __amdgpu_buffer_rsrc_t r = make_rsrc(base + t0, (uint32_t)(T - t0) * 4u);
-    __builtin_amdgcn_raw_ptr_buffer_load_lds(r, (lds_void*)dst, 4, (uint32_t)lane * 4u, 0, 0, 0);
+    dma4(__builtin_amdgcn_readfirstlane(lds_addr(dst)), (uint32_t)lane * 4u, r);
 }
 
 // this wave's LDS DMA and LDS accesses are complete before any wave passes it
