@@ -40,6 +40,9 @@
 // reads and transposing reads are both free of bank conflicts. Tiles arrive
 // by LDS DMA (buffer_load ... lds), double-buffered, one barrier per tile;
 // buffer descriptors end at row T - 1 so rows past the sequence arrive as zeros.
+// Every product reads its LDS fragments through a four-deep register ring,
+// three reads ahead of the MFMA that consumes them: with one wave per SIMD
+// nothing else hides an LDS round trip.
 
 #include "dt_internal.h"
 
@@ -92,6 +95,9 @@ template <int N, typename F>
 __device__ __forceinline__ void static_for(F&& f) {
     static_for_impl(f, std::make_integer_sequence<int, N>{});
 }
+
+// keeps each MFMA with the LDS read issued beside it: the scheduler may not move work across
+#define DT_BUNDLE_END __builtin_amdgcn_sched_barrier(0)
 
 // Row fragment r = 2*cc + blk of a tile: rows 32*blk + ln, dims 16*cc + 8*hh .. +8 (the A operand
 // with the tile's rows as M). raddr[cc] is this lane's address of chunk 2*cc + hh in block 0.
@@ -273,17 +279,26 @@ __global__ __launch_bounds__(kThreads, 1) void flash_bwd_dkdv_bf16_kernel(FlashB
             if (has_next) dma(nxt, q0 + kTile);
             if (a.causal && q0 + kTile - 1 < kw) return;  // every query of the tile precedes the wave's keys
             const bool need_mask = a.causal && q0 < kw + 31;
-            // S = Q K^T and dP = dO V^T for 64 queries (two 32-row blocks) x the wave's 32 keys
+            // S = Q K^T and dP = dO V^T for 64 queries (two 32-row blocks) x the wave's 32 keys. The 32
+            // row fragments (index r = 16*qb + 2*cc + w, w = 0: Q for S, 1: dO for dP) go through a
+            // four-deep register ring, three reads ahead of the MFMA that consumes them.
             floatx16 sc[2], dp[2];
-#pragma unroll
-            for (int qb = 0; qb < 2; ++qb) {
-                sc[qb] = zero16();
-                dp[qb] = zero16();
-#pragma unroll
-                for (int cc = 0; cc < 8; ++cc) {
-                    sc[qb] = mfma(read_row(s.q, LA.raddr, cc, qb), kf[cc], sc[qb]);
-                    dp[qb] = mfma(read_row(s.g, LA.raddr, cc, qb), vf[cc], dp[qb]);
-                }
+            {
+                auto rd = [&](int r) {
+                    return read_row((r & 1) ? s.g : s.q, LA.raddr, (r >> 1) & 7, r >> 4);
+                };
+                bf16x8 ring[4];
+                ring[0] = rd(0);
+                ring[1] = rd(1);
+                ring[2] = rd(2);
+                static_for<32>([&](auto R) {
+                    constexpr int r = decltype(R)::value;
+                    constexpr int qb = r >> 4, cc = (r >> 1) & 7;
+                    if constexpr (r + 3 < 32) ring[(r + 3) & 3] = rd(r + 3);
+                    if constexpr (r & 1) dp[qb] = mfma(ring[r & 3], vf[cc], cc == 0 ? zero16() : dp[qb]);
+                    else sc[qb] = mfma(ring[r & 3], kf[cc], cc == 0 ? zero16() : sc[qb]);
+                    DT_BUNDLE_END;
+                });
             }
             // P = exp2(S c - lse2), dS = P (dP - delta); element i of block qb is query
             // q0 + 32*qb + 8*(i/4) + 4*hh + i%4
@@ -319,12 +334,23 @@ __global__ __launch_bounds__(kThreads, 1) void flash_bwd_dkdv_bf16_kernel(FlashB
                     dsb[qb][u] = __builtin_bit_cast(bf16x8, make_uint4(wd[0], wd[1], wd[2], wd[3]));
                 }
             }
-            // dV^T += dO^T P, dK^T += Q^T dS (k = the tile's queries, in accumulator row order)
-            static_for<16>([&](auto C) {
-                constexpr int ci = decltype(C)::value;  // = 8*qb + 4*u + db
-                dv[ci & 3] = mfma(read_tr(s.g, LA.taddr, ci), pb[ci >> 3][(ci >> 2) & 1], dv[ci & 3]);
-                dk[ci & 3] = mfma(read_tr(s.q, LA.taddr, ci), dsb[ci >> 3][(ci >> 2) & 1], dk[ci & 3]);
-            });
+            // dV^T += dO^T P, dK^T += Q^T dS (k = the tile's queries, in accumulator row order); fragment
+            // r = 2*ci + w (ci = 8*qb + 4*u + db; w = 0: dO^T for dV, 1: Q^T for dK) through the same ring
+            {
+                auto rd = [&](int r) { return read_tr((r & 1) ? s.q : s.g, LA.taddr, r >> 1); };
+                bf16x8 ring[4];
+                ring[0] = rd(0);
+                ring[1] = rd(1);
+                ring[2] = rd(2);
+                static_for<32>([&](auto R) {
+                    constexpr int r = decltype(R)::value;
+                    constexpr int ci = r >> 1;
+                    if constexpr (r + 3 < 32) ring[(r + 3) & 3] = rd(r + 3);
+                    if constexpr (r & 1) dk[ci & 3] = mfma(ring[r & 3], dsb[ci >> 3][(ci >> 2) & 1], dk[ci & 3]);
+                    else dv[ci & 3] = mfma(ring[r & 3], pb[ci >> 3][(ci >> 2) & 1], dv[ci & 3]);
+                    DT_BUNDLE_END;
+                });
+            }
         };
 
         dma(st0, q_begin);
@@ -405,17 +431,25 @@ __global__ __launch_bounds__(kThreads, 1) void flash_bwd_dq_bf16_kernel(FlashBwd
             if (has_next) dma(nxt, k0 + kTile);
             if (a.causal && k0 > qw + 31) return;  // every key of the tile follows the wave's queries
             const bool need_mask = (a.causal && k0 + kTile - 1 > qw) || k0 + kTile > T;
-            // S^T = K Q^T and dP^T = V dO^T for 64 keys (two 32-row blocks) x the wave's 32 queries
+            // S^T = K Q^T and dP^T = V dO^T for 64 keys (two 32-row blocks) x the wave's 32 queries; row
+            // fragment r = 16*kb + 2*cc + w (w = 0: K, 1: V) through a four-deep ring, three reads ahead
             floatx16 sc[2], dp[2];
-#pragma unroll
-            for (int kb = 0; kb < 2; ++kb) {
-                sc[kb] = zero16();
-                dp[kb] = zero16();
-#pragma unroll
-                for (int cc = 0; cc < 8; ++cc) {
-                    sc[kb] = mfma(read_row(s.k, LA.raddr, cc, kb), qf[cc], sc[kb]);
-                    dp[kb] = mfma(read_row(s.v, LA.raddr, cc, kb), gf[cc], dp[kb]);
-                }
+            {
+                auto rd = [&](int r) {
+                    return read_row((r & 1) ? s.v : s.k, LA.raddr, (r >> 1) & 7, r >> 4);
+                };
+                bf16x8 ring[4];
+                ring[0] = rd(0);
+                ring[1] = rd(1);
+                ring[2] = rd(2);
+                static_for<32>([&](auto R) {
+                    constexpr int r = decltype(R)::value;
+                    constexpr int kb = r >> 4, cc = (r >> 1) & 7;
+                    if constexpr (r + 3 < 32) ring[(r + 3) & 3] = rd(r + 3);
+                    if constexpr (r & 1) dp[kb] = mfma(ring[r & 3], gf[cc], cc == 0 ? zero16() : dp[kb]);
+                    else sc[kb] = mfma(ring[r & 3], qf[cc], cc == 0 ? zero16() : sc[kb]);
+                    DT_BUNDLE_END;
+                });
             }
             // dS^T = P^T (dP^T - delta); element i of block kb is key k0 + 32*kb + 8*(i/4) + 4*hh + i%4
             bf16x8 dsb[2][2];
@@ -436,11 +470,19 @@ __global__ __launch_bounds__(kThreads, 1) void flash_bwd_dq_bf16_kernel(FlashBwd
                     dsb[kb][u] = __builtin_bit_cast(bf16x8, make_uint4(wd[0], wd[1], wd[2], wd[3]));
                 }
             }
-            // dQ^T += K^T dS^T (k = the tile's keys, in accumulator row order)
-            static_for<16>([&](auto C) {
-                constexpr int ci = decltype(C)::value;  // = 8*kb + 4*u + db
-                dq[ci & 3] = mfma(read_tr(s.k, LA.taddr, ci), dsb[ci >> 3][(ci >> 2) & 1], dq[ci & 3]);
-            });
+            // dQ^T += K^T dS^T (k = the tile's keys, in accumulator row order), K^T fragments through the ring
+            {
+                bf16x8 ring[4];
+                ring[0] = read_tr(s.k, LA.taddr, 0);
+                ring[1] = read_tr(s.k, LA.taddr, 1);
+                ring[2] = read_tr(s.k, LA.taddr, 2);
+                static_for<16>([&](auto C) {
+                    constexpr int ci = decltype(C)::value;  // = 8*kb + 4*u + db
+                    if constexpr (ci + 3 < 16) ring[(ci + 3) & 3] = read_tr(s.k, LA.taddr, ci + 3);
+                    dq[ci & 3] = mfma(ring[ci & 3], dsb[ci >> 3][(ci >> 2) & 1], dq[ci & 3]);
+                    DT_BUNDLE_END;
+                });
+            }
         };
 
         dma(st0, 0);
