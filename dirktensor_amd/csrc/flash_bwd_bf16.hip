@@ -279,78 +279,73 @@ __global__ __launch_bounds__(kThreads, 1) void flash_bwd_dkdv_bf16_kernel(FlashB
             if (has_next) dma(nxt, q0 + kTile);
             if (a.causal && q0 + kTile - 1 < kw) return;  // every query of the tile precedes the wave's keys
             const bool need_mask = a.causal && q0 < kw + 31;
-            // S = Q K^T and dP = dO V^T for 64 queries (two 32-row blocks) x the wave's 32 keys. The 32
-            // row fragments (index r = 16*qb + 2*cc + w, w = 0: Q for S, 1: dO for dP) go through a
-            // four-deep register ring, three reads ahead of the MFMA that consumes them.
-            floatx16 sc[2], dp[2];
-            {
-                auto rd = [&](int r) {
-                    return read_row((r & 1) ? s.g : s.q, LA.raddr, (r >> 1) & 7, r >> 4);
-                };
-                bf16x8 ring[4];
-                ring[0] = rd(0);
-                ring[1] = rd(1);
-                ring[2] = rd(2);
-                static_for<32>([&](auto R) {
-                    constexpr int r = decltype(R)::value;
-                    constexpr int qb = r >> 4, cc = (r >> 1) & 7;
-                    if constexpr (r + 3 < 32) ring[(r + 3) & 3] = rd(r + 3);
-                    if constexpr (r & 1) dp[qb] = mfma(ring[r & 3], vf[cc], cc == 0 ? zero16() : dp[qb]);
-                    else sc[qb] = mfma(ring[r & 3], kf[cc], cc == 0 ? zero16() : sc[qb]);
-                    DT_BUNDLE_END;
-                });
-            }
-            // P = exp2(S c - lse2), dS = P (dP - delta); element i of block qb is query
-            // q0 + 32*qb + 8*(i/4) + 4*hh + i%4
-            bf16x8 pb[2][2], dsb[2][2];
+            // One software-pipelined sequence of 64 bundles (one LDS fragment read three ahead + one MFMA
+            // each), the P / dS arithmetic of one 32-query block riding on the MFMAs of the next phase so
+            // that it issues while the matrix pipe works:
+            //   bundles  0..15  S and dP of queries 0..31   (fragment f = b: Q / dO rows)
+            //   bundles 16..31  S and dP of queries 32..63; P, dS of queries 0..31, one element per bundle
+            //   bundles 32..63  dV^T += dO^T P, dK^T += Q^T dS (fragment f = b: dO^T / Q^T); P, dS of
+            //                   queries 32..63 in bundles 32..47
+            // Row fragment f < 32: 16*qb + 2*cc + w (w = 0: Q for S, 1: dO for dP); transposed fragment
+            // f >= 32: 2*ci + w with ci = 8*qb + 4*u + db (w = 0: dO^T for dV, 1: Q^T for dK).
+            // Element i of block qb is query q0 + 32*qb + 8*(i/4) + 4*hh + i%4.
+            float Lr[2][16], Dr[2][16];
 #pragma unroll
-            for (int qb = 0; qb < 2; ++qb) {
-                float p[16], ds[16];
+            for (int qb = 0; qb < 2; ++qb)
 #pragma unroll
                 for (int g = 0; g < 4; ++g) {
                     const int qi = 32 * qb + 8 * g + 4 * hh;
                     const float4 L4 = *reinterpret_cast<const float4*>(&s.lse2[qi]);
                     const float4 D4 = *reinterpret_cast<const float4*>(&s.delta[qi]);
-                    const float Lr[4] = {L4.x, L4.y, L4.z, L4.w};
-                    const float Dr[4] = {D4.x, D4.y, D4.z, D4.w};
-#pragma unroll
-                    for (int r = 0; r < 4; ++r) {
-                        const int i = 4 * g + r;
-                        float pv = __builtin_amdgcn_exp2f(sc[qb][i] * c - Lr[r]);
-                        if (need_mask && key > q0 + qi + r) pv = 0.0f;
-                        p[i] = pv;
-                        ds[i] = pv * (dp[qb][i] - Dr[r]);
-                    }
+                    Lr[qb][4 * g] = L4.x, Lr[qb][4 * g + 1] = L4.y, Lr[qb][4 * g + 2] = L4.z, Lr[qb][4 * g + 3] = L4.w;
+                    Dr[qb][4 * g] = D4.x, Dr[qb][4 * g + 1] = D4.y, Dr[qb][4 * g + 2] = D4.z, Dr[qb][4 * g + 3] = D4.w;
                 }
+            floatx16 sc[2], dp[2];
+            float p[2][16], ds[2][16];
+            bf16x8 pb[2][2], dsb[2][2];
+            auto rd = [&](int f) {
+                if (f < 32) return read_row((f & 1) ? s.g : s.q, LA.raddr, (f >> 1) & 7, f >> 4);
+                return read_tr((f & 1) ? s.q : s.g, LA.taddr, (f - 32) >> 1);
+            };
+            auto elem = [&](int qb, int i) {  // P = exp2(S c - lse2), dS = P (dP - delta)
+                float pv = __builtin_amdgcn_exp2f(sc[qb][i] * c - Lr[qb][i]);
+                const int q = q0 + 32 * qb + 8 * (i >> 2) + 4 * hh + (i & 3);
+                pv = (need_mask && key > q) ? 0.0f : pv;
+                p[qb][i] = pv;
+                ds[qb][i] = pv * (dp[qb][i] - Dr[qb][i]);
+            };
+            auto pack = [&](int qb, int u) {  // bf16 B operands: elements 8u .. 8u+7
+                uint32_t wp[4], wd[4];
 #pragma unroll
-                for (int u = 0; u < 2; ++u) {
-                    uint32_t wp[4], wd[4];
-#pragma unroll
-                    for (int e = 0; e < 4; ++e) {
-                        wp[e] = pack_bf16x2(p[8 * u + 2 * e], p[8 * u + 2 * e + 1]);
-                        wd[e] = pack_bf16x2(ds[8 * u + 2 * e], ds[8 * u + 2 * e + 1]);
-                    }
-                    pb[qb][u] = __builtin_bit_cast(bf16x8, make_uint4(wp[0], wp[1], wp[2], wp[3]));
-                    dsb[qb][u] = __builtin_bit_cast(bf16x8, make_uint4(wd[0], wd[1], wd[2], wd[3]));
+                for (int e = 0; e < 4; ++e) {
+                    wp[e] = pack_bf16x2(p[qb][8 * u + 2 * e], p[qb][8 * u + 2 * e + 1]);
+                    wd[e] = pack_bf16x2(ds[qb][8 * u + 2 * e], ds[qb][8 * u + 2 * e + 1]);
                 }
-            }
-            // dV^T += dO^T P, dK^T += Q^T dS (k = the tile's queries, in accumulator row order); fragment
-            // r = 2*ci + w (ci = 8*qb + 4*u + db; w = 0: dO^T for dV, 1: Q^T for dK) through the same ring
-            {
-                auto rd = [&](int r) { return read_tr((r & 1) ? s.q : s.g, LA.taddr, r >> 1); };
-                bf16x8 ring[4];
-                ring[0] = rd(0);
-                ring[1] = rd(1);
-                ring[2] = rd(2);
-                static_for<32>([&](auto R) {
-                    constexpr int r = decltype(R)::value;
-                    constexpr int ci = r >> 1;
-                    if constexpr (r + 3 < 32) ring[(r + 3) & 3] = rd(r + 3);
-                    if constexpr (r & 1) dk[ci & 3] = mfma(ring[r & 3], dsb[ci >> 3][(ci >> 2) & 1], dk[ci & 3]);
-                    else dv[ci & 3] = mfma(ring[r & 3], pb[ci >> 3][(ci >> 2) & 1], dv[ci & 3]);
-                    DT_BUNDLE_END;
-                });
-            }
+                pb[qb][u] = __builtin_bit_cast(bf16x8, make_uint4(wp[0], wp[1], wp[2], wp[3]));
+                dsb[qb][u] = __builtin_bit_cast(bf16x8, make_uint4(wd[0], wd[1], wd[2], wd[3]));
+            };
+            bf16x8 ring[4];
+            ring[0] = rd(0);
+            ring[1] = rd(1);
+            ring[2] = rd(2);
+            static_for<64>([&](auto B) {
+                constexpr int b = decltype(B)::value;
+                if constexpr (b + 3 < 64) ring[(b + 3) & 3] = rd(b + 3);
+                if constexpr (b < 32) {
+                    constexpr int qb = b >> 4, cc = (b >> 1) & 7;
+                    if constexpr (b & 1) dp[qb] = mfma(ring[b & 3], vf[cc], cc == 0 ? zero16() : dp[qb]);
+                    else sc[qb] = mfma(ring[b & 3], kf[cc], cc == 0 ? zero16() : sc[qb]);
+                } else {
+                    constexpr int ci = (b - 32) >> 1;
+                    if constexpr (b & 1) dk[ci & 3] = mfma(ring[b & 3], dsb[ci >> 3][(ci >> 2) & 1], dk[ci & 3]);
+                    else dv[ci & 3] = mfma(ring[b & 3], pb[ci >> 3][(ci >> 2) & 1], dv[ci & 3]);
+                }
+                if constexpr (b >= 16 && b < 32) elem(0, b - 16);
+                if constexpr (b >= 32 && b < 48) elem(1, b - 32);
+                if constexpr (b == 23 || b == 31) pack(0, b == 31);
+                if constexpr (b == 39 || b == 47) pack(1, b == 47);
+                DT_BUNDLE_END;
+            });
         };
 
         dma(st0, q_begin);
@@ -431,58 +426,55 @@ __global__ __launch_bounds__(kThreads, 1) void flash_bwd_dq_bf16_kernel(FlashBwd
             if (has_next) dma(nxt, k0 + kTile);
             if (a.causal && k0 > qw + 31) return;  // every key of the tile follows the wave's queries
             const bool need_mask = (a.causal && k0 + kTile - 1 > qw) || k0 + kTile > T;
-            // S^T = K Q^T and dP^T = V dO^T for 64 keys (two 32-row blocks) x the wave's 32 queries; row
-            // fragment r = 16*kb + 2*cc + w (w = 0: K, 1: V) through a four-deep ring, three reads ahead
+            // One software-pipelined sequence of 48 bundles (one LDS fragment read three ahead + one MFMA):
+            //   bundles  0..15  S^T and dP^T of keys 0..31   (fragment f = b: K / V rows)
+            //   bundles 16..31  S^T and dP^T of keys 32..63; dS of keys 0..31, one element per bundle
+            //   bundles 32..47  dQ^T += K^T dS^T (fragment f = b: K^T); dS of keys 32..63, two per bundle
+            // Row fragment f < 32: 16*kb + 2*cc + w (w = 0: K, 1: V); f >= 32: K^T chunk ci = f - 32 =
+            // 8*kb + 4*u + db. Element i of block kb is key k0 + 32*kb + 8*(i/4) + 4*hh + i%4.
             floatx16 sc[2], dp[2];
-            {
-                auto rd = [&](int r) {
-                    return read_row((r & 1) ? s.v : s.k, LA.raddr, (r >> 1) & 7, r >> 4);
-                };
-                bf16x8 ring[4];
-                ring[0] = rd(0);
-                ring[1] = rd(1);
-                ring[2] = rd(2);
-                static_for<32>([&](auto R) {
-                    constexpr int r = decltype(R)::value;
-                    constexpr int kb = r >> 4, cc = (r >> 1) & 7;
-                    if constexpr (r + 3 < 32) ring[(r + 3) & 3] = rd(r + 3);
-                    if constexpr (r & 1) dp[kb] = mfma(ring[r & 3], gf[cc], cc == 0 ? zero16() : dp[kb]);
-                    else sc[kb] = mfma(ring[r & 3], qf[cc], cc == 0 ? zero16() : sc[kb]);
-                    DT_BUNDLE_END;
-                });
-            }
-            // dS^T = P^T (dP^T - delta); element i of block kb is key k0 + 32*kb + 8*(i/4) + 4*hh + i%4
+            float ds[2][16];
             bf16x8 dsb[2][2];
+            auto rd = [&](int f) {
+                if (f < 32) return read_row((f & 1) ? s.v : s.k, LA.raddr, (f >> 1) & 7, f >> 4);
+                return read_tr(s.k, LA.taddr, f - 32);
+            };
+            auto elem = [&](int kb, int i) {  // dS^T = P^T (dP^T - delta), P^T = exp2(S^T c - lse2)
+                float pv = __builtin_amdgcn_exp2f(sc[kb][i] * c - lse2);
+                const int key = k0 + 32 * kb + 8 * (i >> 2) + 4 * hh + (i & 3);
+                pv = (need_mask && key > lim) ? 0.0f : pv;
+                ds[kb][i] = pv * (dp[kb][i] - delta);
+            };
+            auto pack = [&](int kb, int u) {
+                uint32_t wd[4];
 #pragma unroll
-            for (int kb = 0; kb < 2; ++kb) {
-                float ds[16];
-#pragma unroll
-                for (int i = 0; i < 16; ++i) {
-                    float pv = __builtin_amdgcn_exp2f(sc[kb][i] * c - lse2);
-                    if (need_mask && k0 + 32 * kb + 8 * (i / 4) + 4 * hh + (i % 4) > lim) pv = 0.0f;
-                    ds[i] = pv * (dp[kb][i] - delta);
+                for (int e = 0; e < 4; ++e) wd[e] = pack_bf16x2(ds[kb][8 * u + 2 * e], ds[kb][8 * u + 2 * e + 1]);
+                dsb[kb][u] = __builtin_bit_cast(bf16x8, make_uint4(wd[0], wd[1], wd[2], wd[3]));
+            };
+            bf16x8 ring[4];
+            ring[0] = rd(0);
+            ring[1] = rd(1);
+            ring[2] = rd(2);
+            static_for<48>([&](auto B) {
+                constexpr int b = decltype(B)::value;
+                if constexpr (b + 3 < 48) ring[(b + 3) & 3] = rd(b + 3);
+                if constexpr (b < 32) {
+                    constexpr int kb = b >> 4, cc = (b >> 1) & 7;
+                    if constexpr (b & 1) dp[kb] = mfma(ring[b & 3], gf[cc], cc == 0 ? zero16() : dp[kb]);
+                    else sc[kb] = mfma(ring[b & 3], qf[cc], cc == 0 ? zero16() : sc[kb]);
+                } else {
+                    constexpr int ci = b - 32;
+                    dq[ci & 3] = mfma(ring[b & 3], dsb[ci >> 3][(ci >> 2) & 1], dq[ci & 3]);
                 }
-#pragma unroll
-                for (int u = 0; u < 2; ++u) {
-                    uint32_t wd[4];
-#pragma unroll
-                    for (int e = 0; e < 4; ++e) wd[e] = pack_bf16x2(ds[8 * u + 2 * e], ds[8 * u + 2 * e + 1]);
-                    dsb[kb][u] = __builtin_bit_cast(bf16x8, make_uint4(wd[0], wd[1], wd[2], wd[3]));
+                if constexpr (b >= 16 && b < 32) elem(0, b - 16);
+                if constexpr (b == 23 || b == 31) pack(0, b == 31);
+                if constexpr (b >= 32 && b < 40) {
+                    elem(1, 2 * (b - 32));
+                    elem(1, 2 * (b - 32) + 1);
                 }
-            }
-            // dQ^T += K^T dS^T (k = the tile's keys, in accumulator row order), K^T fragments through the ring
-            {
-                bf16x8 ring[4];
-                ring[0] = read_tr(s.k, LA.taddr, 0);
-                ring[1] = read_tr(s.k, LA.taddr, 1);
-                ring[2] = read_tr(s.k, LA.taddr, 2);
-                static_for<16>([&](auto C) {
-                    constexpr int ci = decltype(C)::value;  // = 8*kb + 4*u + db
-                    if constexpr (ci + 3 < 16) ring[(ci + 3) & 3] = read_tr(s.k, LA.taddr, ci + 3);
-                    dq[ci & 3] = mfma(ring[ci & 3], dsb[ci >> 3][(ci >> 2) & 1], dq[ci & 3]);
-                    DT_BUNDLE_END;
-                });
-            }
+                if constexpr (b == 35 || b == 39) pack(1, b == 39);
+                DT_BUNDLE_END;
+            });
         };
 
         dma(st0, 0);
