@@ -153,18 +153,16 @@ __device__ __forceinline__ void dma_offsets(uint32_t (&voff)[4], int lane, int w
 // LDS DMA issued through inline assembly: the compiler does not track these loads, so it does not wait
 // for them before reading the other LDS stage (it cannot prove the two stages apart and otherwise
 // stalls every other step on the DMA just issued). stage_barrier() waits for them explicitly before any
-// wave reads the stage they fill. M0 holds the wave-uniform LDS destination; lane i writes 16 (or 4)
-// bytes at M0 + 16*i (4*i).
+// wave reads the stage they fill. M0 holds the wave-uniform LDS destination (an operand bound to M0, so
+// the compiler sets it and knows it changed); lane i writes 16 (or 4) bytes at M0 + 16*i (4*i).
 __device__ __forceinline__ uint32_t lds_addr(const void* p) {
     return (uint32_t)(uintptr_t)(const __attribute__((address_space(3))) void*)p;
 }
 __device__ __forceinline__ void dma16(uint32_t lds, uint32_t voff, __amdgpu_buffer_rsrc_t r) {
-    asm volatile("s_mov_b32 m0, %0\n\tbuffer_load_dwordx4 %1, %2, 0 offen lds" ::"s"(lds), "v"(voff), "s"(r)
-                 : "memory", "m0");
+    asm volatile("buffer_load_dwordx4 %0, %1, 0 offen lds" ::"v"(voff), "s"(r), "{m0}"(lds) : "memory");
 }
 __device__ __forceinline__ void dma4(uint32_t lds, uint32_t voff, __amdgpu_buffer_rsrc_t r) {
-    asm volatile("s_mov_b32 m0, %0\n\tbuffer_load_dword %1, %2, 0 offen lds" ::"s"(lds), "v"(voff), "s"(r)
-                 : "memory", "m0");
+    asm volatile("buffer_load_dword %0, %1, 0 offen lds" ::"v"(voff), "s"(r), "{m0}"(lds) : "memory");
 }
 // rows r0 .. T-1 of a [T][ld] bf16 tensor -> one LDS tile (rows past T arrive as zeros)
 __device__ __forceinline__ void dma_tile(uint8_t* tile, const uint16_t* base, int r0, int T, int ld,

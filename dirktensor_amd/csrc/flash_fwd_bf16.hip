@@ -290,6 +290,8 @@ __device__ __forceinline__ void tile_step(Acc& A, const bf16x8 (&qf)[8], const u
 // Barrier for the double-buffered loop: this wave's LDS DMA and LDS accesses are
 // complete before any wave passes it.
 __device__ __forceinline__ void stage_barrier() { asm volatile("s_waitcnt vmcnt(0) lgkmcnt(0)\n\ts_barrier" ::: "memory"); }
+// Barrier over LDS accesses only: vector memory requests in flight are not waited for.
+__device__ __forceinline__ void lds_barrier() { asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory"); }
 
 __global__ __launch_bounds__(kThreads, 1) void flash_fwd_bf16_kernel(FlashArgs a, SeqLens lens, RaggedOrder ro) {
     __shared__ __attribute__((aligned(1024))) Stage stage0;
@@ -373,35 +375,6 @@ __global__ __launch_bounds__(kThreads, 1) void flash_fwd_bf16_kernel(FlashArgs a
             continue;  // no LDS was touched: no barrier needed
         }
 
-        // Q fragment, pre-multiplied by scale * log2 e: qf[cc] = Q[qrow][16*cc + 8*hh .. +8] * c
-        bf16x8 qf[8];
-        if (qrow < T) {
-            const uint16_t* qp = Qg + (int64_t)qrow * a.ldq + 8 * hh;
-#pragma unroll
-            for (int cc = 0; cc < 8; ++cc) {
-                const uint4 raw = *reinterpret_cast<const uint4*>(qp + 16 * cc);
-                const uint32_t w[4] = {raw.x, raw.y, raw.z, raw.w};
-                uint32_t sw[4];
-#pragma unroll
-                for (int e = 0; e < 4; ++e) sw[e] = pack_bf16x2(bf16_lo(w[e]) * c, bf16_hi(w[e]) * c);
-                qf[cc] = __builtin_bit_cast(bf16x8, make_uint4(sw[0], sw[1], sw[2], sw[3]));
-            }
-        } else {
-#pragma unroll
-            for (int cc = 0; cc < 8; ++cc) qf[cc] = __builtin_bit_cast(bf16x8, make_uint4(0, 0, 0, 0));
-        }
-
-        Acc A;
-#pragma unroll
-        for (int db = 0; db < 4; ++db)
-#pragma unroll
-            for (int i = 0; i < 16; ++i) A.o[db][i] = 0.0f;
-#pragma unroll
-        for (int i = 0; i < 16; ++i) A.neg_ms[i] = 0.0f;
-        A.m_t = kNegInf;
-        A.m_s = kNegInf;
-        A.l = 0.0f;
-
         const int k_end = a.causal ? min(q0 + kBM, L) : L;
         const int n_tiles = (k_end + kBN - 1) / kBN;
         const int n_iter = (n_tiles + 1) / 2;
@@ -416,6 +389,47 @@ __global__ __launch_bounds__(kThreads, 1) void flash_fwd_bf16_kernel(FlashArgs a
                 __builtin_amdgcn_raw_ptr_buffer_load_lds(r, (lds_void*)&stg[grp][kv][(4 * i + wq) * 1024], 16, voff[i],
                                                          0, 0, 0);
         };
+        // the first tile streams in while the query row loads
+        if (grp < n_tiles) {
+            dma(stage0, 0, grp);
+            dma(stage0, 1, grp);
+        }
+
+        // Q fragment, pre-multiplied by scale * log2 e: qf[cc] = Q[qrow][16*cc + 8*hh .. +8] * c. All eight
+        // loads are in flight together (and with the first tile's DMA) before the first is converted.
+        bf16x8 qf[8];
+        {
+            uint4 raw[8];
+            if (qrow < T) {
+                const uint16_t* qp = Qg + (int64_t)qrow * a.ldq + 8 * hh;
+#pragma unroll
+                for (int cc = 0; cc < 8; ++cc) raw[cc] = *reinterpret_cast<const uint4*>(qp + 16 * cc);
+            } else {
+#pragma unroll
+                for (int cc = 0; cc < 8; ++cc) raw[cc] = make_uint4(0, 0, 0, 0);
+            }
+            __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+            for (int cc = 0; cc < 8; ++cc) {
+                const uint32_t w[4] = {raw[cc].x, raw[cc].y, raw[cc].z, raw[cc].w};
+                uint32_t sw[4];
+#pragma unroll
+                for (int e = 0; e < 4; ++e) sw[e] = pack_bf16x2(bf16_lo(w[e]) * c, bf16_hi(w[e]) * c);
+                qf[cc] = __builtin_bit_cast(bf16x8, make_uint4(sw[0], sw[1], sw[2], sw[3]));
+            }
+        }
+
+        Acc A;
+#pragma unroll
+        for (int db = 0; db < 4; ++db)
+#pragma unroll
+            for (int i = 0; i < 16; ++i) A.o[db][i] = 0.0f;
+#pragma unroll
+        for (int i = 0; i < 16; ++i) A.neg_ms[i] = 0.0f;
+        A.m_t = kNegInf;
+        A.m_s = kNegInf;
+        A.l = 0.0f;
+
         // Step on stage `cur` (tile kt) while the group's next tile kn streams into `nxt`: its K at the start
         // of the step, its V after the softmax, so the V rows do not compete with this step's K reads.
         auto step = [&](const Stage& cur, Stage& nxt, int kt, int kn) {
@@ -434,11 +448,7 @@ __global__ __launch_bounds__(kThreads, 1) void flash_fwd_bf16_kernel(FlashArgs a
             tile_step(A, qf, cur[grp][0], cur[grp][1], kaddr, vaddr, k0, need_mask, lim, hh, mid);
         };
 
-        if (grp < n_tiles) {
-            dma(stage0, 0, grp);
-            dma(stage0, 1, grp);
-        }
-        stage_barrier();
+        stage_barrier();  // the first tile has landed
         for (int it = 0; it < n_iter; it += 2) {
             // even step: compute from stage0 while the group's next tile streams into stage1
             step(stage0, stage1, 2 * it + grp, 2 * (it + 1) + grp);
@@ -500,7 +510,9 @@ __global__ __launch_bounds__(kThreads, 1) void flash_fwd_bf16_kernel(FlashArgs a
                 }
             }
         }
-        __syncthreads();
+        // group 0 has read the exchange (its LDS reads are complete) before the next item's DMA may overwrite
+        // it; the output stores need not have completed
+        lds_barrier();
     }
 }
 
