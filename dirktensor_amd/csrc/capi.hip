@@ -143,6 +143,23 @@ int gemm_rm(dt_ctx* ctx, hipStream_t s, bool ta, bool tb, int M, int N, int K, c
     return DT_OK;
 }
 
+int gemm_rm_bf16(dt_ctx* ctx, hipStream_t s, bool ta, bool tb, int M, int N, int K, const void* A, int lda,
+                 const void* B, int ldb, void* C, int ldc) {
+    DT_TRY(ensure_blas(ctx));
+    rocblas_handle h = static_cast<rocblas_handle>(ctx->blas);
+    rocblas_set_stream(h, s);
+    const float one = 1.0f, zero = 0.0f;
+    const rocblas_operation opb = tb ? rocblas_operation_transpose : rocblas_operation_none;
+    const rocblas_operation opa = ta ? rocblas_operation_transpose : rocblas_operation_none;
+    const rocblas_status st =
+        rocblas_gemm_ex(h, opb, opa, N, M, K, &one, B, rocblas_datatype_bf16_r, ldb, A, rocblas_datatype_bf16_r, lda,
+                        &zero, C, rocblas_datatype_bf16_r, ldc, C, rocblas_datatype_bf16_r, ldc, rocblas_datatype_f32_r,
+                        rocblas_gemm_algo_standard, 0, 0);
+    if (st != rocblas_status_success)
+        return set_error(DT_ERR_BLAS, "rocBLAS GEMM (%d x %d x %d, bf16 out): %s", M, N, K, blas_status_str(st));
+    return DT_OK;
+}
+
 // y = x W^T with W stored [N][K] like torch Linear (OlmoAttention.cpp:68,74,80,104)
 static int gemm_xwt(dt_ctx* ctx, hipStream_t s, int M, int N, int K, const void* A, int lda, const void* W, int ldw,
                     float* C, int ldc, bool bf16_in) {

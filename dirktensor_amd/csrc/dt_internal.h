@@ -132,6 +132,9 @@ int launch_f32_to_bf16(const float* in, uint16_t* out, int64_t n, hipStream_t st
 // accumulation and output); op = transpose when ta / tb is set.
 int gemm_rm(dt_ctx* ctx, hipStream_t s, bool ta, bool tb, int M, int N, int K, const void* A, int lda,
             const void* B, int ldb, float beta, float* C, int ldc, bool bf16_in);
+// the same with bf16 inputs and a bf16 output C (beta = 0; fp32 accumulation, one rounding at the end)
+int gemm_rm_bf16(dt_ctx* ctx, hipStream_t s, bool ta, bool tb, int M, int N, int K, const void* A, int lda,
+                 const void* B, int ldb, void* C, int ldc);
 // .npy reader (v1-v3 headers, little-endian fp32, C order)
 int read_npy_f32(const std::string& path, std::vector<float>& out, std::vector<size_t>& shape);
 bool aligned16(const void* p);
@@ -187,13 +190,13 @@ int launch_embed_gather(const int32_t* tok, const float* E, float* x, int rows, 
 int launch_add(const float* a, const float* b, float* out, int64_t n, hipStream_t s);  // n % 4 == 0
 int launch_rmsnorm_rows(const float* a, const float* w, const float* res, float* out, uint16_t* out16, float* y_save,
                         float* rms_save, int rows, int dm, float eps, hipStream_t s);
-int launch_swiglu(const float* gu, void* act, int rows, int hid, int bf16, hipStream_t s);
+int launch_swiglu(const void* gu, void* act, int rows, int hid, int bf16, hipStream_t s);
 int launch_ce_loss(const float* logits, const int32_t* target, float* term, float* grad, float* loss, int rows, int V,
                    int count, hipStream_t s);
 int rmsnorm_bwd_blocks(int rows);
 int launch_rmsnorm_bwd(const float* dy, const float* y, const float* rms, const float* w, const float* dx_add,
                        float* dx, float* partial, float* grad_w, int rows, int dm, hipStream_t s);
-int launch_swiglu_bwd(const float* d_act, const float* gu, void* d_gu, int rows, int hid, int bf16, hipStream_t s);
+int launch_swiglu_bwd(const float* d_act, const void* gu, void* d_gu, int rows, int hid, int bf16, hipStream_t s);
 int launch_embed_bwd(const float* dx, const int32_t* uniq, const int32_t* start, const int32_t* pos, int n_uniq,
                      float* g_embed, int dm, hipStream_t s);
 }  // namespace dt

@@ -372,7 +372,7 @@ int dt_model_fwd(dt_model* M, const int32_t* tokens, int B, int T, float* logits
         ModelLayer& S = save_for_backward ? Ly : M->L[0];  // state buffers (layer 0's serve as scratch)
         DT_TRY(S.a.ensure(act * 4));
         DT_TRY(S.h.ensure(act * 4));
-        DT_TRY(S.gu.ensure((size_t)rows * 2 * hid * 4));
+        DT_TRY(S.gu.ensure((size_t)rows * 2 * hid * (bf ? 2 : 4)));
         DT_TRY(S.act.ensure((size_t)rows * hid * (bf ? 2 : 4)));
         DT_TRY(S.m.ensure(act * 4));
         if (bf) DT_TRY(S.h16.ensure(act * 2));
@@ -384,7 +384,7 @@ int dt_model_fwd(dt_model* M, const int32_t* tokens, int B, int T, float* logits
         }
         float* a = static_cast<float*>(S.a.ptr);
         float* h = static_cast<float*>(S.h.ptr);
-        float* gu = static_cast<float*>(S.gu.ptr);
+        void* gu = S.gu.ptr;  // fp32, or bf16 in bf16 mode
         float* mo = static_cast<float*>(S.m.ptr);
         uint16_t* h16 = bf ? static_cast<uint16_t*>(S.h16.ptr) : nullptr;
         float* y_pa = save_for_backward ? static_cast<float*>(S.y_pa.ptr) : nullptr;
@@ -395,8 +395,10 @@ int dt_model_fwd(dt_model* M, const int32_t* tokens, int B, int T, float* logits
         DT_TRY(dt_attn_layer_fwd(Ly.attn, x, a, B, T, nullptr, dtype, DT_MEM_DEVICE, save_for_backward, stream));
         DT_TRY(launch_rmsnorm_rows(a, Ly.w_pa, x, h, h16, y_pa, rms_pa, (int)rows, dm, kEps, s));
         // MLP (OlmoMlp.cpp:26-63): [gate | up] = h [Wgate; Wup]^T, act = silu(gate) * up, m = act Wdown^T
-        if (bf) DT_TRY(gemm_rm(ctx, s, false, true, (int)rows, 2 * hid, dm, h16, dm, Ly.w_gu16, dm, 0.0f, gu, 2 * hid, true));
-        else DT_TRY(gemm_rm(ctx, s, false, true, (int)rows, 2 * hid, dm, h, dm, Ly.w_gu, dm, 0.0f, gu, 2 * hid, false));
+        // (in bf16 mode the N = 16384 gate|up product is written as bf16: it is only read by SwiGLU)
+        if (bf) DT_TRY(gemm_rm_bf16(ctx, s, false, true, (int)rows, 2 * hid, dm, h16, dm, Ly.w_gu16, dm, gu, 2 * hid));
+        else DT_TRY(gemm_rm(ctx, s, false, true, (int)rows, 2 * hid, dm, h, dm, Ly.w_gu, dm, 0.0f, static_cast<float*>(gu),
+                            2 * hid, false));
         DT_TRY(launch_swiglu(gu, S.act.ptr, (int)rows, hid, bf, s));
         DT_TRY(gemm_rm(ctx, s, false, true, (int)rows, dm, hid, S.act.ptr, hid,
                        bf ? static_cast<const void*>(Ly.w_down16) : static_cast<const void*>(Ly.w_down), hid, 0.0f, mo,
@@ -504,7 +506,7 @@ int dt_model_bwd(dt_model* M, const float* d_logits, int mem, void* stream) {
             DT_TRY(gemm_rm(ctx, s, true, false, dm, hid, rows, dmo, dm, Ly.act.ptr, hid, 1.0f, Ly.g_down, hid, false));
             DT_TRY(gemm_rm(ctx, s, false, false, rows, hid, dm, dmo, dm, Ly.w_down, hid, 0.0f, d_act, hid, false));
         }
-        DT_TRY(launch_swiglu_bwd(d_act, static_cast<const float*>(Ly.gu.ptr), M->d_gu.ptr, rows, hid, bf, s));
+        DT_TRY(launch_swiglu_bwd(d_act, Ly.gu.ptr, M->d_gu.ptr, rows, hid, bf, s));
         const void* hin = bf ? Ly.h16.ptr : Ly.h.ptr;
         const void* wgu = bf ? static_cast<const void*>(Ly.w_gu16) : static_cast<const void*>(Ly.w_gu);
         DT_TRY(gemm_rm(ctx, s, true, false, 2 * hid, dm, rows, M->d_gu.ptr, 2 * hid, hin, dm, 1.0f, Ly.g_gu, dm, bf));

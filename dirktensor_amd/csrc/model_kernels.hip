@@ -81,15 +81,28 @@ __global__ __launch_bounds__(256) void rmsnorm_rows_kernel(const float* a, const
     }
 }
 
-// act[r][i] = silu(gu[r][i]) * gu[r][hid + i]; fp32 or bf16 output (grid-stride over rows * hid / 4)
+__device__ __forceinline__ float4 load4(const void* p, int64_t idx, bool bf16) {
+    if (bf16) {
+        const uint2 w = *reinterpret_cast<const uint2*>(static_cast<const uint16_t*>(p) + idx);
+        return make_float4(__builtin_bit_cast(float, w.x << 16), __builtin_bit_cast(float, w.x & 0xffff0000u),
+                           __builtin_bit_cast(float, w.y << 16), __builtin_bit_cast(float, w.y & 0xffff0000u));
+    }
+    return *reinterpret_cast<const float4*>(static_cast<const float*>(p) + idx);
+}
+__device__ __forceinline__ float load1(const void* p, int64_t idx, bool bf16) {
+    if (bf16) return __builtin_bit_cast(float, (uint32_t)static_cast<const uint16_t*>(p)[idx] << 16);
+    return static_cast<const float*>(p)[idx];
+}
+
+// act[r][i] = silu(gu[r][i]) * gu[r][hid + i]; gu and act both fp32, or both bf16 (grid-stride over rows * hid / 4)
 template <bool kBF16>
-__global__ __launch_bounds__(256) void swiglu_kernel(const float* gu, void* act, int64_t rows, int hid) {
+__global__ __launch_bounds__(256) void swiglu_kernel(const void* gu, void* act, int64_t rows, int hid) {
     const int64_t n4 = rows * (hid / 4);
     for (int64_t q = (int64_t)blockIdx.x * 256 + threadIdx.x; q < n4; q += (int64_t)gridDim.x * 256) {
         const int64_t r = q / (hid / 4);
         const int i = (int)(q - r * (hid / 4)) * 4;
-        const float4 g = *reinterpret_cast<const float4*>(gu + r * 2 * hid + i);
-        const float4 u = *reinterpret_cast<const float4*>(gu + r * 2 * hid + hid + i);
+        const float4 g = load4(gu, r * 2 * hid + i, kBF16);
+        const float4 u = load4(gu, r * 2 * hid + hid + i, kBF16);
         const float4 o = make_float4(g.x / (1.0f + expf(-g.x)) * u.x, g.y / (1.0f + expf(-g.y)) * u.y,
                                      g.z / (1.0f + expf(-g.z)) * u.z, g.w / (1.0f + expf(-g.w)) * u.w);
         if constexpr (kBF16) {
@@ -224,16 +237,16 @@ __global__ __launch_bounds__(256) void col_reduce_kernel(const float* partial, i
     grad[j] += s;
 }
 
-// from d_act and the saved [gate | up] rows: d_gu = [d_gate | d_up] (fp32 or bf16 output)
+// from d_act and the saved [gate | up] rows: d_gu = [d_gate | d_up] (gu and d_gu fp32, or both bf16)
 template <bool kBF16>
-__global__ __launch_bounds__(256) void swiglu_bwd_kernel(const float* d_act, const float* gu, void* d_gu, int64_t rows,
+__global__ __launch_bounds__(256) void swiglu_bwd_kernel(const float* d_act, const void* gu, void* d_gu, int64_t rows,
                                                          int hid) {
     const int64_t n = rows * hid;
     for (int64_t q = (int64_t)blockIdx.x * 256 + threadIdx.x; q < n; q += (int64_t)gridDim.x * 256) {
         const int64_t r = q / hid;
         const int i = (int)(q - r * hid);
         const float da = d_act[q];
-        const float gate = gu[r * 2 * hid + i], up = gu[r * 2 * hid + hid + i];
+        const float gate = load1(gu, r * 2 * hid + i, kBF16), up = load1(gu, r * 2 * hid + hid + i, kBF16);
         const float sig = 1.0f / (1.0f + expf(-gate));
         const float silu = gate * sig;
         const float d_up = da * silu;
@@ -301,7 +314,7 @@ int launch_rmsnorm_rows(const float* a, const float* w, const float* res, float*
     return DT_OK;
 }
 
-int launch_swiglu(const float* gu, void* act, int rows, int hid, int bf16, hipStream_t s) {
+int launch_swiglu(const void* gu, void* act, int rows, int hid, int bf16, hipStream_t s) {
     const unsigned g = grid_for((int64_t)rows * hid / 4);
     if (bf16) hipLaunchKernelGGL(swiglu_kernel<true>, dim3(g), dim3(256), 0, s, gu, act, (int64_t)rows, hid);
     else hipLaunchKernelGGL(swiglu_kernel<false>, dim3(g), dim3(256), 0, s, gu, act, (int64_t)rows, hid);
@@ -332,7 +345,7 @@ int launch_rmsnorm_bwd(const float* dy, const float* y, const float* rms, const 
     return DT_OK;
 }
 
-int launch_swiglu_bwd(const float* d_act, const float* gu, void* d_gu, int rows, int hid, int bf16, hipStream_t s) {
+int launch_swiglu_bwd(const float* d_act, const void* gu, void* d_gu, int rows, int hid, int bf16, hipStream_t s) {
     const unsigned g = grid_for((int64_t)rows * hid);
     if (bf16) hipLaunchKernelGGL(swiglu_bwd_kernel<true>, dim3(g), dim3(256), 0, s, d_act, gu, d_gu, (int64_t)rows, hid);
     else hipLaunchKernelGGL(swiglu_bwd_kernel<false>, dim3(g), dim3(256), 0, s, d_act, gu, d_gu, (int64_t)rows, hid);
