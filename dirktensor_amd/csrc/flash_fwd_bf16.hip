@@ -59,7 +59,7 @@
 // Keys with k_pos > q_pos are masked (FlashAttention.cpp:102); a row with no
 // valid key is written as the reference's empty row (FlashAttention.cpp:165-174).
 
-#include "dt_internal.h"
+#include "flash_items.h"
 
 #include <algorithm>
 #include <type_traits>
@@ -78,7 +78,7 @@ typedef __attribute__((address_space(3))) shortx4 lds_shortx4;
 typedef __attribute__((address_space(3))) void lds_void;
 
 constexpr int kD = 128;
-constexpr int kBM = 128;       // queries per item
+constexpr int kBM = kItemRows;  // queries per item
 constexpr int kBN = 64;        // keys per tile
 constexpr int kThreads = 512;  // 8 waves
 constexpr int kRowBytes = 256;               // one K or V row (128 bf16), unpadded
@@ -117,45 +117,6 @@ __device__ __forceinline__ float bf16_hi(uint32_t w) { return __builtin_bit_cast
 
 // chunk swizzle of an LDS row: chunk c of row r lives at position c ^ swz(r)
 __device__ __forceinline__ int swz(int r) { return ((r & 3) << 2) | ((r >> 2) & 3); }
-
-struct Item {
-    int b, h, qt;
-};
-
-// Item order of a ragged batch, built on the host: the items that compute (query tiles that start
-// before their sequence's end) sorted by decreasing causal cost, i.e. query tile from the last to the
-// first and, within a tile, the sequences long enough to reach it; then the padding items (tiles past
-// a sequence's end, which only write the empty rows).
-struct RaggedOrder {
-    int n_valid;             // computing items
-    int cum_valid[65];       // cum_valid[j]: computing items in the tiles n_qt-1 .. n_qt-j
-    int cum_pad[65];         // the same for padding items
-    int nb[64];              // nb[qt]: sequences with rows in tile qt
-    uint16_t order[kMaxRaggedBatch];  // sequences by decreasing length (stable)
-};
-
-__device__ __forceinline__ Item decode_item(int k, int n_qt, int BH, int H) {
-    Item it;
-    it.qt = n_qt - 1 - k / BH;  // items sorted by decreasing causal cost
-    const int r = k % BH;
-    it.b = r / H;
-    it.h = r % H;
-    return it;
-}
-
-__device__ __forceinline__ Item decode_item_ragged(int k, int n_qt, int H, const RaggedOrder& ro) {
-    const bool pad = k >= ro.n_valid;
-    const int* cum = pad ? ro.cum_pad : ro.cum_valid;
-    const int kk = pad ? k - ro.n_valid : k;
-    int j = 0;
-    while (j + 1 < n_qt && cum[j + 1] <= kk) ++j;
-    Item it;
-    it.qt = n_qt - 1 - j;
-    const int r = kk - cum[j];
-    it.b = ro.order[(pad ? ro.nb[it.qt] : 0) + r / H];
-    it.h = r % H;
-    return it;
-}
 
 // Per-wave state of one item.
 struct Acc {
@@ -347,7 +308,7 @@ __global__ __launch_bounds__(kThreads, 1) void flash_fwd_bf16_kernel(FlashArgs a
     const float c = a.scale * kLog2e;
 
     for (int round = 0;; ++round) {
-        const int k_item = (round & 1) ? (round + 1) * G - 1 - (int)blockIdx.x : round * G + (int)blockIdx.x;
+        const int k_item = snake_item(round, G, (int)blockIdx.x);
         if (k_item >= n_items) break;
         const Item itm = a.ragged ? decode_item_ragged(k_item, n_qt, a.H, ro) : decode_item(k_item, n_qt, BH, a.H);
         const int b = itm.b, h = itm.h;
@@ -516,9 +477,22 @@ __global__ __launch_bounds__(kThreads, 1) void flash_fwd_bf16_kernel(FlashArgs a
     }
 }
 
-int g_num_cus[64];
-
 }  // namespace
+
+int persistent_grid(int64_t n_items, int* grid) {
+    static int num_cus[64];
+    int dev = 0;
+    DT_HIP_TRY(hipGetDevice(&dev));
+    if (dev < 0 || dev >= 64) return set_error(DT_ERR_UNSUPPORTED, "device index %d out of range", dev);
+    if (num_cus[dev] == 0) {
+        int n = 0;
+        DT_HIP_TRY(hipDeviceGetAttribute(&n, hipDeviceAttributeMultiprocessorCount, dev));
+        num_cus[dev] = n > 0 ? n : 1;
+    }
+    if (n_items > 0x7fffffff) return set_error(DT_ERR_UNSUPPORTED, "too many attention items");
+    *grid = (int)(n_items < num_cus[dev] ? n_items : num_cus[dev]);
+    return DT_OK;
+}
 
 int launch_flash_fwd_bf16(const FlashArgs& a, const SeqLens* lens, hipStream_t stream) {
     SeqLens sl;
@@ -527,36 +501,10 @@ int launch_flash_fwd_bf16(const FlashArgs& a, const SeqLens* lens, hipStream_t s
     if (a.ldk != a.ldv) return set_error(DT_ERR_UNSUPPORTED, "bf16 kernel needs equal K and V row strides");
     if ((int64_t)a.T * a.ldk * 2 >= ((int64_t)1 << 31))
         return set_error(DT_ERR_UNSUPPORTED, "K/V extent of one sequence exceeds 2 GiB");
-    int dev = 0;
-    DT_HIP_TRY(hipGetDevice(&dev));
-    if (dev < 0 || dev >= 64) return set_error(DT_ERR_UNSUPPORTED, "device index %d out of range", dev);
-    if (g_num_cus[dev] == 0) {
-        int n = 0;
-        DT_HIP_TRY(hipDeviceGetAttribute(&n, hipDeviceAttributeMultiprocessorCount, dev));
-        g_num_cus[dev] = n > 0 ? n : 1;
-    }
-    const int64_t n_items = (int64_t)((a.T + kBM - 1) / kBM) * a.B * a.H;
-    if (n_items > 0x7fffffff) return set_error(DT_ERR_UNSUPPORTED, "too many attention items");
-    const int grid = (int)(n_items < g_num_cus[dev] ? n_items : g_num_cus[dev]);
-    RaggedOrder ro{};
-    if (a.ragged) {
-        const int n_qt = (a.T + kBM - 1) / kBM;  // <= 64: T <= 8192 is checked by the caller
-        int idx[kMaxRaggedBatch];
-        for (int b = 0; b < a.B; ++b) idx[b] = b;
-        std::stable_sort(idx, idx + a.B, [&](int x, int y) { return sl.len[x] > sl.len[y]; });
-        for (int b = 0; b < a.B; ++b) ro.order[b] = (uint16_t)idx[b];
-        for (int qt = 0; qt < n_qt; ++qt) {
-            int nb = 0;
-            for (int b = 0; b < a.B; ++b) nb += sl.len[b] > qt * kBM;
-            ro.nb[qt] = nb;
-        }
-        for (int j = 0; j < n_qt; ++j) {
-            const int qt = n_qt - 1 - j;
-            ro.cum_valid[j + 1] = ro.cum_valid[j] + ro.nb[qt] * a.H;
-            ro.cum_pad[j + 1] = ro.cum_pad[j] + (a.B - ro.nb[qt]) * a.H;
-        }
-        ro.n_valid = ro.cum_valid[n_qt];
-    }
+    int grid = 0;
+    DT_TRY(persistent_grid((int64_t)((a.T + kBM - 1) / kBM) * a.B * a.H, &grid));
+    RaggedOrder ro;
+    build_ragged_order(a, sl, &ro);
     hipLaunchKernelGGL(flash_fwd_bf16_kernel, dim3(grid), dim3(kThreads), 0, stream, a, sl, ro);
     DT_HIP_TRY(hipGetLastError());
     return DT_OK;
