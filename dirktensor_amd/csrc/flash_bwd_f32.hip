@@ -19,11 +19,20 @@
 // with row 32*blk + 8*(i/4) + 4*hh + i%4, the accumulator layout, and the A
 // operand is one float of that row read from LDS.
 //
-// Tiles are staged through registers: the next tile's global loads are issued
-// before the current tile's products and written to LDS after them (two
-// barriers per tile). LDS rows are padded to 132 floats.
+// Tiles move from HBM straight into LDS with buffer_load ... lds, double-buffered
+// (the next tile streams in while the current one is used; one barrier per
+// tile). LDS rows are 512 bytes (128 floats), unpadded; the 16-byte chunk c of
+// row r is stored at chunk position c ^ (r & 15), so the row-wise reads of the
+// head-dimension products (16 rows, one chunk each) are conflict-free; the
+// column reads of the other products (two rows, 8 chunks each) meet in pairs
+// of banks (LDS bandwidth is far from the limit at fp32 MFMA rates). Every LDS
+// operand goes through a four-deep register ring, three reads ahead of the
+// MFMAs that consume it.
 
 #include "dt_internal.h"
+
+#include <type_traits>
+#include <utility>
 
 namespace dt {
 namespace {
@@ -32,10 +41,13 @@ typedef float floatx16 __attribute__((ext_vector_type(16)));
 
 constexpr int kD = 128;
 constexpr int kTile = 64;
-constexpr int kLd = 132;  // LDS row stride (floats)
+constexpr int kRowBytes = kD * 4;              // one LDS row, unpadded
+constexpr int kTileBytes = kTile * kRowBytes;  // 32 KB
 constexpr int kBlk = 128;
 constexpr int kThreads = 256;
 constexpr float kLog2e = 1.4426950408889634f;
+constexpr int kBufferDword3 = 0x00020000;  // raw buffer, 32-bit data format (gfx9 family)
+typedef __attribute__((address_space(3))) void lds_void;
 
 __device__ __forceinline__ floatx16 mfma(float a, float b, floatx16 c) {
     return __builtin_amdgcn_mfma_f32_32x32x2f32(a, b, c, 0, 0, 0);
@@ -47,21 +59,64 @@ __device__ __forceinline__ floatx16 zero16() {
     return z;
 }
 
-// A 64 x 128 fp32 tile in flight: thread tid holds rows tid/32 + 8*j (j < 8), floats 4*(tid%32) .. +3
-struct TileRegs {
-    float4 v[8];
-};
-__device__ __forceinline__ void tile_load(TileRegs& R, const float* base, int r0, int T, int ld, int tid) {
+template <typename F, int... Is>
+__device__ __forceinline__ void static_for_impl(F&& f, std::integer_sequence<int, Is...>) {
+    (f(std::integral_constant<int, Is>{}), ...);
+}
+// calls f(std::integral_constant<int, I>{}) for I = 0 .. N-1 (compile-time unrolled)
+template <int N, typename F>
+__device__ __forceinline__ void static_for(F&& f) {
+    static_for_impl(f, std::make_integer_sequence<int, N>{});
+}
+// keeps each group of MFMAs with the LDS reads issued beside it: the scheduler may not move work across
+#define DT_BUNDLE_END __builtin_amdgcn_sched_barrier(0)
+
+// x as an opaque value at this point: address arithmetic derived from it is done where it is used instead
+// of being hoisted out of the tile loop into long-lived registers
+__device__ __forceinline__ int fresh(int x) {
+    asm volatile("" : "+v"(x));
+    return x;
+}
+// byte offset of float x of row r in a swizzled LDS tile
+__device__ __forceinline__ int swz(int r) { return r & 15; }
+
+// Buffer descriptor over [base, base + bytes): loads at or past the end return zeros.
+__device__ __forceinline__ __amdgpu_buffer_rsrc_t make_rsrc(const void* base, uint32_t bytes) {
+    return __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(base), (short)0, (int)bytes, kBufferDword3);
+}
+// LDS DMA issued through inline assembly: the compiler does not track these loads, so it does not wait
+// for them before reading the other LDS stage; stage_barrier() waits for them before any wave reads the
+// stage they fill. M0 (an operand bound to M0) holds the wave-uniform LDS destination; lane i writes 16
+// (or 4) bytes at M0 + 16*i (4*i).
+__device__ __forceinline__ uint32_t lds_addr(const void* p) { return (uint32_t)(uintptr_t)(const lds_void*)p; }
+__device__ __forceinline__ void dma16(uint32_t lds, uint32_t voff, __amdgpu_buffer_rsrc_t r) {
+    asm volatile("buffer_load_dwordx4 %0, %1, 0 offen lds" ::"v"(voff), "s"(r), "{m0}"(lds) : "memory");
+}
+__device__ __forceinline__ void dma4(uint32_t lds, uint32_t voff, __amdgpu_buffer_rsrc_t r) {
+    asm volatile("buffer_load_dword %0, %1, 0 offen lds" ::"v"(voff), "s"(r), "{m0}"(lds) : "memory");
+}
+// this wave's LDS DMA and LDS accesses are complete before any wave passes it
+__device__ __forceinline__ void stage_barrier() { asm volatile("s_waitcnt vmcnt(0) lgkmcnt(0)\n\ts_barrier" ::: "memory"); }
+
+// rows r0 .. T-1 of a [T][ld] fp32 tensor -> one LDS tile (rows past T arrive as zeros). Instruction n
+// of wave w fills LDS rows 2*(4n + w) and 2*(4n + w) + 1 (1 KB, 16 bytes per lane at chunk position
+// lane % 32); the lane fetches the chunk the swizzle puts there. The row offsets are formed here from
+// one opaque value rather than kept in registers across the tile loop.
+__device__ __forceinline__ void dma_tile(uint8_t* tile, const float* base, int r0, int T, int ld, int lane, int wave) {
+    const __amdgpu_buffer_rsrc_t r = make_rsrc(base + (int64_t)r0 * ld, (uint32_t)(T - r0) * (uint32_t)ld * 4u);
+    const uint32_t l0 = __builtin_amdgcn_readfirstlane(lds_addr(tile + wave * 1024));
+    const int r_lane = fresh(2 * wave + (lane >> 5));  // row of instruction 0; instruction n adds 8n
+    const int pos = lane & 31;
 #pragma unroll
-    for (int j = 0; j < 8; ++j) {
-        const int r = r0 + (tid >> 5) + 8 * j;
-        R.v[j] = r < T ? *reinterpret_cast<const float4*>(base + (int64_t)r * ld + 4 * (tid & 31))
-                       : make_float4(0.f, 0.f, 0.f, 0.f);
+    for (int n = 0; n < 8; ++n) {
+        const int row = r_lane + 8 * n;
+        dma16(l0 + 4096 * n, (uint32_t)((row * ld + 4 * (pos ^ swz(row))) * 4), r);
     }
 }
-__device__ __forceinline__ void tile_store(float* lds, const TileRegs& R, int tid) {
-#pragma unroll
-    for (int j = 0; j < 8; ++j) *reinterpret_cast<float4*>(lds + ((tid >> 5) + 8 * j) * kLd + 4 * (tid & 31)) = R.v[j];
+// 64 floats t0 .. t0+63 of a [T] row -> LDS (one wave; entries past T arrive as zeros)
+__device__ __forceinline__ void dma_stats(float* dst, const float* base, int t0, int T, int lane) {
+    const __amdgpu_buffer_rsrc_t r = make_rsrc(base + t0, (uint32_t)(T - t0) * 4u);
+    dma4(__builtin_amdgcn_readfirstlane(lds_addr(dst)), (uint32_t)lane * 4u, r);
 }
 // one row half from global memory: f[s] = X[row][64*hh + s], zeros when row >= T
 __device__ __forceinline__ void load_half_row(float (&f)[64], const float* base, int row, int T, int ld, int hh) {
@@ -81,30 +136,72 @@ __device__ __forceinline__ void load_half_row(float (&f)[64], const float* base,
     }
 }
 // C[32 rows of block blk] += X[rows][64*hh + s] * f[s] over s: the product over the head dimension with
-// the LDS tile's rows as M and a register row half as the B operand
-__device__ __forceinline__ floatx16 dot_rows(const float* tile, int blk, int ln, int hh, const float (&f)[64]) {
-    floatx16 acc = zero16();
-    const float* row = tile + (32 * blk + ln) * kLd + 64 * hh;
-#pragma unroll
-    for (int j = 0; j < 16; ++j) {
-        const float4 x = *reinterpret_cast<const float4*>(row + 4 * j);
-        acc = mfma(x.x, f[4 * j], acc);
-        acc = mfma(x.y, f[4 * j + 1], acc);
-        acc = mfma(x.z, f[4 * j + 2], acc);
-        acc = mfma(x.w, f[4 * j + 3], acc);
-    }
-    return acc;
+// the LDS tile's rows as M and a register row half as the B operand. Two such products (tiles x and y,
+// register halves fx and fy) run as two interleaved accumulator chains, so consecutive MFMAs never
+// depend on each other; the LDS operands go through a three-deep register ring, two reads ahead of
+// the MFMAs that consume them.
+__device__ __forceinline__ void dot_rows2(floatx16& cx, floatx16& cy, const uint8_t* tx, const uint8_t* ty, int blk,
+                                          int ln, int hh, const float (&fx)[64], const float (&fy)[64]) {
+    cx = zero16();
+    cy = zero16();
+    // chunk 16*hh + j of row r = 32*blk + ln sits at position 16*hh + (j ^ (ln & 15))
+    const int base = fresh((32 * blk + ln) * kRowBytes + 256 * hh) | ((ln & 15) << 4);
+    auto rd = [&](const uint8_t* t, int j) { return *reinterpret_cast<const float4*>(t + (base ^ (j << 4))); };
+    float4 x[3], y[3];
+    x[0] = rd(tx, 0);
+    y[0] = rd(ty, 0);
+    x[1] = rd(tx, 1);
+    y[1] = rd(ty, 1);
+    static_for<16>([&](auto J) {
+        constexpr int j = decltype(J)::value;
+        if constexpr (j + 2 < 16) {
+            x[(j + 2) % 3] = rd(tx, j + 2);
+            y[(j + 2) % 3] = rd(ty, j + 2);
+        }
+        const float4 u = x[j % 3], v = y[j % 3];
+        cx = mfma(u.x, fx[4 * j], cx);
+        cy = mfma(v.x, fy[4 * j], cy);
+        cx = mfma(u.y, fx[4 * j + 1], cx);
+        cy = mfma(v.y, fy[4 * j + 1], cy);
+        cx = mfma(u.z, fx[4 * j + 2], cx);
+        cy = mfma(v.z, fy[4 * j + 2], cy);
+        cx = mfma(u.w, fx[4 * j + 3], cx);
+        cy = mfma(v.w, fy[4 * j + 3], cy);
+        DT_BUNDLE_END;
+    });
 }
 // acc[db] += sum over the 64 tile rows of tile[row][32*db + ln] * w[blk][i], row = 32*blk + 8*(i/4) + 4*hh + i%4
-__device__ __forceinline__ void acc_cols(floatx16 (&acc)[4], const float* tile, int ln, int hh, const floatx16 (&w)[2]) {
-#pragma unroll
-    for (int blk = 0; blk < 2; ++blk)
-#pragma unroll
-        for (int i = 0; i < 16; ++i) {
-            const float* row = tile + (32 * blk + 8 * (i / 4) + 4 * hh + (i % 4)) * kLd + ln;
-#pragma unroll
-            for (int db = 0; db < 4; ++db) acc[db] = mfma(row[32 * db], w[blk][i], acc[db]);
-        }
+// (step t = 16*blk + i reads its four LDS values, one per db, three steps ahead)
+__device__ __forceinline__ void acc_cols(floatx16 (&acc)[4], const uint8_t* tile, int ln, int hh, const floatx16 (&w)[2]) {
+    // float 32*db + ln of row r = 32*(t/16) + 8*((t%16)/4) + 4*hh + t%4 is chunk 8*db + ln/4, at position
+    // (8*db + ln/4) ^ (r & 15) = 8*(db ^ ((t/4) & 1)) + ((ln/4) ^ (4*hh + t%4))
+    const int lane_part = fresh((hh * 4) * kRowBytes + 4 * (ln & 3));
+    const int cx = fresh((ln >> 2) ^ (4 * hh));
+    auto rd = [&](int t) {
+        const int i = t & 15;
+        const int r0 = 32 * (t >> 4) + 8 * (i / 4) + (i % 4);  // row without the lane half
+        const int g = (t >> 2) & 1;
+        const uint8_t* row = tile + r0 * kRowBytes + lane_part + ((cx ^ (t & 3)) << 4);
+        return make_float4(*reinterpret_cast<const float*>(row + ((0 ^ g) << 7)),
+                           *reinterpret_cast<const float*>(row + ((1 ^ g) << 7)),
+                           *reinterpret_cast<const float*>(row + ((2 ^ g) << 7)),
+                           *reinterpret_cast<const float*>(row + ((3 ^ g) << 7)));
+    };
+    float4 x[4];
+    x[0] = rd(0);
+    x[1] = rd(1);
+    x[2] = rd(2);
+    static_for<32>([&](auto Tc) {
+        constexpr int t = decltype(Tc)::value;
+        if constexpr (t + 3 < 32) x[(t + 3) & 3] = rd(t + 3);
+        const float4 v = x[t & 3];
+        const float wv = w[t >> 4][t & 15];
+        acc[0] = mfma(v.x, wv, acc[0]);
+        acc[1] = mfma(v.y, wv, acc[1]);
+        acc[2] = mfma(v.z, wv, acc[2]);
+        acc[3] = mfma(v.w, wv, acc[3]);
+        DT_BUNDLE_END;
+    });
 }
 // accumulator X^T (4 blocks of 32 dims x 32 rows, lane = row) * mul -> row `row` of [T][ld] at base
 __device__ __forceinline__ void store_rows(float* base, int row, int ld, int hh, const floatx16 (&x)[4], float mul) {
@@ -118,15 +215,20 @@ __device__ __forceinline__ void store_rows(float* base, int row, int ld, int hh,
 }
 
 // ------------------------------------------------------------------------------------------------ dK, dV
+// LDS stage: Q tile, dO tile, and the tile rows' lse2 and delta
+struct DkdvStage {
+    uint8_t q[kTileBytes];
+    uint8_t g[kTileBytes];
+    float lse2[kTile];
+    float delta[kTile];
+};
+
 __global__ __launch_bounds__(kThreads, 1) void flash_bwd_dkdv_f32_kernel(FlashBwdArgs a) {
-    __shared__ __attribute__((aligned(16))) float Qs[kTile * kLd];
-    __shared__ __attribute__((aligned(16))) float Gs[kTile * kLd];
-    __shared__ __attribute__((aligned(16))) float Ls[kTile];
-    __shared__ __attribute__((aligned(16))) float Ds[kTile];
+    __shared__ __attribute__((aligned(1024))) DkdvStage stg[2];
 
     const int tid = threadIdx.x;
     const int lane = tid & 63;
-    const int wave = tid >> 6;
+    const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
     const int ln = lane & 31;
     const int hh = lane >> 5;
     const int T = a.T;
@@ -147,11 +249,23 @@ __global__ __launch_bounds__(kThreads, 1) void flash_bwd_dkdv_f32_kernel(FlashBw
     float* dKg = static_cast<float*>(a.d_k) + (int64_t)b * T * a.ld_grad + (int64_t)h * kD;
     float* dVg = static_cast<float*>(a.d_v) + (int64_t)b * T * a.ld_grad + (int64_t)h * kD;
 
+    // Q, dO, lse2 and delta rows q0 .. q0+63 -> stage s
+    auto fetch = [&](DkdvStage& s, int q0) {
+        dma_tile(s.q, Qg, q0, T, a.ld_qkv, lane, wave);
+        dma_tile(s.g, Gg, q0, T, a.ld_o, lane, wave);
+        if (wave == 0) dma_stats(s.lse2, lse2g, q0, T, lane);
+        if (wave == 1) dma_stats(s.delta, deltag, q0, T, lane);
+    };
+
     for (int half = 0; half < 2; ++half) {
         const int kb = half ? nkb - 1 - pair : pair;
         if (half && kb == pair) break;
         const int kw = kb * kBlk + 32 * wave;
         const int key = kw + ln;
+
+        const int q_begin = a.causal ? kb * kBlk : 0;
+        const int n_steps = (T - q_begin + kTile - 1) / kTile;
+        fetch(stg[0], q_begin);  // both stages are free: the previous block ended with a barrier
 
         float kf[64], vf[64];
         load_half_row(kf, Kg, key, T, a.ld_qkv, hh);
@@ -162,61 +276,32 @@ __global__ __launch_bounds__(kThreads, 1) void flash_bwd_dkdv_f32_kernel(FlashBw
             dv[db] = zero16();
             dk[db] = zero16();
         }
-
-        const int q_begin = a.causal ? kb * kBlk : 0;
-        const int n_steps = (T - q_begin + kTile - 1) / kTile;
-        TileRegs rq, rg;
-        float rl = 0.0f, rd = 0.0f;
-        auto fetch = [&](int q0) {
-            tile_load(rq, Qg, q0, T, a.ld_qkv, tid);
-            tile_load(rg, Gg, q0, T, a.ld_o, tid);
-            if (tid < kTile) {
-                rl = q0 + tid < T ? lse2g[q0 + tid] : 0.0f;
-                rd = q0 + tid < T ? deltag[q0 + tid] : 0.0f;
-            }
-        };
-        auto commit = [&]() {
-            tile_store(Qs, rq, tid);
-            tile_store(Gs, rg, tid);
-            if (tid < kTile) {
-                Ls[tid] = rl;
-                Ds[tid] = rd;
-            }
-        };
-        fetch(q_begin);
-        __syncthreads();  // the previous block's last tile is no longer read
-        commit();
-        __syncthreads();
+        stage_barrier();
         for (int it = 0; it < n_steps; ++it) {
             const int q0 = q_begin + it * kTile;
-            if (it + 1 < n_steps) fetch(q0 + kTile);
+            const DkdvStage& s = stg[it & 1];
+            if (it + 1 < n_steps) fetch(stg[(it + 1) & 1], q0 + kTile);
             if (!(a.causal && q0 + kTile - 1 < kw)) {
                 const bool need_mask = a.causal && q0 < kw + 31;
                 floatx16 sc[2], dp[2];
-#pragma unroll
-                for (int qb = 0; qb < 2; ++qb) {
-                    sc[qb] = dot_rows(Qs, qb, ln, hh, kf);  // S = Q K^T (raw)
-                    dp[qb] = dot_rows(Gs, qb, ln, hh, vf);  // dP = dO V^T
-                }
-                floatx16 p[2], ds[2];
+                // S = Q K^T (raw), dP = dO V^T (two query blocks; explicit calls keep every index static)
+                dot_rows2(sc[0], dp[0], s.q, s.g, 0, ln, hh, kf, vf);
+                dot_rows2(sc[1], dp[1], s.q, s.g, 1, ln, hh, kf, vf);
+                // P and dS overwrite S and dP in place
 #pragma unroll
                 for (int qb = 0; qb < 2; ++qb)
 #pragma unroll
                     for (int i = 0; i < 16; ++i) {
                         const int qi = 32 * qb + 8 * (i / 4) + 4 * hh + (i % 4);
-                        float pv = __builtin_amdgcn_exp2f(sc[qb][i] * c - Ls[qi]);
+                        float pv = __builtin_amdgcn_exp2f(sc[qb][i] * c - s.lse2[qi]);
                         if (need_mask && key > q0 + qi) pv = 0.0f;
-                        p[qb][i] = pv;
-                        ds[qb][i] = pv * (dp[qb][i] - Ds[qi]);
+                        sc[qb][i] = pv;
+                        dp[qb][i] = pv * (dp[qb][i] - s.delta[qi]);
                     }
-                acc_cols(dv, Gs, ln, hh, p);   // dV^T += dO^T P
-                acc_cols(dk, Qs, ln, hh, ds);  // dK^T += Q^T dS
+                acc_cols(dv, s.g, ln, hh, sc);  // dV^T += dO^T P
+                acc_cols(dk, s.q, ln, hh, dp);  // dK^T += Q^T dS
             }
-            if (it + 1 < n_steps) {
-                __syncthreads();
-                commit();
-                __syncthreads();
-            }
+            stage_barrier();  // stage it&1 is free for the tile after next; tile it+1 has landed
         }
         if (key < T) {
             store_rows(dKg, key, a.ld_grad, hh, dk, a.scale);  // dS carries the reference's scale (:293)
@@ -226,13 +311,18 @@ __global__ __launch_bounds__(kThreads, 1) void flash_bwd_dkdv_f32_kernel(FlashBw
 }
 
 // ------------------------------------------------------------------------------------------------ dQ
+// LDS stage: K tile, V tile
+struct DqStage {
+    uint8_t k[kTileBytes];
+    uint8_t v[kTileBytes];
+};
+
 __global__ __launch_bounds__(kThreads, 1) void flash_bwd_dq_f32_kernel(FlashBwdArgs a) {
-    __shared__ __attribute__((aligned(16))) float Ks[kTile * kLd];
-    __shared__ __attribute__((aligned(16))) float Vs[kTile * kLd];
+    __shared__ __attribute__((aligned(1024))) DqStage stg[2];
 
     const int tid = threadIdx.x;
     const int lane = tid & 63;
-    const int wave = tid >> 6;
+    const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
     const int ln = lane & 31;
     const int hh = lane >> 5;
     const int T = a.T;
@@ -250,11 +340,21 @@ __global__ __launch_bounds__(kThreads, 1) void flash_bwd_dq_f32_kernel(FlashBwdA
     const float* Gg = static_cast<const float*>(a.d_o) + (int64_t)b * T * a.ld_o + (int64_t)h * kD;
     float* dQg = static_cast<float*>(a.d_q) + (int64_t)b * T * a.ld_grad + (int64_t)h * kD;
 
+    // K and V rows k0 .. k0+63 -> stage s
+    auto fetch = [&](DqStage& s, int k0) {
+        dma_tile(s.k, Kg, k0, T, a.ld_qkv, lane, wave);
+        dma_tile(s.v, Vg, k0, T, a.ld_qkv, lane, wave);
+    };
+
     for (int half = 0; half < 2; ++half) {
         const int qb = half ? nqb - 1 - pair : pair;
         if (half && qb == pair) break;
         const int qw = qb * kBlk + 32 * wave;
         const int q = qw + ln;
+
+        const int k_end = a.causal ? min(qb * kBlk + kBlk, T) : T;
+        const int n_steps = (k_end + kTile - 1) / kTile;
+        fetch(stg[0], 0);  // both stages are free: the previous block ended with a barrier
 
         float qf[64], gf[64];
         load_half_row(qf, Qg, q, T, a.ld_qkv, hh);
@@ -266,29 +366,17 @@ __global__ __launch_bounds__(kThreads, 1) void flash_bwd_dq_f32_kernel(FlashBwdA
 #pragma unroll
         for (int db = 0; db < 4; ++db) dq[db] = zero16();
 
-        const int k_end = a.causal ? min(qb * kBlk + kBlk, T) : T;
-        const int n_steps = (k_end + kTile - 1) / kTile;
-        TileRegs rk, rv;
-        tile_load(rk, Kg, 0, T, a.ld_qkv, tid);
-        tile_load(rv, Vg, 0, T, a.ld_qkv, tid);
-        __syncthreads();
-        tile_store(Ks, rk, tid);
-        tile_store(Vs, rv, tid);
-        __syncthreads();
+        stage_barrier();
         for (int it = 0; it < n_steps; ++it) {
             const int k0 = it * kTile;
-            if (it + 1 < n_steps) {
-                tile_load(rk, Kg, k0 + kTile, T, a.ld_qkv, tid);
-                tile_load(rv, Vg, k0 + kTile, T, a.ld_qkv, tid);
-            }
+            const DqStage& s = stg[it & 1];
+            if (it + 1 < n_steps) fetch(stg[(it + 1) & 1], k0 + kTile);
             if (!(a.causal && k0 > qw + 31)) {
                 const bool need_mask = (a.causal && k0 + kTile - 1 > qw) || k0 + kTile > T;
                 floatx16 sc[2], dp[2];
-#pragma unroll
-                for (int kb = 0; kb < 2; ++kb) {
-                    sc[kb] = dot_rows(Ks, kb, ln, hh, qf);  // S^T = K Q^T (raw)
-                    dp[kb] = dot_rows(Vs, kb, ln, hh, gf);  // dP^T = V dO^T
-                }
+                // S^T = K Q^T (raw), dP^T = V dO^T (two key blocks; explicit calls keep every index static)
+                dot_rows2(sc[0], dp[0], s.k, s.v, 0, ln, hh, qf, gf);
+                dot_rows2(sc[1], dp[1], s.k, s.v, 1, ln, hh, qf, gf);
                 floatx16 ds[2];
 #pragma unroll
                 for (int kb = 0; kb < 2; ++kb)
@@ -298,14 +386,9 @@ __global__ __launch_bounds__(kThreads, 1) void flash_bwd_dq_f32_kernel(FlashBwdA
                         if (need_mask && k0 + 32 * kb + 8 * (i / 4) + 4 * hh + (i % 4) > lim) pv = 0.0f;
                         ds[kb][i] = pv * (dp[kb][i] - delta);
                     }
-                acc_cols(dq, Ks, ln, hh, ds);  // dQ^T += K^T dS^T
+                acc_cols(dq, s.k, ln, hh, ds);  // dQ^T += K^T dS^T
             }
-            if (it + 1 < n_steps) {
-                __syncthreads();
-                tile_store(Ks, rk, tid);
-                tile_store(Vs, rv, tid);
-                __syncthreads();
-            }
+            stage_barrier();  // stage it&1 is free for the tile after next; tile it+1 has landed
         }
         if (q < T) store_rows(dQg, q, a.ld_grad, hh, dq, a.scale);
     }
@@ -314,6 +397,9 @@ __global__ __launch_bounds__(kThreads, 1) void flash_bwd_dq_f32_kernel(FlashBwdA
 }  // namespace
 
 int launch_flash_bwd_f32(const FlashBwdArgs& a, hipStream_t stream) {
+    const int64_t ld = a.ld_qkv > a.ld_o ? a.ld_qkv : a.ld_o;
+    if ((int64_t)a.T * ld * 4 >= ((int64_t)1 << 31))
+        return set_error(DT_ERR_UNSUPPORTED, "Q/K/V/dO extent of one sequence exceeds 2 GiB");
     DT_TRY(launch_flash_bwd_prep(a, 0, stream));
     const int64_t npair = ((a.T + kBlk - 1) / kBlk + 1) / 2;
     const int64_t grid = npair * a.B * a.H;
