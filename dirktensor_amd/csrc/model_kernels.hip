@@ -116,6 +116,26 @@ __global__ __launch_bounds__(256) void swiglu_kernel(const void* gu, void* act, 
     }
 }
 
+// bf16 [gate | up] -> bf16 act, eight elements (16 bytes) per thread and step (hid % 8 == 0)
+__global__ __launch_bounds__(256) void swiglu_bf16x8_kernel(const uint16_t* gu, uint16_t* act, int64_t rows, int hid) {
+    const int64_t n8 = rows * (hid / 8);
+    for (int64_t q = (int64_t)blockIdx.x * 256 + threadIdx.x; q < n8; q += (int64_t)gridDim.x * 256) {
+        const int64_t r = q / (hid / 8);
+        const int i = (int)(q - r * (hid / 8)) * 8;
+        const uint4 g = *reinterpret_cast<const uint4*>(gu + r * 2 * hid + i);
+        const uint4 u = *reinterpret_cast<const uint4*>(gu + r * 2 * hid + hid + i);
+        const uint32_t gw[4] = {g.x, g.y, g.z, g.w}, uw[4] = {u.x, u.y, u.z, u.w};
+        uint32_t ow[4];
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+            const float g0 = __builtin_bit_cast(float, gw[e] << 16), g1 = __builtin_bit_cast(float, gw[e] & 0xffff0000u);
+            const float u0 = __builtin_bit_cast(float, uw[e] << 16), u1 = __builtin_bit_cast(float, uw[e] & 0xffff0000u);
+            ow[e] = pack_bf16x2(g0 / (1.0f + expf(-g0)) * u0, g1 / (1.0f + expf(-g1)) * u1);
+        }
+        *reinterpret_cast<uint4*>(act + r * hid + i) = make_uint4(ow[0], ow[1], ow[2], ow[3]);
+    }
+}
+
 // One row of logits: target[row] >= 0 is the next token (a loss term), -1 none (no loss, zero gradient).
 // term[row] = log(sum exp(l - max)) - (l[target] - max); grad row (nullable) = (softmax - onehot) * inv_count.
 __global__ __launch_bounds__(256) void ce_rows_kernel(const float* logits, const int32_t* target, float* term,
@@ -316,7 +336,10 @@ int launch_rmsnorm_rows(const float* a, const float* w, const float* res, float*
 
 int launch_swiglu(const void* gu, void* act, int rows, int hid, int bf16, hipStream_t s) {
     const unsigned g = grid_for((int64_t)rows * hid / 4);
-    if (bf16) hipLaunchKernelGGL(swiglu_kernel<true>, dim3(g), dim3(256), 0, s, gu, act, (int64_t)rows, hid);
+    if (bf16 && hid % 8 == 0)
+        hipLaunchKernelGGL(swiglu_bf16x8_kernel, dim3(grid_for((int64_t)rows * hid / 8)), dim3(256), 0, s,
+                           static_cast<const uint16_t*>(gu), static_cast<uint16_t*>(act), (int64_t)rows, hid);
+    else if (bf16) hipLaunchKernelGGL(swiglu_kernel<true>, dim3(g), dim3(256), 0, s, gu, act, (int64_t)rows, hid);
     else hipLaunchKernelGGL(swiglu_kernel<false>, dim3(g), dim3(256), 0, s, gu, act, (int64_t)rows, hid);
     DT_HIP_TRY(hipGetLastError());
     return DT_OK;
