@@ -615,9 +615,9 @@ int dt_attn_layer_fwd(dt_attn_layer* L, const float* x, float* out, int B, int T
         DT_TRY(run_flash(ctx, fa, seq_lens, DT_FP32_EXACT, s));  // OlmoAttention.cpp:94
         DT_TRY(gemm_xwt(ctx, s, rows, dm, dm, attn, dm, L->w_o, dm, od, dm, false));  // :104
     } else {
-        if (!L->w_qkv16) {
-            DT_HIP_TRY(hipMalloc(&L->w_qkv16, (size_t)3 * dm * dm * 2));
-            DT_HIP_TRY(hipMalloc(&L->w_o16, (size_t)dm * dm * 2));
+        if (!L->w_qkv16 || !L->w_o16) {  // (a failed allocation leaves the pair incomplete: retried here)
+            if (!L->w_qkv16) DT_HIP_TRY(hipMalloc(&L->w_qkv16, (size_t)3 * dm * dm * 2));
+            if (!L->w_o16) DT_HIP_TRY(hipMalloc(&L->w_o16, (size_t)dm * dm * 2));
             L->w16_stale = true;
         }
         if (L->w16_stale) {

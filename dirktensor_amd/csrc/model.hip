@@ -168,11 +168,13 @@ int ensure_model_grads(dt_model* M, hipStream_t s) {
 
 int refresh_bf16(dt_model* M, hipStream_t s) {
     const int64_t dm = M->dm, hid = M->hid, V = M->V;
-    if (!M->lm_head16) {
-        DT_HIP_TRY(hipMalloc(&M->lm_head16, V * dm * 2));
+    bool complete = M->lm_head16 != nullptr;
+    for (const ModelLayer& Ly : M->L) complete = complete && Ly.w_gu16 && Ly.w_down16;
+    if (!complete) {  // first bf16 call, or a failed allocation left the set incomplete: allocate what is missing
+        if (!M->lm_head16) DT_HIP_TRY(hipMalloc(&M->lm_head16, V * dm * 2));
         for (ModelLayer& Ly : M->L) {
-            DT_HIP_TRY(hipMalloc(&Ly.w_gu16, 2 * hid * dm * 2));
-            DT_HIP_TRY(hipMalloc(&Ly.w_down16, dm * hid * 2));
+            if (!Ly.w_gu16) DT_HIP_TRY(hipMalloc(&Ly.w_gu16, 2 * hid * dm * 2));
+            if (!Ly.w_down16) DT_HIP_TRY(hipMalloc(&Ly.w_down16, dm * hid * 2));
         }
         M->w16_stale = true;
     }
