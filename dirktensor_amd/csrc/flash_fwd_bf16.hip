@@ -62,6 +62,7 @@
 #include "flash_items.h"
 
 #include <algorithm>
+#include <atomic>
 #include <type_traits>
 #include <utility>
 
@@ -480,17 +481,19 @@ __global__ __launch_bounds__(kThreads, 1) void flash_fwd_bf16_kernel(FlashArgs a
 }  // namespace
 
 int persistent_grid(int64_t n_items, int* grid) {
-    static int num_cus[64];
+    static std::atomic<int> num_cus[64];  // per device, filled on first use (any thread; same value)
     int dev = 0;
     DT_HIP_TRY(hipGetDevice(&dev));
     if (dev < 0 || dev >= 64) return set_error(DT_ERR_UNSUPPORTED, "device index %d out of range", dev);
-    if (num_cus[dev] == 0) {
+    int cus = num_cus[dev].load(std::memory_order_relaxed);
+    if (cus == 0) {
         int n = 0;
         DT_HIP_TRY(hipDeviceGetAttribute(&n, hipDeviceAttributeMultiprocessorCount, dev));
-        num_cus[dev] = n > 0 ? n : 1;
+        cus = n > 0 ? n : 1;
+        num_cus[dev].store(cus, std::memory_order_relaxed);
     }
     if (n_items > 0x7fffffff) return set_error(DT_ERR_UNSUPPORTED, "too many attention items");
-    *grid = (int)(n_items < num_cus[dev] ? n_items : num_cus[dev]);
+    *grid = (int)(n_items < cus ? n_items : cus);
     return DT_OK;
 }
 
