@@ -22,8 +22,11 @@
 //   instead of the reference's 5) in exchange for no atomics.
 // Causality (FlashAttention.cpp:247, 265-268) limits the dK/dV kernel to query
 // tiles at or after its keys and the dQ kernel to key tiles at or before its
-// queries; a workgroup takes block j and block n-1-j of the same head so that
-// every workgroup has the same number of tiles.
+// queries. Each workgroup owns one 128-row block; the grid lists the blocks in
+// decreasing causal cost, and the hardware gives the next workgroup to the first
+// CU that frees up, which schedules the longest blocks first and fills the tail
+// with the short ones (at T = 6144 the longest CU then carries 81 tile steps
+// for an average of 73.5, where fixed pairs of blocks j and n-1-j carried 98).
 //
 // MFMA operand layouts (v_mfma_f32_32x32x16_bf16): the A operand is a 32-row
 // fragment, lane l holding row l%32 and k elements 8*(l/32) .. +8; the B
@@ -228,10 +231,10 @@ __global__ __launch_bounds__(kThreads, 1) void flash_bwd_dkdv_bf16_kernel(FlashB
     const int T = a.T;
     const float c = a.scale * kLog2e;
 
-    const int nkb = (T + kBlk - 1) / kBlk;
-    const int npair = (nkb + 1) / 2;
-    const int pair = blockIdx.x % npair;
-    const int bh = blockIdx.x / npair;
+    // one key block per workgroup, in decreasing causal cost (key block 0 sees every query tile): the
+    // hardware hands the next workgroup to the first CU that frees up, a longest-first schedule
+    const int kb_own = (int)blockIdx.x / (a.B * a.H);
+    const int bh = (int)blockIdx.x % (a.B * a.H);
     const int b = bh / a.H, h = bh % a.H;
 
     const LaneAddr LA = lane_addr(lane);
@@ -248,9 +251,8 @@ __global__ __launch_bounds__(kThreads, 1) void flash_bwd_dkdv_bf16_kernel(FlashB
     uint16_t* dKg = static_cast<uint16_t*>(a.d_k) + (int64_t)b * T * a.ld_grad + (int64_t)h * kD;
     uint16_t* dVg = static_cast<uint16_t*>(a.d_v) + (int64_t)b * T * a.ld_grad + (int64_t)h * kD;
 
-    for (int half = 0; half < 2; ++half) {
-        const int kb = half ? nkb - 1 - pair : pair;
-        if (half && kb == pair) break;  // odd count: the middle block once
+    {
+        const int kb = kb_own;
         const int kw = kb * kBlk + 32 * wave;  // the wave's first key
         const int key = kw + ln;               // this lane's key (the products' N index)
 
@@ -382,9 +384,10 @@ __global__ __launch_bounds__(kThreads, 1) void flash_bwd_dq_bf16_kernel(FlashBwd
     const float c = a.scale * kLog2e;
 
     const int nqb = (T + kBlk - 1) / kBlk;
-    const int npair = (nqb + 1) / 2;
-    const int pair = blockIdx.x % npair;
-    const int bh = blockIdx.x / npair;
+    // one query block per workgroup, in decreasing causal cost (the last query block sees every key
+    // tile): the hardware hands the next workgroup to the first CU that frees up, a longest-first schedule
+    const int qb_own = nqb - 1 - (int)blockIdx.x / (a.B * a.H);
+    const int bh = (int)blockIdx.x % (a.B * a.H);
     const int b = bh / a.H, h = bh % a.H;
 
     const LaneAddr LA = lane_addr(lane);
@@ -397,9 +400,8 @@ __global__ __launch_bounds__(kThreads, 1) void flash_bwd_dq_bf16_kernel(FlashBwd
     const uint16_t* Gg = static_cast<const uint16_t*>(a.d_o) + (int64_t)b * T * a.ld_o + (int64_t)h * kD;
     uint16_t* dQg = static_cast<uint16_t*>(a.d_q) + (int64_t)b * T * a.ld_grad + (int64_t)h * kD;
 
-    for (int half = 0; half < 2; ++half) {
-        const int qb = half ? nqb - 1 - pair : pair;
-        if (half && qb == pair) break;
+    {
+        const int qb = qb_own;
         const int qw = qb * kBlk + 32 * wave;  // the wave's first query
         const int q = qw + ln;                 // this lane's query (the products' N index)
 
@@ -495,8 +497,7 @@ int launch_flash_bwd_bf16(const FlashBwdArgs& a, hipStream_t stream) {
     if ((int64_t)a.T * a.ld_qkv * 2 >= ((int64_t)1 << 31) || (int64_t)a.T * a.ld_o * 2 >= ((int64_t)1 << 31))
         return set_error(DT_ERR_UNSUPPORTED, "extent of one sequence exceeds 2 GiB");
     DT_TRY(launch_flash_bwd_prep(a, 1, stream));
-    const int64_t npair = ((a.T + kBlk - 1) / kBlk + 1) / 2;
-    const int64_t grid = npair * a.B * a.H;
+    const int64_t grid = (int64_t)((a.T + kBlk - 1) / kBlk) * a.B * a.H;  // one 128-row block per workgroup
     if (grid > 0x7fffffff) return set_error(DT_ERR_UNSUPPORTED, "too many workgroups");
     hipLaunchKernelGGL(flash_bwd_dkdv_bf16_kernel, dim3((unsigned)grid), dim3(kThreads), 0, stream, a);
     DT_HIP_TRY(hipGetLastError());

@@ -8,7 +8,9 @@
 // streams 64-query tiles of Q, dO, lse2 and delta; flash_bwd_dq_f32 owns 128
 // queries (Q and dO rows in registers) and streams 64-key tiles of K and V.
 // Each gradient row has a single owner, so no atomics; S and dP are computed
-// in both kernels. Block j and block n-1-j of a head share a workgroup.
+// in both kernels. Each workgroup owns one block; the grid lists the blocks in
+// decreasing causal cost, so the hardware's first-free-CU dispatch runs the
+// longest blocks first.
 //
 // v_mfma_f32_32x32x2_f32 takes one A value per lane (row l%32, k = l/32) and
 // one B value (column l%32, k = l/32). For the products over the head
@@ -234,10 +236,10 @@ __global__ __launch_bounds__(kThreads, 1) void flash_bwd_dkdv_f32_kernel(FlashBw
     const int T = a.T;
     const float c = a.scale * kLog2e;
 
-    const int nkb = (T + kBlk - 1) / kBlk;
-    const int npair = (nkb + 1) / 2;
-    const int pair = blockIdx.x % npair;
-    const int bh = blockIdx.x / npair;
+    // one key block per workgroup, in decreasing causal cost (key block 0 sees every query tile): the
+    // hardware hands the next workgroup to the first CU that frees up, a longest-first schedule
+    const int kb_own = (int)blockIdx.x / (a.B * a.H);
+    const int bh = (int)blockIdx.x % (a.B * a.H);
     const int b = bh / a.H, h = bh % a.H;
 
     const float* Qg = static_cast<const float*>(a.q) + (int64_t)b * T * a.ld_qkv + (int64_t)h * kD;
@@ -257,9 +259,8 @@ __global__ __launch_bounds__(kThreads, 1) void flash_bwd_dkdv_f32_kernel(FlashBw
         if (wave == 1) dma_stats(s.delta, deltag, q0, T, lane);
     };
 
-    for (int half = 0; half < 2; ++half) {
-        const int kb = half ? nkb - 1 - pair : pair;
-        if (half && kb == pair) break;
+    {
+        const int kb = kb_own;
         const int kw = kb * kBlk + 32 * wave;
         const int key = kw + ln;
 
@@ -329,9 +330,10 @@ __global__ __launch_bounds__(kThreads, 1) void flash_bwd_dq_f32_kernel(FlashBwdA
     const float c = a.scale * kLog2e;
 
     const int nqb = (T + kBlk - 1) / kBlk;
-    const int npair = (nqb + 1) / 2;
-    const int pair = blockIdx.x % npair;
-    const int bh = blockIdx.x / npair;
+    // one query block per workgroup, in decreasing causal cost (the last query block sees every key
+    // tile): the hardware hands the next workgroup to the first CU that frees up, a longest-first schedule
+    const int qb_own = nqb - 1 - (int)blockIdx.x / (a.B * a.H);
+    const int bh = (int)blockIdx.x % (a.B * a.H);
     const int b = bh / a.H, h = bh % a.H;
 
     const float* Qg = static_cast<const float*>(a.q) + (int64_t)b * T * a.ld_qkv + (int64_t)h * kD;
@@ -346,9 +348,8 @@ __global__ __launch_bounds__(kThreads, 1) void flash_bwd_dq_f32_kernel(FlashBwdA
         dma_tile(s.v, Vg, k0, T, a.ld_qkv, lane, wave);
     };
 
-    for (int half = 0; half < 2; ++half) {
-        const int qb = half ? nqb - 1 - pair : pair;
-        if (half && qb == pair) break;
+    {
+        const int qb = qb_own;
         const int qw = qb * kBlk + 32 * wave;
         const int q = qw + ln;
 
@@ -401,8 +402,7 @@ int launch_flash_bwd_f32(const FlashBwdArgs& a, hipStream_t stream) {
     if ((int64_t)a.T * ld * 4 >= ((int64_t)1 << 31))
         return set_error(DT_ERR_UNSUPPORTED, "Q/K/V/dO extent of one sequence exceeds 2 GiB");
     DT_TRY(launch_flash_bwd_prep(a, 0, stream));
-    const int64_t npair = ((a.T + kBlk - 1) / kBlk + 1) / 2;
-    const int64_t grid = npair * a.B * a.H;
+    const int64_t grid = (int64_t)((a.T + kBlk - 1) / kBlk) * a.B * a.H;  // one 128-row block per workgroup
     if (grid > 0x7fffffff) return set_error(DT_ERR_UNSUPPORTED, "too many workgroups");
     hipLaunchKernelGGL(flash_bwd_dkdv_f32_kernel, dim3((unsigned)grid), dim3(kThreads), 0, stream, a);
     DT_HIP_TRY(hipGetLastError());
