@@ -276,6 +276,15 @@ __global__ __launch_bounds__(kThreads, 1) void flash_fwd_bf16_kernel(FlashArgs a
 #pragma unroll
         for (int i = 0; i < 4; ++i) voff[i] = (uint32_t)(((16 * i + 4 * wq + rlo) * a.ldk + 8 * chunk) * 2);
     }
+    // Q DMA of an item's 128 rows: instruction i of wave w fills rows 32*i + 4*w + lane/16, in the same
+    // swizzled layout (swz(32*i + 4*w + lane/16) = 4*(lane/16) + (w & 3) does not depend on i)
+    uint32_t qoff[4];
+    {
+        const int rlo = lane >> 4;
+        const int chunk = (lane & 15) ^ (4 * rlo + (wave & 3));
+#pragma unroll
+        for (int i = 0; i < 4; ++i) qoff[i] = (uint32_t)(((32 * i + 4 * wave + rlo) * a.ldq + 8 * chunk) * 2);
+    }
     // K fragment reads: row 32*kb + ln, chunk 2*cc + hh
     uint32_t kaddr[8];
     {
@@ -351,36 +360,22 @@ __global__ __launch_bounds__(kThreads, 1) void flash_fwd_bf16_kernel(FlashArgs a
                 __builtin_amdgcn_raw_ptr_buffer_load_lds(r, (lds_void*)&stg[grp][kv][(4 * i + wq) * 1024], 16, voff[i],
                                                          0, 0, 0);
         };
-        // the first tile streams in while the query row loads
+        // The first tile streams into stage0 and the item's 128 query rows into stage1 (free until step 0),
+        // both as whole 256-byte rows; rows past T arrive as zeros.
         if (grp < n_tiles) {
             dma(stage0, 0, grp);
             dma(stage0, 1, grp);
         }
-
-        // Q fragment, pre-multiplied by scale * log2 e: qf[cc] = Q[qrow][16*cc + 8*hh .. +8] * c. All eight
-        // loads are in flight together (and with the first tile's DMA) before the first is converted.
-        bf16x8 qf[8];
+        uint8_t* Qs = &stage1[0][0][0];  // 128 rows x 256 bytes (group 0's K and V areas of stage1)
         {
-            uint4 raw[8];
-            if (qrow < T) {
-                const uint16_t* qp = Qg + (int64_t)qrow * a.ldq + 8 * hh;
+            const __amdgpu_buffer_rsrc_t rq = make_rsrc(Qg + (int64_t)q0 * a.ldq, (uint32_t)(T - q0) * (uint32_t)a.ldq * 2u);
 #pragma unroll
-                for (int cc = 0; cc < 8; ++cc) raw[cc] = *reinterpret_cast<const uint4*>(qp + 16 * cc);
-            } else {
-#pragma unroll
-                for (int cc = 0; cc < 8; ++cc) raw[cc] = make_uint4(0, 0, 0, 0);
-            }
-            __builtin_amdgcn_sched_barrier(0);
-#pragma unroll
-            for (int cc = 0; cc < 8; ++cc) {
-                const uint32_t w[4] = {raw[cc].x, raw[cc].y, raw[cc].z, raw[cc].w};
-                uint32_t sw[4];
-#pragma unroll
-                for (int e = 0; e < 4; ++e) sw[e] = pack_bf16x2(bf16_lo(w[e]) * c, bf16_hi(w[e]) * c);
-                qf[cc] = __builtin_bit_cast(bf16x8, make_uint4(sw[0], sw[1], sw[2], sw[3]));
-            }
+            for (int i = 0; i < 4; ++i)
+                __builtin_amdgcn_raw_ptr_buffer_load_lds(rq, (lds_void*)(Qs + i * 8192 + wave * 1024), 16, qoff[i], 0, 0,
+                                                         0);
         }
 
+        bf16x8 qf[8];  // filled from the Q tile once it has landed
         Acc A;
 #pragma unroll
         for (int db = 0; db < 4; ++db)
@@ -410,7 +405,19 @@ __global__ __launch_bounds__(kThreads, 1) void flash_fwd_bf16_kernel(FlashArgs a
             tile_step(A, qf, cur[grp][0], cur[grp][1], kaddr, vaddr, k0, need_mask, lim, hh, mid);
         };
 
-        stage_barrier();  // the first tile has landed
+        stage_barrier();  // the first tile and the query rows have landed
+        // Q fragment, pre-multiplied by scale * log2 e: qf[cc] = Q[qrow][16*cc + 8*hh .. +8] * c
+        // (row 32*wq + ln of the Q tile, read like a K fragment)
+#pragma unroll
+        for (int cc = 0; cc < 8; ++cc) {
+            const uint4 raw = *reinterpret_cast<const uint4*>(Qs + wq * 8192 + kaddr[cc]);
+            const uint32_t w[4] = {raw.x, raw.y, raw.z, raw.w};
+            uint32_t sw[4];
+#pragma unroll
+            for (int e = 0; e < 4; ++e) sw[e] = pack_bf16x2(bf16_lo(w[e]) * c, bf16_hi(w[e]) * c);
+            qf[cc] = __builtin_bit_cast(bf16x8, make_uint4(sw[0], sw[1], sw[2], sw[3]));
+        }
+        lds_barrier();  // every wave holds its Q fragment before step 0's DMA refills stage1
         for (int it = 0; it < n_iter; it += 2) {
             // even step: compute from stage0 while the group's next tile streams into stage1
             step(stage0, stage1, 2 * it + grp, 2 * (it + 1) + grp);
@@ -502,8 +509,8 @@ int launch_flash_fwd_bf16(const FlashArgs& a, const SeqLens* lens, hipStream_t s
     if (a.ragged) sl = *lens;
     else sl.len[0] = a.T;
     if (a.ldk != a.ldv) return set_error(DT_ERR_UNSUPPORTED, "bf16 kernel needs equal K and V row strides");
-    if ((int64_t)a.T * a.ldk * 2 >= ((int64_t)1 << 31))
-        return set_error(DT_ERR_UNSUPPORTED, "K/V extent of one sequence exceeds 2 GiB");
+    if ((int64_t)a.T * a.ldk * 2 >= ((int64_t)1 << 31) || (int64_t)a.T * a.ldq * 2 >= ((int64_t)1 << 31))
+        return set_error(DT_ERR_UNSUPPORTED, "Q/K/V extent of one sequence exceeds 2 GiB");
     int grid = 0;
     DT_TRY(persistent_grid((int64_t)((a.T + kBM - 1) / kBM) * a.B * a.H, &grid));
     RaggedOrder ro;
