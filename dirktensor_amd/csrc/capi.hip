@@ -761,11 +761,14 @@ int dt_attn_layer_step(dt_attn_layer* L, float lr, void* stream) {
     hipStream_t s = static_cast<hipStream_t>(stream);
     DT_TRY(attn_layer_ensure_grads(L, s));
     const int64_t dm = L->d_model;
-    DT_TRY(launch_sgd(L->w_qkv, L->g_qkv, lr, 3 * dm * dm, s));  // OlmoAttention.cpp:315-317
-    DT_TRY(launch_sgd(L->w_o, L->g_o, lr, dm * dm, s));          // :318
-    DT_TRY(launch_sgd(L->q_norm, L->g_qn, lr, dm, s));           // :319, RMSNorm.cpp:38-40
-    DT_TRY(launch_sgd(L->k_norm, L->g_kn, lr, dm, s));           // :320
-    L->w16_stale = true;
+    // the bf16 copies (once the bf16 mode has made them) are rewritten from the updated weights in the
+    // same pass, so they are current afterwards
+    const bool copies = L->w_qkv16 && L->w_o16;
+    DT_TRY(launch_sgd(L->w_qkv, L->g_qkv, lr, 3 * dm * dm, s, copies ? L->w_qkv16 : nullptr));  // OlmoAttention.cpp:315-317
+    DT_TRY(launch_sgd(L->w_o, L->g_o, lr, dm * dm, s, copies ? L->w_o16 : nullptr));            // :318
+    DT_TRY(launch_sgd(L->q_norm, L->g_qn, lr, dm, s));  // :319, RMSNorm.cpp:38-40
+    DT_TRY(launch_sgd(L->k_norm, L->g_kn, lr, dm, s));  // :320
+    L->w16_stale = !copies;
     return DT_OK;
 }
 

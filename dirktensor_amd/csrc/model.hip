@@ -553,18 +553,22 @@ int dt_model_step(dt_model* M, float lr, void* stream) {
     hipStream_t s = static_cast<hipStream_t>(stream);
     DT_TRY(ensure_model_grads(M, s));
     const int64_t dm = M->dm, hid = M->hid, V = M->V;
+    // the bf16 copies (once the bf16 mode has made them all) are rewritten from the updated weights in the
+    // same pass, so they are current afterwards
+    bool copies = M->lm_head16 != nullptr;
+    for (const ModelLayer& Ly : M->L) copies = copies && Ly.w_gu16 && Ly.w_down16;
     // OlmoModel.cpp:69-75
     DT_TRY(launch_sgd(M->embed, M->g_embed, lr, V * dm, s));
     for (ModelLayer& Ly : M->L) {
         DT_TRY(dt_attn_layer_step(Ly.attn, lr, stream));  // OlmoBlock.cpp:32-37
         DT_TRY(launch_sgd(Ly.w_pa, Ly.g_pa, lr, dm, s));
-        DT_TRY(launch_sgd(Ly.w_gu, Ly.g_gu, lr, 2 * hid * dm, s));
-        DT_TRY(launch_sgd(Ly.w_down, Ly.g_down, lr, dm * hid, s));
+        DT_TRY(launch_sgd(Ly.w_gu, Ly.g_gu, lr, 2 * hid * dm, s, copies ? Ly.w_gu16 : nullptr));
+        DT_TRY(launch_sgd(Ly.w_down, Ly.g_down, lr, dm * hid, s, copies ? Ly.w_down16 : nullptr));
         DT_TRY(launch_sgd(Ly.w_pf, Ly.g_pf, lr, dm, s));
     }
     DT_TRY(launch_sgd(M->final_norm, M->g_final, lr, dm, s));
-    DT_TRY(launch_sgd(M->lm_head, M->g_lm, lr, V * dm, s));
-    M->w16_stale = true;
+    DT_TRY(launch_sgd(M->lm_head, M->g_lm, lr, V * dm, s, copies ? M->lm_head16 : nullptr));
+    M->w16_stale = !copies;
     return DT_OK;
 }
 

@@ -123,3 +123,24 @@ def test_train_step_like_main_cpp(gpu, params):
     print(f"loss {loss1:.6f} -> {loss2:.6f} (oracle {ref_loss1:.6f} -> {ref_loss2:.6f})")
     assert abs(loss2 - ref_loss2) <= 1e-4 * abs(ref_loss2)
     assert loss2 < loss1
+
+
+def test_bf16_forward_after_step(gpu, params):
+    """After step(), the bf16 mode's weight copies (refreshed by the SGD pass itself) match the updated fp32
+    weights: a bf16 forward of the stepped model against the oracle on the updated parameters."""
+    B, T, lr = 1, 48, 1e-2
+    tok = synth.model_tokens(B, T, VOCAB, seed=6601)
+    model = OlmoModel.from_params(params)
+    model.forward(tok, mode="bf16")  # makes the bf16 copies
+    G = synth.normal(6602, (B, T, VOCAB), 0.0, 1e-2)
+    model.backward(torch.from_numpy(G).to(gpu))
+    model.step(lr)
+    updated = {k: model.param(k) for k in params}
+    assert any(not np.array_equal(updated[k], params[k]) for k in params)
+    ref = oracle.model_forward(tok, updated)
+    # the step moves the logits far more than the tolerance, so stale copies could not pass
+    assert rel_err(ref, oracle.model_forward(tok, params)) > 10 * TOL_BF16
+    got = model.forward(tok, mode="bf16", save_for_backward=False)
+    err = rel_err(got, ref)
+    print(f"bf16 forward after step: rel err {err:.3e}")
+    assert err <= TOL_BF16
