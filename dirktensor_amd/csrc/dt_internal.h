@@ -125,6 +125,8 @@ struct NormRopeBwdArgs {
 int norm_rope_bwd_blocks(int rows);
 int launch_qk_norm_rope_bwd(const NormRopeBwdArgs& a, int bf16, float* grad_q_w, float* grad_k_w, hipStream_t stream);
 // w -= lr * g; w16 (nullable): the bf16 copy of w, refreshed in the same pass
+// out[c] += sum_b partial[b][c] (b = 0 .. nblk-1), deterministic order
+int launch_colsum(const float* partial, int nblk, int ncols, float* out, hipStream_t s);
 int launch_sgd(float* w, const float* g, float lr, int64_t n, hipStream_t stream, uint16_t* w16 = nullptr);
 int launch_fill_zero(float* p, int64_t n, hipStream_t stream);
 int launch_f32_to_bf16(const float* in, uint16_t* out, int64_t n, hipStream_t stream);

@@ -206,7 +206,7 @@ __global__ __launch_bounds__(256) void ce_reduce_kernel(const float* term, int64
 // RMSNorm::backward for kRowsPerBlock rows per workgroup: c = mean(dy * y), n = y / w,
 // dx = (w * dy - n * c) / rms; this workgroup's column sums of dy * n go to partial[blockIdx.x][dm].
 // dx_add (nullable) is added to dx (the residual branch of the block's backward, OlmoBlock.cpp:28,32).
-constexpr int kRowsPerBlock = 16;
+constexpr int kRowsPerBlock = 4;  // 512 workgroups for 2048 rows
 __global__ __launch_bounds__(256) void rmsnorm_bwd_rows_kernel(const float* dy, const float* y, const float* rms,
                                                                const float* w, const float* dx_add, float* dx,
                                                                float* partial, int64_t rows, int dm) {
@@ -249,12 +249,21 @@ __global__ __launch_bounds__(256) void rmsnorm_bwd_rows_kernel(const float* dy, 
 }
 
 // grad[j] += sum over blocks of partial[b][j], in block order
-__global__ __launch_bounds__(256) void col_reduce_kernel(const float* partial, int nblk, int dm, float* grad) {
-    const int j = blockIdx.x * 256 + threadIdx.x;
-    if (j >= dm) return;
+// out[c] += sum over b of partial[b][c], in a fixed order: a workgroup takes 64 columns; thread group g (of
+// 4) sums rows g, g+4, g+8, ... in increasing order, then the four sums are added g = 0..3. Deterministic,
+// and 4 x 64 lanes keep many rows in flight instead of one serial chain per column.
+__global__ __launch_bounds__(256) void colsum_kernel(const float* partial, int nblk, int ncols, float* out) {
+    __shared__ float part[4][64];
+    const int cl = threadIdx.x & 63, g = threadIdx.x >> 6;
+    const int c = blockIdx.x * 64 + cl;
     float s = 0.0f;
-    for (int b = 0; b < nblk; ++b) s += partial[(int64_t)b * dm + j];
-    grad[j] += s;
+    if (c < ncols) {
+#pragma unroll 8
+        for (int b = g; b < nblk; b += 4) s += partial[(int64_t)b * ncols + c];
+    }
+    part[g][cl] = s;
+    __syncthreads();
+    if (g == 0 && c < ncols) out[c] += ((part[0][cl] + part[1][cl]) + part[2][cl]) + part[3][cl];
 }
 
 // from d_act and the saved [gate | up] rows: d_gu = [d_gate | d_up] (gu and d_gu fp32, or both bf16)
@@ -363,7 +372,11 @@ int launch_rmsnorm_bwd(const float* dy, const float* y, const float* rms, const 
     hipLaunchKernelGGL(rmsnorm_bwd_rows_kernel, dim3(nblk), dim3(256), 0, s, dy, y, rms, w, dx_add, dx, partial,
                        (int64_t)rows, dm);
     DT_HIP_TRY(hipGetLastError());
-    hipLaunchKernelGGL(col_reduce_kernel, dim3((dm + 255) / 256), dim3(256), 0, s, partial, nblk, dm, grad_w);
+    return launch_colsum(partial, nblk, dm, grad_w, s);
+}
+
+int launch_colsum(const float* partial, int nblk, int ncols, float* out, hipStream_t s) {
+    hipLaunchKernelGGL(colsum_kernel, dim3((ncols + 63) / 64), dim3(256), 0, s, partial, nblk, ncols, out);
     DT_HIP_TRY(hipGetLastError());
     return DT_OK;
 }

@@ -14,7 +14,7 @@
 // [rows][3*d_model] dq|dk|dv buffer and dx is written back in place.
 //
 // dw is reduced deterministically: a workgroup handles kRows rows and writes
-// one partial row of column sums; norm_grad_reduce adds the partials, in
+// one partial row of column sums; launch_colsum adds the partials, in a fixed
 // order, into the gradient (the reference's `+=`, RMSNorm.cpp:31).
 //
 // One workgroup of 256 threads per kRows rows of q (blockIdx.y == 0) or k (== 1);
@@ -155,17 +155,6 @@ __global__ __launch_bounds__(256) void qk_norm_rope_bwd_kernel(NormRopeBwdArgs a
 }
 
 // grad_q[j] += sum_b partial[0][b][j], grad_k[j] += sum_b partial[1][b][j], in block order
-__global__ __launch_bounds__(256) void norm_grad_reduce_kernel(const float* partial, int nblk, int C, float* gq,
-                                                               float* gk) {
-    const int j = blockIdx.x * 256 + threadIdx.x;
-    if (j >= 2 * C) return;
-    const int which = j / C, col = j - which * C;
-    const float* p = partial + (int64_t)which * nblk * C + col;
-    float s = 0.0f;
-    for (int b = 0; b < nblk; ++b) s += p[(int64_t)b * C];
-    float* dst = which ? gk : gq;
-    dst[col] += s;
-}
 
 // w -= lr * g (OlmoAttention.cpp:314-321, RMSNorm.cpp:38-40), rounded as written: the product, then the
 // difference (no fused multiply-add), so the update is reproducible on the host
@@ -214,11 +203,9 @@ int launch_qk_norm_rope_bwd(const NormRopeBwdArgs& a, int bf16, float* grad_q_w,
     if (bf16) hipLaunchKernelGGL(qk_norm_rope_bwd_kernel<true>, grid, dim3(256), 0, stream, a);
     else hipLaunchKernelGGL(qk_norm_rope_bwd_kernel<false>, grid, dim3(256), 0, stream, a);
     DT_HIP_TRY(hipGetLastError());
-    const int C = a.H * 128;
-    hipLaunchKernelGGL(norm_grad_reduce_kernel, dim3((2 * C + 255) / 256), dim3(256), 0, stream, a.partial, nblk, C,
-                       grad_q_w, grad_k_w);
-    DT_HIP_TRY(hipGetLastError());
-    return DT_OK;
+    const int C = a.H * 128;  // partial: [q, k][nblk][C]
+    DT_TRY(launch_colsum(a.partial, nblk, C, grad_q_w, stream));
+    return launch_colsum(a.partial + (int64_t)nblk * C, nblk, C, grad_k_w, stream);
 }
 
 int launch_sgd(float* w, const float* g, float lr, int64_t n, hipStream_t stream, uint16_t* w16) {
