@@ -293,6 +293,41 @@ __global__ __launch_bounds__(256) void swiglu_bwd_kernel(const float* d_act, con
     }
 }
 
+// bf16 [gate | up] and fp32 d_act -> bf16 d_gu, eight elements per thread and step (16-byte accesses,
+// hid % 8 == 0); the same arithmetic as swiglu_bwd_kernel<true>
+__global__ __launch_bounds__(256) void swiglu_bwd_bf16x8_kernel(const float* d_act, const uint16_t* gu, uint16_t* d_gu,
+                                                                int64_t rows, int hid) {
+    const int64_t n8 = rows * (hid / 8);
+    for (int64_t q = (int64_t)blockIdx.x * 256 + threadIdx.x; q < n8; q += (int64_t)gridDim.x * 256) {
+        const int64_t r = q / (hid / 8);
+        const int i = (int)(q - r * (hid / 8)) * 8;
+        const float4 a0 = *reinterpret_cast<const float4*>(d_act + r * hid + i);
+        const float4 a1 = *reinterpret_cast<const float4*>(d_act + r * hid + i + 4);
+        const uint4 g = *reinterpret_cast<const uint4*>(gu + r * 2 * hid + i);
+        const uint4 u = *reinterpret_cast<const uint4*>(gu + r * 2 * hid + hid + i);
+        const float da[8] = {a0.x, a0.y, a0.z, a0.w, a1.x, a1.y, a1.z, a1.w};
+        const uint32_t gw[4] = {g.x, g.y, g.z, g.w}, uw[4] = {u.x, u.y, u.z, u.w};
+        uint32_t dg[4], du[4];
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+            float d_gate[2], d_up[2];
+#pragma unroll
+            for (int h = 0; h < 2; ++h) {
+                const float gate = __builtin_bit_cast(float, h ? (gw[e] & 0xffff0000u) : (gw[e] << 16));
+                const float up = __builtin_bit_cast(float, h ? (uw[e] & 0xffff0000u) : (uw[e] << 16));
+                const float sig = 1.0f / (1.0f + expf(-gate));
+                const float silu = gate * sig;
+                d_up[h] = da[2 * e + h] * silu;
+                d_gate[h] = da[2 * e + h] * up * sig * (1.0f + gate * (1.0f - sig));
+            }
+            dg[e] = pack_bf16x2(d_gate[0], d_gate[1]);
+            du[e] = pack_bf16x2(d_up[0], d_up[1]);
+        }
+        *reinterpret_cast<uint4*>(d_gu + r * 2 * hid + i) = make_uint4(dg[0], dg[1], dg[2], dg[3]);
+        *reinterpret_cast<uint4*>(d_gu + r * 2 * hid + hid + i) = make_uint4(du[0], du[1], du[2], du[3]);
+    }
+}
+
 // one workgroup per distinct token: E_grad[tok] += sum of dx rows pos[start[u]] .. pos[start[u+1]-1], in order
 __global__ __launch_bounds__(256) void embed_bwd_kernel(const float* dx, const int32_t* uniq, const int32_t* start,
                                                         const int32_t* pos, float* g_embed, int dm) {
@@ -383,7 +418,10 @@ int launch_colsum(const float* partial, int nblk, int ncols, float* out, hipStre
 
 int launch_swiglu_bwd(const float* d_act, const void* gu, void* d_gu, int rows, int hid, int bf16, hipStream_t s) {
     const unsigned g = grid_for((int64_t)rows * hid);
-    if (bf16) hipLaunchKernelGGL(swiglu_bwd_kernel<true>, dim3(g), dim3(256), 0, s, d_act, gu, d_gu, (int64_t)rows, hid);
+    if (bf16 && hid % 8 == 0)
+        hipLaunchKernelGGL(swiglu_bwd_bf16x8_kernel, dim3(grid_for((int64_t)rows * hid / 8)), dim3(256), 0, s, d_act,
+                           static_cast<const uint16_t*>(gu), static_cast<uint16_t*>(d_gu), (int64_t)rows, hid);
+    else if (bf16) hipLaunchKernelGGL(swiglu_bwd_kernel<true>, dim3(g), dim3(256), 0, s, d_act, gu, d_gu, (int64_t)rows, hid);
     else hipLaunchKernelGGL(swiglu_bwd_kernel<false>, dim3(g), dim3(256), 0, s, d_act, gu, d_gu, (int64_t)rows, hid);
     DT_HIP_TRY(hipGetLastError());
     return DT_OK;
