@@ -7,7 +7,12 @@
 // shape checks are compiled-out asserts, CMakeLists.txt:68, and T > 8192 is
 // undefined behaviour there, OlmoAttention.cpp:129).
 
+#include <hipblaslt/hipblaslt.h>
 #include <rocblas/rocblas.h>
+
+#include <algorithm>
+#include <array>
+#include <map>
 
 #include <cmath>
 #include <cstdarg>
@@ -118,6 +123,87 @@ static int ensure_blas(dt_ctx* ctx) {
     return DT_OK;
 }
 
+// bf16-input GEMMs go through hipBLASLt with its first heuristic choice (rocBLAS remains for fp32 inputs and
+// for a shape hipBLASLt has no algorithm for). For the long-K products of the backward (the MLP's and the
+// LM head's input gradients, d_h = d_gu W_gu with K = 16384 and d_y = d_logits W_lm with K = 100352, where
+// M = N = 2048 gives a plain tiling only 64 output tiles) its choice splits K across workgroups and sums the
+// parts in a workspace; it is bitwise repeatable run to run. Measured on the OLMo-2-1B shapes: forward
+// 6.56 -> 6.42 ms, training step 31.5 -> 30.8 ms. A plan (descriptors and the chosen algorithm) is made
+// once per shape and kept in the context.
+namespace {
+constexpr size_t kLtWorkspace = size_t(128) << 20;
+struct LtPlan {
+    hipblasLtMatmulDesc_t desc = nullptr;
+    hipblasLtMatrixLayout_t la = nullptr, lb = nullptr, lc = nullptr;
+    hipblasLtMatmulAlgo_t algo{};
+};
+struct LtCache {
+    hipblasLtHandle_t h = nullptr;
+    std::map<std::array<int, 9>, LtPlan> plans;
+};
+void lt_free(LtPlan& p) {
+    if (p.la) hipblasLtMatrixLayoutDestroy(p.la);
+    if (p.lb) hipblasLtMatrixLayoutDestroy(p.lb);
+    if (p.lc) hipblasLtMatrixLayoutDestroy(p.lc);
+    if (p.desc) hipblasLtMatmulDescDestroy(p.desc);
+}
+}  // namespace
+
+// Row-major C[M][N] = op(A) op(B) + beta C with bf16 A, B and fp32 C through hipBLASLt (the same column-major
+// mapping as gemm_rm below). Returns 1 (no error set) when hipBLASLt offers no algorithm for the shape.
+static int gemm_lt(dt_ctx* ctx, hipStream_t s, bool ta, bool tb, int M, int N, int K, const void* A, int lda,
+                   const void* B, int ldb, float beta, float* C, int ldc) {
+    LtCache* lc = static_cast<LtCache*>(ctx->lt);
+    if (!lc) {
+        lc = new LtCache;
+        if (hipblasLtCreate(&lc->h) != HIPBLAS_STATUS_SUCCESS) {
+            delete lc;
+            return set_error(DT_ERR_BLAS, "hipblasLtCreate failed");
+        }
+        ctx->lt = lc;
+    }
+    const std::array<int, 9> key{ta, tb, M, N, K, lda, ldb, ldc, beta == 0.0f};
+    auto it = lc->plans.find(key);
+    if (it == lc->plans.end()) {
+        LtPlan p;
+        const hipblasOperation_t opa = tb ? HIPBLAS_OP_T : HIPBLAS_OP_N;  // hipBLASLt's A is our B
+        const hipblasOperation_t opb = ta ? HIPBLAS_OP_T : HIPBLAS_OP_N;
+        bool ok = hipblasLtMatmulDescCreate(&p.desc, HIPBLAS_COMPUTE_32F, HIP_R_32F) == HIPBLAS_STATUS_SUCCESS &&
+                  hipblasLtMatmulDescSetAttribute(p.desc, HIPBLASLT_MATMUL_DESC_TRANSA, &opa, sizeof(opa)) ==
+                      HIPBLAS_STATUS_SUCCESS &&
+                  hipblasLtMatmulDescSetAttribute(p.desc, HIPBLASLT_MATMUL_DESC_TRANSB, &opb, sizeof(opb)) ==
+                      HIPBLAS_STATUS_SUCCESS &&
+                  hipblasLtMatrixLayoutCreate(&p.la, HIP_R_16BF, tb ? K : N, tb ? N : K, ldb) == HIPBLAS_STATUS_SUCCESS &&
+                  hipblasLtMatrixLayoutCreate(&p.lb, HIP_R_16BF, ta ? M : K, ta ? K : M, lda) == HIPBLAS_STATUS_SUCCESS &&
+                  hipblasLtMatrixLayoutCreate(&p.lc, HIP_R_32F, N, M, ldc) == HIPBLAS_STATUS_SUCCESS;
+        int n = 0;
+        hipblasLtMatmulHeuristicResult_t heur{};
+        if (ok) {
+            hipblasLtMatmulPreference_t pref = nullptr;
+            size_t wsz = kLtWorkspace;
+            ok = hipblasLtMatmulPreferenceCreate(&pref) == HIPBLAS_STATUS_SUCCESS &&
+                 hipblasLtMatmulPreferenceSetAttribute(pref, HIPBLASLT_MATMUL_PREF_MAX_WORKSPACE_BYTES, &wsz,
+                                                       sizeof(wsz)) == HIPBLAS_STATUS_SUCCESS &&
+                 hipblasLtMatmulAlgoGetHeuristic(lc->h, p.desc, p.la, p.lb, p.lc, p.lc, pref, 1, &heur, &n) ==
+                     HIPBLAS_STATUS_SUCCESS;
+            if (pref) hipblasLtMatmulPreferenceDestroy(pref);
+        }
+        if (!ok || n < 1) {
+            lt_free(p);
+            return 1;
+        }
+        p.algo = heur.algo;
+        it = lc->plans.emplace(key, p).first;
+    }
+    DT_TRY(ctx->lt_ws.ensure(kLtWorkspace));
+    const float one = 1.0f;
+    const LtPlan& p = it->second;
+    if (hipblasLtMatmul(lc->h, p.desc, &one, B, p.la, A, p.lb, &beta, C, p.lc, C, p.lc, &p.algo, ctx->lt_ws.ptr,
+                        kLtWorkspace, s) != HIPBLAS_STATUS_SUCCESS)
+        return set_error(DT_ERR_BLAS, "hipBLASLt GEMM (%d x %d x %d) failed", M, N, K);
+    return DT_OK;
+}
+
 // Row-major C[M][N] = op(A)[M][K] op(B)[K][N] + beta C, op = transpose when the flag is set (A is then
 // stored [K][M], B [N][K]). In rocBLAS's column-major terms a row-major X is X^T, so this is
 // C^T = op(B)^T op(A)^T: B goes first, each transposed exactly when it is transposed here.
@@ -129,6 +215,10 @@ int gemm_rm(dt_ctx* ctx, hipStream_t s, bool ta, bool tb, int M, int N, int K, c
     const float one = 1.0f;
     const rocblas_operation opb = tb ? rocblas_operation_transpose : rocblas_operation_none;
     const rocblas_operation opa = ta ? rocblas_operation_transpose : rocblas_operation_none;
+    if (bf16_in) {
+        const int rc = gemm_lt(ctx, s, ta, tb, M, N, K, A, lda, B, ldb, beta, C, ldc);
+        if (rc <= 0) return rc;  // done, or an error; 1: no hipBLASLt algorithm, rocBLAS below
+    }
     rocblas_status st;
     if (!bf16_in) {
         st = rocblas_sgemm(h, opb, opa, N, M, K, &one, static_cast<const float*>(B), ldb, static_cast<const float*>(A),
@@ -256,6 +346,13 @@ int dt_ctx_destroy(dt_ctx* ctx) {
     for (auto& b : ctx->stage) b.release();
     ctx->bwd_stats.release();
     if (ctx->blas) rocblas_destroy_handle(static_cast<rocblas_handle>(ctx->blas));
+    if (ctx->lt) {
+        LtCache* lc = static_cast<LtCache*>(ctx->lt);
+        for (auto& kv : lc->plans) lt_free(kv.second);
+        hipblasLtDestroy(lc->h);
+        delete lc;
+    }
+    ctx->lt_ws.release();
     delete ctx;
     return DT_OK;
 }

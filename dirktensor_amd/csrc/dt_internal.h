@@ -155,6 +155,8 @@ struct dt_ctx {
     dt::DeviceBuffer stage[10];  // host-memory path staging
     dt::DeviceBuffer bwd_stats;  // attention-core backward: delta and lse2, 2 x [B][H][T] fp32
     void* blas = nullptr;        // rocblas_handle, created on first use
+    void* lt = nullptr;          // hipBLASLt handle and per-shape plans (capi.hip), created on first use
+    dt::DeviceBuffer lt_ws;      // hipBLASLt workspace (split-K partial sums)
 };
 
 // OlmoAttention on the device (OlmoAttention.h:10-42): weights, forward state kept for backward, gradients.

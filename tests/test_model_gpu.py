@@ -144,3 +144,25 @@ def test_bf16_forward_after_step(gpu, params):
     err = rel_err(got, ref)
     print(f"bf16 forward after step: rel err {err:.3e}")
     assert err <= TOL_BF16
+
+
+def test_backward_long_k_products(gpu):
+    """bf16 backward of a model whose MLP input gradient (K = 2 * 4096) and LM-head input gradient (K = vocab
+    8192) take the split-K path (K >= 4 x max(M, N)): every gradient against the oracle, and bitwise equal over
+    two backward passes."""
+    vocab, hidden, B, T = 8192, 4096, 1, 16
+    p = synth.model_params(1, vocab, hidden, seed_base=6700)
+    tok = synth.model_tokens(B, T, vocab, seed=6701)
+    G = synth.normal(6702, (B, T, vocab), 0.0, 1e-3)
+    ref = oracle.model_backward(tok, p, G)
+    runs = []
+    for _ in range(2):
+        model = OlmoModel.from_params(p)
+        model.forward(tok, mode="bf16")
+        model.backward(torch.from_numpy(G).to(gpu))
+        runs.append({k: model.grad(k) for k in p})
+    errs = {k: rel_err(runs[0][k], ref[k]) for k in p}
+    worst = sorted(errs.items(), key=lambda kv: -kv[1])[:3]
+    print("long-K backward: worst " + ", ".join(f"{k} {v:.2e}" for k, v in worst))
+    assert max(errs.values()) <= TOL_BF16, worst
+    assert all(np.array_equal(runs[0][k], runs[1][k]) for k in p)
