@@ -139,7 +139,7 @@ struct LtPlan {
 };
 struct LtCache {
     hipblasLtHandle_t h = nullptr;
-    std::map<std::array<int, 9>, LtPlan> plans;
+    std::map<std::array<int, 10>, LtPlan> plans;
 };
 void lt_free(LtPlan& p) {
     if (p.la) hipblasLtMatrixLayoutDestroy(p.la);
@@ -149,10 +149,11 @@ void lt_free(LtPlan& p) {
 }
 }  // namespace
 
-// Row-major C[M][N] = op(A) op(B) + beta C with bf16 A, B and fp32 C through hipBLASLt (the same column-major
-// mapping as gemm_rm below). Returns 1 (no error set) when hipBLASLt offers no algorithm for the shape.
+// Row-major C[M][N] = op(A) op(B) + beta C with bf16 A, B and fp32 C (bf16 C when c_bf16) through hipBLASLt
+// (the same column-major mapping as gemm_rm below). Returns 1 (no error set) when hipBLASLt offers no
+// algorithm for the shape.
 static int gemm_lt(dt_ctx* ctx, hipStream_t s, bool ta, bool tb, int M, int N, int K, const void* A, int lda,
-                   const void* B, int ldb, float beta, float* C, int ldc) {
+                   const void* B, int ldb, float beta, void* C, int ldc, bool c_bf16 = false) {
     LtCache* lc = static_cast<LtCache*>(ctx->lt);
     if (!lc) {
         lc = new LtCache;
@@ -162,7 +163,7 @@ static int gemm_lt(dt_ctx* ctx, hipStream_t s, bool ta, bool tb, int M, int N, i
         }
         ctx->lt = lc;
     }
-    const std::array<int, 9> key{ta, tb, M, N, K, lda, ldb, ldc, beta == 0.0f};
+    const std::array<int, 10> key{ta, tb, M, N, K, lda, ldb, ldc, beta == 0.0f, c_bf16};
     auto it = lc->plans.find(key);
     if (it == lc->plans.end()) {
         LtPlan p;
@@ -175,7 +176,8 @@ static int gemm_lt(dt_ctx* ctx, hipStream_t s, bool ta, bool tb, int M, int N, i
                       HIPBLAS_STATUS_SUCCESS &&
                   hipblasLtMatrixLayoutCreate(&p.la, HIP_R_16BF, tb ? K : N, tb ? N : K, ldb) == HIPBLAS_STATUS_SUCCESS &&
                   hipblasLtMatrixLayoutCreate(&p.lb, HIP_R_16BF, ta ? M : K, ta ? K : M, lda) == HIPBLAS_STATUS_SUCCESS &&
-                  hipblasLtMatrixLayoutCreate(&p.lc, HIP_R_32F, N, M, ldc) == HIPBLAS_STATUS_SUCCESS;
+                  hipblasLtMatrixLayoutCreate(&p.lc, c_bf16 ? HIP_R_16BF : HIP_R_32F, N, M, ldc) ==
+                      HIPBLAS_STATUS_SUCCESS;
         int n = 0;
         hipblasLtMatmulHeuristicResult_t heur{};
         if (ok) {
@@ -200,7 +202,7 @@ static int gemm_lt(dt_ctx* ctx, hipStream_t s, bool ta, bool tb, int M, int N, i
     const LtPlan& p = it->second;
     if (hipblasLtMatmul(lc->h, p.desc, &one, B, p.la, A, p.lb, &beta, C, p.lc, C, p.lc, &p.algo, ctx->lt_ws.ptr,
                         kLtWorkspace, s) != HIPBLAS_STATUS_SUCCESS)
-        return set_error(DT_ERR_BLAS, "hipBLASLt GEMM (%d x %d x %d) failed", M, N, K);
+        return set_error(DT_ERR_BLAS, "hipBLASLt GEMM (%d x %d x %d%s) failed", M, N, K, c_bf16 ? ", bf16 out" : "");
     return DT_OK;
 }
 
@@ -235,6 +237,8 @@ int gemm_rm(dt_ctx* ctx, hipStream_t s, bool ta, bool tb, int M, int N, int K, c
 
 int gemm_rm_bf16(dt_ctx* ctx, hipStream_t s, bool ta, bool tb, int M, int N, int K, const void* A, int lda,
                  const void* B, int ldb, void* C, int ldc) {
+    const int rc = gemm_lt(ctx, s, ta, tb, M, N, K, A, lda, B, ldb, 0.0f, C, ldc, true);
+    if (rc <= 0) return rc;  // done, or an error; 1: no hipBLASLt algorithm, rocBLAS below
     DT_TRY(ensure_blas(ctx));
     rocblas_handle h = static_cast<rocblas_handle>(ctx->blas);
     rocblas_set_stream(h, s);
@@ -633,7 +637,7 @@ int dt_attn_layer_destroy(dt_attn_layer* L) {
     if (L->g_o) (void)hipFree(L->g_o);
     if (L->g_qn) (void)hipFree(L->g_qn);
     if (L->g_kn) (void)hipFree(L->g_kn);
-    for (dt::DeviceBuffer* b : {&L->qkv32, &L->qkv16, &L->attn, &L->x16, &L->x32, &L->att32, &L->rms, &L->stats,
+    for (dt::DeviceBuffer* b : {&L->qkv_pre, &L->qkv16, &L->attn, &L->x16, &L->x32, &L->att32, &L->rms, &L->stats,
                                 &L->d_attn32, &L->d16, &L->d_qkv, &L->partial})
         b->release();
     delete L;
@@ -687,11 +691,11 @@ int dt_attn_layer_fwd(dt_attn_layer* L, const float* x, float* out, int B, int T
     float* rms = save_for_backward ? static_cast<float*>(L->rms.ptr) : nullptr;
     float* st_m = save_for_backward ? static_cast<float*>(L->stats.ptr) : nullptr;
     float* st_l = save_for_backward ? st_m + (size_t)rows * H : nullptr;
-    DT_TRY(L->qkv32.ensure(act * 3 * 4));
-    float* qkv = static_cast<float*>(L->qkv32.ptr);
     const float scale = 1.0f / std::sqrt((float)DT_HEAD_DIM);  // OlmoAttention.cpp:91
 
     if (dtype == DT_FP32_EXACT) {
+        DT_TRY(L->qkv_pre.ensure(act * 3 * 4));
+        float* qkv = static_cast<float*>(L->qkv_pre.ptr);
         DT_TRY(L->attn.ensure(act * 4));
         float* attn = static_cast<float*>(L->attn.ptr);
         // Q|K|V = x [Wq;Wk;Wv]^T in one N = 3*d_model GEMM (OlmoAttention.cpp:68,74,80)
@@ -723,17 +727,21 @@ int dt_attn_layer_fwd(dt_attn_layer* L, const float* x, float* out, int B, int T
             L->w16_stale = false;
         }
         DT_TRY(L->x16.ensure(act * 2));
+        DT_TRY(L->qkv_pre.ensure(act * 3 * 2));
         DT_TRY(L->qkv16.ensure(act * 3 * 2));
         DT_TRY(L->attn.ensure(act * 2));
         uint16_t* x16 = static_cast<uint16_t*>(L->x16.ptr);
+        uint16_t* pre16 = static_cast<uint16_t*>(L->qkv_pre.ptr);
         uint16_t* qkv16 = static_cast<uint16_t*>(L->qkv16.ptr);
         uint16_t* attn16 = static_cast<uint16_t*>(L->attn.ptr);
         DT_TRY(launch_f32_to_bf16(xd, x16, (int64_t)act, s));
-        DT_TRY(gemm_xwt(ctx, s, rows, 3 * dm, dm, x16, dm, L->w_qkv16, dm, qkv, 3 * dm, true));
-        NormRopeArgs na{qkv, qkv + dm, qkv + 2 * dm, L->q_norm, L->k_norm, qkv16, qkv16 + dm, qkv16 + 2 * dm,
+        // the projections leave the GEMM as bf16 (fp32 accumulation, one rounding): the norm kernel reads half
+        // the bytes, and the norms' backward reads the same bf16 rows
+        DT_TRY(gemm_rm_bf16(ctx, s, false, true, rows, 3 * dm, dm, x16, dm, L->w_qkv16, dm, pre16, 3 * dm));
+        NormRopeArgs na{pre16, pre16 + dm, pre16 + 2 * dm, L->q_norm, L->k_norm, qkv16, qkv16 + dm, qkv16 + 2 * dm,
                         rms, rms ? rms + rows : nullptr, ctx->rope_cos, ctx->rope_sin, rows, T, H, 3 * dm, 3 * dm,
                         DT_RMS_EPS};
-        DT_TRY(launch_qk_norm_rope(na, 1, s));
+        DT_TRY(launch_qk_norm_rope(na, 1, s, 1));
         FlashArgs fa{qkv16, qkv16 + dm, qkv16 + 2 * dm, attn16, st_m, st_l, B, T, H, 3 * dm, 3 * dm, 3 * dm,
                      dm, scale, 1, seq_lens ? 1 : 0};
         DT_TRY(run_flash(ctx, fa, seq_lens, DT_BF16, s));
@@ -810,7 +818,7 @@ int dt_attn_layer_bwd(dt_attn_layer* L, const float* d_out, float* d_x, int B, i
     const float* st_m = static_cast<const float*>(L->stats.ptr);
     const float* st_l = st_m + (size_t)rows * H;
     const float* rms = static_cast<const float*>(L->rms.ptr);
-    const float* qkv = static_cast<const float*>(L->qkv32.ptr);
+    const char* pre = static_cast<const char*>(L->qkv_pre.ptr);  // pre-norm Q|K|V, in the mode's dtype
     const float scale = 1.0f / std::sqrt((float)DT_HEAD_DIM);
 
     // step 1 (OlmoAttention.cpp:198-217): dWo += d_out^T attn; d_attn = d_out Wo
@@ -835,7 +843,7 @@ int dt_attn_layer_bwd(dt_attn_layer* L, const float* d_out, float* d_x, int B, i
                     dq + 2 * dm * esz, bstats, bstats + (size_t)rows * H, B, T, H, 3 * dm, dm, 3 * dm, scale, 1};
     DT_TRY(bf ? launch_flash_bwd_bf16(ba, s) : launch_flash_bwd_f32(ba, s));
     // steps 3-4 (:234-244): RoPE backward and the q/k norms' backward, in place on dq | dk
-    NormRopeBwdArgs nb{dq, dq + dm * esz, qkv, qkv + dm, rms, rms + rows, L->q_norm, L->k_norm,
+    NormRopeBwdArgs nb{dq, dq + dm * esz, pre, pre + dm * esz, rms, rms + rows, L->q_norm, L->k_norm,
                        static_cast<float*>(L->partial.ptr), ctx->rope_cos, ctx->rope_sin, rows, T, H, 3 * dm, 3 * dm};
     DT_TRY(launch_qk_norm_rope_bwd(nb, bf, L->g_qn, L->g_kn, s));
     // step 5 (:246-309): [dWq;dWk;dWv] += [dq|dk|dv]^T x and d_x = [dq|dk|dv] [Wq;Wk;Wv]

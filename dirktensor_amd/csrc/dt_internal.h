@@ -87,9 +87,9 @@ int launch_flash_bwd_bf16(const FlashBwdArgs& a, hipStream_t stream);
 int launch_flash_bwd_f32(const FlashBwdArgs& a, hipStream_t stream);
 
 struct NormRopeArgs {
-    const float* q_in;
-    const float* k_in;
-    const float* v_in;  // nullable: when set, V rows are converted into v_out
+    const void* q_in;  // fp32, or bf16 when launched with in_bf16
+    const void* k_in;
+    const void* v_in;  // nullable: when set, V rows are converted into v_out
     const float* q_w;
     const float* k_w;
     void* q_out;
@@ -103,15 +103,15 @@ struct NormRopeArgs {
     int ld_in, ld_out;
     float eps;
 };
-int launch_qk_norm_rope(const NormRopeArgs& a, int out_bf16, hipStream_t stream);
+int launch_qk_norm_rope(const NormRopeArgs& a, int out_bf16, hipStream_t stream, int in_bf16 = 0);
 
 // Backward of the fused q/k RMSNorm + RoPE (OlmoAttention.cpp:234-244): dq/dk rows are rewritten in place
 // from d(rope output) to d(pre-norm projection); the norm-weight gradients are accumulated (+=).
 struct NormRopeBwdArgs {
     void* dq;  // [rows] rows of stride ld_d, fp32 or bf16 (in place)
     void* dk;
-    const float* q_x;  // saved pre-norm projections, stride ld_x
-    const float* k_x;
+    const void* q_x;  // saved pre-norm projections, stride ld_x, in the dtype of dq / dk
+    const void* k_x;
     const float* q_rms;  // saved rms, [rows]
     const float* k_rms;
     const float* q_w;
@@ -131,8 +131,8 @@ int launch_sgd(float* w, const float* g, float lr, int64_t n, hipStream_t stream
 int launch_fill_zero(float* p, int64_t n, hipStream_t stream);
 int launch_f32_to_bf16(const float* in, uint16_t* out, int64_t n, hipStream_t stream);
 
-// Row-major C[M][N] = op(A)[M][K] op(B)[K][N] + beta C on rocBLAS (fp32, or bf16 inputs with fp32
-// accumulation and output); op = transpose when ta / tb is set.
+// Row-major C[M][N] = op(A)[M][K] op(B)[K][N] + beta C: fp32 on rocBLAS, bf16 inputs with fp32 accumulation
+// and output on hipBLASLt (rocBLAS when it has no algorithm for the shape); op = transpose when ta / tb is set.
 int gemm_rm(dt_ctx* ctx, hipStream_t s, bool ta, bool tb, int M, int N, int K, const void* A, int lda,
             const void* B, int ldb, float beta, float* C, int ldc, bool bf16_in);
 // the same with bf16 inputs and a bf16 output C (beta = 0; fp32 accumulation, one rounding at the end)
@@ -169,7 +169,7 @@ struct dt_attn_layer {
     uint16_t* w_o16 = nullptr;
     float* q_norm = nullptr;
     float* k_norm = nullptr;
-    dt::DeviceBuffer qkv32, qkv16, attn, x16;
+    dt::DeviceBuffer qkv_pre, qkv16, attn, x16;  // qkv_pre: pre-norm Q|K|V, fp32 or bf16 by mode
     bool w16_stale = true;  // the bf16 copies lag the fp32 weights (before the first bf16 forward, after step)
     // forward state kept for backward (OlmoAttention.h:28-38) when save_for_backward is set
     dt::DeviceBuffer x32;   // the input rows (fp32)

@@ -6,10 +6,11 @@
 // (OlmoAttention.cpp:111-146, rotate-half pairs (d, d+64), position = t).
 //
 // One workgroup of 256 threads handles one row of q (blockIdx.y == 0), of k
-// (== 1) or, in the bf16 layer path, converts one row of v (== 2). Thread t
+// (== 1) or, when v_in is set, converts one row of v (== 2). Thread t
 // owns dims [4*(t%16), +4) and [4*(t%16)+64, +4) of head t/16, so both halves
 // of each rotate-half pair sit in the same thread. HBM-bound: per row it reads
-// d_model fp32 values and writes d_model outputs; the sin/cos tables are
+// d_model inputs (fp32, or in the bf16 layer path the bf16 output of the QKV
+// GEMM) and writes d_model outputs (fp32 or bf16); the sin/cos tables are
 // [rope_len][64] fp32 (the reference's [rope_len][128] tables repeat the same
 // angles in both halves, OlmoAttention.cpp:24, so one half is exact).
 //
@@ -29,6 +30,19 @@ __device__ __forceinline__ uint32_t pack_bf16x2(float lo, float hi) {
     return __builtin_bit_cast(uint32_t, r);
 }
 
+__device__ __forceinline__ float bf16_lo(uint32_t w) { return __builtin_bit_cast(float, w << 16); }
+__device__ __forceinline__ float bf16_hi(uint32_t w) { return __builtin_bit_cast(float, w & 0xffff0000u); }
+
+template <bool kBF16>
+__device__ __forceinline__ float4 load4(const void* base, int64_t idx) {
+    if constexpr (kBF16) {
+        const uint2 w = *reinterpret_cast<const uint2*>(static_cast<const uint16_t*>(base) + idx);
+        return make_float4(bf16_lo(w.x), bf16_hi(w.x), bf16_lo(w.y), bf16_hi(w.y));
+    } else {
+        return *reinterpret_cast<const float4*>(static_cast<const float*>(base) + idx);
+    }
+}
+
 template <bool kBF16>
 __device__ __forceinline__ void store4(void* base, int64_t idx, float4 v) {
     if constexpr (kBF16) {
@@ -41,7 +55,8 @@ __device__ __forceinline__ void store4(void* base, int64_t idx, float4 v) {
     }
 }
 
-template <bool kBF16>
+// kIn16: inputs are bf16; kBF16: outputs are bf16
+template <bool kIn16, bool kBF16>
 __global__ __launch_bounds__(256) void qk_norm_rope_kernel(NormRopeArgs a) {
     __shared__ float red[4];
     const int row = blockIdx.x;
@@ -52,13 +67,13 @@ __global__ __launch_bounds__(256) void qk_norm_rope_kernel(NormRopeArgs a) {
     const int C = a.H * 128;
 
     if (which == 2) {  // v: plain conversion of the row
-        const float* src = a.v_in + (int64_t)row * a.ld_in;
         for (int i = 4 * tid; i < C; i += 4 * 256)
-            store4<kBF16>(a.v_out, (int64_t)row * a.ld_out + i, *reinterpret_cast<const float4*>(&src[i]));
+            store4<kBF16>(a.v_out, (int64_t)row * a.ld_out + i, load4<kIn16>(a.v_in, (int64_t)row * a.ld_in + i));
         return;
     }
 
-    const float* src = (which == 0 ? a.q_in : a.k_in) + (int64_t)row * a.ld_in;
+    const void* src = which == 0 ? a.q_in : a.k_in;
+    const int64_t rb = (int64_t)row * a.ld_in;
     const float* w = which == 0 ? a.q_w : a.k_w;
     void* dst = which == 0 ? a.q_out : a.k_out;
     float* rms_out = which == 0 ? a.q_rms : a.k_rms;
@@ -67,15 +82,15 @@ __global__ __launch_bounds__(256) void qk_norm_rope_kernel(NormRopeArgs a) {
     const bool active = head < a.H;
     float4 x0 = make_float4(0.f, 0.f, 0.f, 0.f), x1 = x0;
     if (active) {
-        x0 = *reinterpret_cast<const float4*>(&src[head * 128 + d0]);
-        x1 = *reinterpret_cast<const float4*>(&src[head * 128 + d0 + 64]);
+        x0 = load4<kIn16>(src, rb + head * 128 + d0);
+        x1 = load4<kIn16>(src, rb + head * 128 + d0 + 64);
     }
     float ss = x0.x * x0.x + x0.y * x0.y + x0.z * x0.z + x0.w * x0.w + x1.x * x1.x + x1.y * x1.y + x1.z * x1.z +
                x1.w * x1.w;
     // handle rows wider than one workgroup pass (H > 16)
     for (int hx = head + 16; hx < a.H; hx += 16) {
-        const float4 y0 = *reinterpret_cast<const float4*>(&src[hx * 128 + d0]);
-        const float4 y1 = *reinterpret_cast<const float4*>(&src[hx * 128 + d0 + 64]);
+        const float4 y0 = load4<kIn16>(src, rb + hx * 128 + d0);
+        const float4 y1 = load4<kIn16>(src, rb + hx * 128 + d0 + 64);
         ss += y0.x * y0.x + y0.y * y0.y + y0.z * y0.z + y0.w * y0.w + y1.x * y1.x + y1.y * y1.y + y1.z * y1.z +
               y1.w * y1.w;
     }
@@ -94,8 +109,8 @@ __global__ __launch_bounds__(256) void qk_norm_rope_kernel(NormRopeArgs a) {
     for (int hx = head; hx < a.H; hx += 16) {
         float4 u0 = x0, u1 = x1;
         if (hx != head) {
-            u0 = *reinterpret_cast<const float4*>(&src[hx * 128 + d0]);
-            u1 = *reinterpret_cast<const float4*>(&src[hx * 128 + d0 + 64]);
+            u0 = load4<kIn16>(src, rb + hx * 128 + d0);
+            u1 = load4<kIn16>(src, rb + hx * 128 + d0 + 64);
         }
         const float4 w0 = *reinterpret_cast<const float4*>(&w[hx * 128 + d0]);
         const float4 w1 = *reinterpret_cast<const float4*>(&w[hx * 128 + d0 + 64]);
@@ -127,10 +142,12 @@ __global__ __launch_bounds__(256) void f32_to_bf16_kernel(const float* in, uint1
 
 }  // namespace
 
-int launch_qk_norm_rope(const NormRopeArgs& a, int out_bf16, hipStream_t stream) {
+int launch_qk_norm_rope(const NormRopeArgs& a, int out_bf16, hipStream_t stream, int in_bf16) {
     dim3 grid(a.rows, a.v_in ? 3 : 2);
-    if (out_bf16) hipLaunchKernelGGL(qk_norm_rope_kernel<true>, grid, dim3(256), 0, stream, a);
-    else hipLaunchKernelGGL(qk_norm_rope_kernel<false>, grid, dim3(256), 0, stream, a);
+    if (in_bf16 && !out_bf16) return set_error(DT_ERR_INVALID_ARG, "qk_norm_rope: bf16 input needs bf16 output");
+    if (in_bf16) hipLaunchKernelGGL((qk_norm_rope_kernel<true, true>), grid, dim3(256), 0, stream, a);
+    else if (out_bf16) hipLaunchKernelGGL((qk_norm_rope_kernel<false, true>), grid, dim3(256), 0, stream, a);
+    else hipLaunchKernelGGL((qk_norm_rope_kernel<false, false>), grid, dim3(256), 0, stream, a);
     DT_HIP_TRY(hipGetLastError());
     return DT_OK;
 }

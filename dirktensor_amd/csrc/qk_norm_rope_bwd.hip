@@ -11,7 +11,9 @@
 // reference recomputes n as y / w from the saved output y (RMSNorm.cpp:29);
 // x / rms is the same quantity without the division by w.
 // The gradient g arrives in the attention-core dtype (fp32 or bf16) inside the
-// [rows][3*d_model] dq|dk|dv buffer and dx is written back in place.
+// [rows][3*d_model] dq|dk|dv buffer and dx is written back in place; the saved
+// x is in the same dtype (the bf16 layer path keeps its pre-norm projections as
+// the bf16 output of the QKV GEMM).
 //
 // dw is reduced deterministically: a workgroup handles kRows rows and writes
 // one partial row of column sums; launch_colsum adds the partials, in a fixed
@@ -85,7 +87,7 @@ __global__ __launch_bounds__(256) void qk_norm_rope_bwd_kernel(NormRopeBwdArgs a
     const int nr = min(kRows, a.rows - r0);
 
     void* g = which == 0 ? a.dq : a.dk;
-    const float* x = which == 0 ? a.q_x : a.k_x;
+    const void* x = which == 0 ? a.q_x : a.k_x;
     const float* rms = which == 0 ? a.q_rms : a.k_rms;
     const float* w = which == 0 ? a.q_w : a.k_w;
 
@@ -102,8 +104,8 @@ __global__ __launch_bounds__(256) void qk_norm_rope_bwd_kernel(NormRopeBwdArgs a
             const int64_t xi = (int64_t)row * a.ld_x + hx * 128 + d0;
             float n0[4], n1[4];
             rope_back(load4<kBF16>(g, gi), load4<kBF16>(g, gi + 64), c4, s4, n0, n1);
-            const float4 x0 = *reinterpret_cast<const float4*>(x + xi);
-            const float4 x1 = *reinterpret_cast<const float4*>(x + xi + 64);
+            const float4 x0 = load4<kBF16>(x, xi);
+            const float4 x1 = load4<kBF16>(x, xi + 64);
             const float4 w0 = *reinterpret_cast<const float4*>(w + hx * 128 + d0);
             const float4 w1 = *reinterpret_cast<const float4*>(w + hx * 128 + d0 + 64);
             acc += n0[0] * (x0.x * inv) * w0.x + n0[1] * (x0.y * inv) * w0.y + n0[2] * (x0.z * inv) * w0.z +
@@ -134,8 +136,8 @@ __global__ __launch_bounds__(256) void qk_norm_rope_bwd_kernel(NormRopeBwdArgs a
             const int64_t xi = (int64_t)row * a.ld_x + hx * 128 + d0;
             float n0[4], n1[4];
             rope_back(load4<kBF16>(g, gi), load4<kBF16>(g, gi + 64), c4, s4, n0, n1);
-            const float4 x0 = *reinterpret_cast<const float4*>(x + xi);
-            const float4 x1 = *reinterpret_cast<const float4*>(x + xi + 64);
+            const float4 x0 = load4<kBF16>(x, xi);
+            const float4 x1 = load4<kBF16>(x, xi + 64);
             const float xv0[4] = {x0.x * inv, x0.y * inv, x0.z * inv, x0.w * inv};
             const float xv1[4] = {x1.x * inv, x1.y * inv, x1.z * inv, x1.w * inv};
             float o0[4], o1[4];
