@@ -761,6 +761,17 @@ int dt_attn_layer_fwd(dt_attn_layer* L, const float* x, float* out, int B, int T
 
 }  // extern "C"
 
+int attn_layer_settle_grads(dt_attn_layer* L, hipStream_t s) {
+    if (!L->grad_zero_pending || !L->g_qkv) return DT_OK;
+    const int64_t dm = L->d_model;
+    DT_TRY(launch_fill_zero(L->g_qkv, 3 * dm * dm, s));
+    DT_TRY(launch_fill_zero(L->g_o, dm * dm, s));
+    DT_TRY(launch_fill_zero(L->g_qn, dm, s));
+    DT_TRY(launch_fill_zero(L->g_kn, dm, s));
+    L->grad_zero_pending = false;
+    return DT_OK;
+}
+
 int attn_layer_ensure_grads(dt_attn_layer* L, hipStream_t s) {
     if (L->g_qkv) return DT_OK;
     const size_t dm = L->d_model;
@@ -777,7 +788,9 @@ int attn_layer_ensure_grads(dt_attn_layer* L, hipStream_t s) {
 
 extern "C" {
 
-int dt_attn_layer_bwd(dt_attn_layer* L, const float* d_out, float* d_x, int B, int T, int mem, void* stream) {
+// `writing` is set once the first gradient buffer is about to be written
+static int attn_layer_bwd(dt_attn_layer* L, const float* d_out, float* d_x, int B, int T, int mem, void* stream,
+                          bool& writing) {
     clear_error();
     if (!d_out || !d_x) return set_error(DT_ERR_INVALID_ARG, "d_out and d_x must be non-NULL");
     if (mem != DT_MEM_DEVICE && mem != DT_MEM_HOST) return set_error(DT_ERR_INVALID_ARG, "unknown mem %d", mem);
@@ -797,6 +810,9 @@ int dt_attn_layer_bwd(dt_attn_layer* L, const float* d_out, float* d_x, int B, i
     const size_t act = (size_t)rows * dm;
     const size_t esz = bf ? 2 : 4;
     DT_TRY(attn_layer_ensure_grads(L, s));
+    // after zero_grad the gradients are written, not added to (beta = 0: the buffers still hold old values)
+    const bool fresh = L->grad_zero_pending;
+    const float gb = fresh ? 0.0f : 1.0f;
 
     const float* gd = d_out;
     float* dxd = d_x;
@@ -829,7 +845,8 @@ int dt_attn_layer_bwd(dt_attn_layer* L, const float* d_out, float* d_x, int B, i
         g_in = L->d16.ptr;
         wo = L->w_o16;
     }
-    DT_TRY(gemm_rm(ctx, s, true, false, dm, dm, rows, g_in, dm, attn, dm, 1.0f, L->g_o, dm, bf));
+    writing = true;
+    DT_TRY(gemm_rm(ctx, s, true, false, dm, dm, rows, g_in, dm, attn, dm, gb, L->g_o, dm, bf));
     DT_TRY(gemm_rm(ctx, s, false, false, rows, dm, dm, g_in, dm, wo, dm, 0.0f, d_attn, dm, bf));
     // step 2 (:219-232): the attention core's backward from the saved m and l
     const void* d_o = d_attn;
@@ -845,17 +862,27 @@ int dt_attn_layer_bwd(dt_attn_layer* L, const float* d_out, float* d_x, int B, i
     // steps 3-4 (:234-244): RoPE backward and the q/k norms' backward, in place on dq | dk
     NormRopeBwdArgs nb{dq, dq + dm * esz, pre, pre + dm * esz, rms, rms + rows, L->q_norm, L->k_norm,
                        static_cast<float*>(L->partial.ptr), ctx->rope_cos, ctx->rope_sin, rows, T, H, 3 * dm, 3 * dm};
-    DT_TRY(launch_qk_norm_rope_bwd(nb, bf, L->g_qn, L->g_kn, s));
+    DT_TRY(launch_qk_norm_rope_bwd(nb, bf, L->g_qn, L->g_kn, s, !fresh));
     // step 5 (:246-309): [dWq;dWk;dWv] += [dq|dk|dv]^T x and d_x = [dq|dk|dv] [Wq;Wk;Wv]
     const void* xin = bf ? L->x16.ptr : L->x32.ptr;
     const void* wqkv = bf ? static_cast<const void*>(L->w_qkv16) : static_cast<const void*>(L->w_qkv);
-    DT_TRY(gemm_rm(ctx, s, true, false, 3 * dm, dm, rows, dqkv, 3 * dm, xin, dm, 1.0f, L->g_qkv, dm, bf));
+    DT_TRY(gemm_rm(ctx, s, true, false, 3 * dm, dm, rows, dqkv, 3 * dm, xin, dm, gb, L->g_qkv, dm, bf));
+    L->grad_zero_pending = false;  // every gradient buffer has been written
     DT_TRY(gemm_rm(ctx, s, false, false, rows, dm, 3 * dm, dqkv, 3 * dm, wqkv, dm, 0.0f, dxd, dm, bf));
     if (mem == DT_MEM_HOST) {
         DT_HIP_TRY(hipMemcpyAsync(d_x, dxd, act * 4, hipMemcpyDeviceToHost, s));
         DT_HIP_TRY(hipStreamSynchronize(s));
     }
     return DT_OK;
+}
+
+int dt_attn_layer_bwd(dt_attn_layer* L, const float* d_out, float* d_x, int B, int T, int mem, void* stream) {
+    bool writing = false;
+    const int rc = attn_layer_bwd(L, d_out, d_x, B, T, mem, stream, writing);
+    // a backward that failed after zero_grad, once it had begun writing gradients, may have written some of them:
+    // clear them all, so that they read as the zero_grad left them (the error stays the one reported)
+    if (rc != DT_OK && writing && L->grad_zero_pending) (void)attn_layer_settle_grads(L, static_cast<hipStream_t>(stream));
+    return rc;
 }
 
 int dt_attn_layer_step(dt_attn_layer* L, float lr, void* stream) {
@@ -865,6 +892,7 @@ int dt_attn_layer_step(dt_attn_layer* L, float lr, void* stream) {
     DT_TRY(check_device_binding(L->ctx));
     hipStream_t s = static_cast<hipStream_t>(stream);
     DT_TRY(attn_layer_ensure_grads(L, s));
+    DT_TRY(attn_layer_settle_grads(L, s));
     const int64_t dm = L->d_model;
     // the bf16 copies (once the bf16 mode has made them) are rewritten from the updated weights in the
     // same pass, so they are current afterwards
@@ -883,11 +911,10 @@ int dt_attn_layer_zero_grad(dt_attn_layer* L, void* stream) {
     DT_TRY(check_device_binding(L->ctx));
     hipStream_t s = static_cast<hipStream_t>(stream);
     if (!L->g_qkv) return attn_layer_ensure_grads(L, s);  // allocated zeroed
-    const int64_t dm = L->d_model;
-    DT_TRY(launch_fill_zero(L->g_qkv, 3 * dm * dm, s));  // OlmoAttention.cpp:323-330
-    DT_TRY(launch_fill_zero(L->g_o, dm * dm, s));
-    DT_TRY(launch_fill_zero(L->g_qn, dm, s));
-    DT_TRY(launch_fill_zero(L->g_kn, dm, s));
+    // OlmoAttention.cpp:323-330, deferred: the next backward overwrites the gradients instead of adding to them,
+    // which saves writing zeros over every buffer and the GEMMs' reads of them; step and the parameter
+    // copies clear the buffers first when no backward came in between
+    L->grad_zero_pending = true;
     return DT_OK;
 }
 
@@ -899,7 +926,10 @@ static int copy_params(dt_attn_layer* L, int grads, float* wq, float* wk, float*
     if (mem != DT_MEM_DEVICE && mem != DT_MEM_HOST) return set_error(DT_ERR_INVALID_ARG, "unknown mem %d", mem);
     DT_TRY(check_device_binding(L->ctx));
     hipStream_t s = static_cast<hipStream_t>(stream);
-    if (grads) DT_TRY(attn_layer_ensure_grads(L, s));
+    if (grads) {
+        DT_TRY(attn_layer_ensure_grads(L, s));
+        DT_TRY(attn_layer_settle_grads(L, s));
+    }
     const size_t dm = L->d_model, w2 = dm * dm * 4;
     const float* src_qkv = grads ? L->g_qkv : L->w_qkv;
     const float* srcs[6] = {src_qkv, src_qkv + dm * dm, src_qkv + 2 * dm * dm, grads ? L->g_o : L->w_o,

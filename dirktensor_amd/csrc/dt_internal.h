@@ -123,10 +123,13 @@ struct NormRopeBwdArgs {
     int ld_d, ld_x;
 };
 int norm_rope_bwd_blocks(int rows);
-int launch_qk_norm_rope_bwd(const NormRopeBwdArgs& a, int bf16, float* grad_q_w, float* grad_k_w, hipStream_t stream);
+// accumulate = false: the norm-weight gradients are overwritten (their buffers are logically zero)
+int launch_qk_norm_rope_bwd(const NormRopeBwdArgs& a, int bf16, float* grad_q_w, float* grad_k_w, hipStream_t stream,
+                            bool accumulate = true);
+// out[c] += sum_b partial[b][c] (b = 0 .. nblk-1; out[c] = 0 + the sum when accumulate is false), deterministic
+// order
+int launch_colsum(const float* partial, int nblk, int ncols, float* out, hipStream_t s, bool accumulate = true);
 // w -= lr * g; w16 (nullable): the bf16 copy of w, refreshed in the same pass
-// out[c] += sum_b partial[b][c] (b = 0 .. nblk-1), deterministic order
-int launch_colsum(const float* partial, int nblk, int ncols, float* out, hipStream_t s);
 int launch_sgd(float* w, const float* g, float lr, int64_t n, hipStream_t stream, uint16_t* w16 = nullptr);
 int launch_fill_zero(float* p, int64_t n, hipStream_t stream);
 int launch_f32_to_bf16(const float* in, uint16_t* out, int64_t n, hipStream_t stream);
@@ -171,6 +174,9 @@ struct dt_attn_layer {
     float* k_norm = nullptr;
     dt::DeviceBuffer qkv_pre, qkv16, attn, x16;  // qkv_pre: pre-norm Q|K|V, fp32 or bf16 by mode
     bool w16_stale = true;  // the bf16 copies lag the fp32 weights (before the first bf16 forward, after step)
+    // zero_grad was called and the gradient buffers have not been cleared: they read as zero. The next backward
+    // writes them instead of adding to them; anything else that reads them clears them first.
+    bool grad_zero_pending = false;
     // forward state kept for backward (OlmoAttention.h:28-38) when save_for_backward is set
     dt::DeviceBuffer x32;   // the input rows (fp32)
     dt::DeviceBuffer att32; // fp32 mode: q_rope | k_rope | v, [rows][3*d_model]
@@ -188,6 +194,8 @@ struct dt_attn_layer {
 // zero-initialised attention layer (weights set afterwards), and its gradient buffers (allocated zeroed)
 int attn_layer_alloc(dt_ctx* ctx, int d_model, int n_heads, dt_attn_layer** out);
 int attn_layer_ensure_grads(dt_attn_layer* L, hipStream_t s);
+// clears the gradient buffers when a zero_grad is pending (they are then zero in memory as well)
+int attn_layer_settle_grads(dt_attn_layer* L, hipStream_t s);
 
 namespace dt {
 // model kernels (model_kernels.hip)
@@ -200,7 +208,8 @@ int launch_ce_loss(const float* logits, const int32_t* target, float* term, floa
                    int count, hipStream_t s);
 int rmsnorm_bwd_blocks(int rows);
 int launch_rmsnorm_bwd(const float* dy, const float* y, const float* rms, const float* w, const float* dx_add,
-                       float* dx, float* partial, float* grad_w, int rows, int dm, hipStream_t s);
+                       float* dx, float* partial, float* grad_w, int rows, int dm, hipStream_t s,
+                       bool accumulate = true);
 int launch_swiglu_bwd(const float* d_act, const void* gu, void* d_gu, int rows, int hid, int bf16, hipStream_t s);
 int launch_embed_bwd(const float* dx, const int32_t* uniq, const int32_t* start, const int32_t* pos, int n_uniq,
                      float* g_embed, int dm, hipStream_t s);

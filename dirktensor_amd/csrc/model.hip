@@ -57,6 +57,10 @@ struct dt_model {
     float* lm_head = nullptr;     // [V][dm]
     uint16_t* lm_head16 = nullptr;
     bool w16_stale = true;
+    // zero_grad was called and the model-level gradient buffers (all but the embedding's, which zero_grad clears
+    // at once, and the attention layers', which keep their own flag) have not been cleared: they read as zero,
+    // the next backward writes them instead of adding to them, and anything else that reads them clears them first
+    bool grad_zero_pending = false;
     std::vector<ModelLayer> L;
     DeviceBuffer tok, x, x2, yf, yf16, rmsf, logits;
     // saved forward
@@ -163,6 +167,23 @@ int ensure_model_grads(dt_model* M, hipStream_t s) {
         DT_TRY(alloc_f32(&Ly.g_down, dm * hid));
     }
     DT_HIP_TRY(hipDeviceSynchronize());  // the hipMemsets above are not stream-ordered with s
+    return DT_OK;
+}
+
+// clears the gradient buffers of the model and of its attention layers when a zero_grad is pending
+int model_settle_grads(dt_model* M, hipStream_t s) {
+    for (ModelLayer& Ly : M->L) DT_TRY(attn_layer_settle_grads(Ly.attn, s));
+    if (!M->grad_zero_pending || !M->g_embed) return DT_OK;
+    const int64_t dm = M->dm, hid = M->hid, V = M->V;
+    for (ModelLayer& Ly : M->L) {
+        DT_TRY(launch_fill_zero(Ly.g_pa, dm, s));
+        DT_TRY(launch_fill_zero(Ly.g_gu, 2 * hid * dm, s));
+        DT_TRY(launch_fill_zero(Ly.g_down, dm * hid, s));
+        DT_TRY(launch_fill_zero(Ly.g_pf, dm, s));
+    }
+    DT_TRY(launch_fill_zero(M->g_final, dm, s));
+    DT_TRY(launch_fill_zero(M->g_lm, V * dm, s));
+    M->grad_zero_pending = false;
     return DT_OK;
 }
 
@@ -290,7 +311,10 @@ int dt_model_get_param(dt_model* M, const char* name, float* out, int64_t count,
         return set_error(DT_ERR_INVALID_ARG, "parameter '%s' has %zu elements, got %lld", name, r.count, (long long)count);
     DT_TRY(check_device_binding(M->ctx));
     hipStream_t s = static_cast<hipStream_t>(stream);
-    if (grad) DT_TRY(ensure_model_grads(M, s));
+    if (grad) {
+        DT_TRY(ensure_model_grads(M, s));
+        DT_TRY(model_settle_grads(M, s));
+    }
     const float* src = grad ? *r.g + r.offset : r.w;
     DT_HIP_TRY(hipMemcpyAsync(out, src, r.count * sizeof(float),
                               mem == DT_MEM_HOST ? hipMemcpyDeviceToHost : hipMemcpyDeviceToDevice, s));
@@ -439,7 +463,8 @@ int dt_model_fwd(dt_model* M, const int32_t* tokens, int B, int T, float* logits
     return DT_OK;
 }
 
-int dt_model_bwd(dt_model* M, const float* d_logits, int mem, void* stream) {
+// `writing` is set once the first gradient buffer is about to be written
+static int model_bwd(dt_model* M, const float* d_logits, int mem, void* stream, bool& writing) {
     clear_error();
     if (!M || !d_logits) return set_error(DT_ERR_INVALID_ARG, "model and d_logits must be non-NULL");
     if (mem != DT_MEM_DEVICE && mem != DT_MEM_HOST) return set_error(DT_ERR_INVALID_ARG, "unknown mem %d", mem);
@@ -453,6 +478,9 @@ int dt_model_bwd(dt_model* M, const float* d_logits, int mem, void* stream) {
     const int rows = B * T;
     const size_t act = (size_t)rows * dm;
     DT_TRY(ensure_model_grads(M, s));
+    // after zero_grad the gradients are written, not added to (beta = 0: the buffers still hold old values)
+    const bool fresh = M->grad_zero_pending;
+    const float gb = fresh ? 0.0f : 1.0f;
 
     const float* gl = d_logits;
     if (mem == DT_MEM_HOST) {
@@ -480,45 +508,47 @@ int dt_model_bwd(dt_model* M, const float* d_logits, int mem, void* stream) {
 
     // LM head (OlmoLmHead.cpp:30-62): dW += d_logits^T y; d_y = d_logits W
     float* d_yf = da;
+    writing = true;
     if (bf) {
         DT_TRY(launch_f32_to_bf16(gl, d16, (int64_t)rows * V, s));
-        DT_TRY(gemm_rm(ctx, s, true, false, V, dm, rows, d16, V, M->yf16.ptr, dm, 1.0f, M->g_lm, dm, true));
+        DT_TRY(gemm_rm(ctx, s, true, false, V, dm, rows, d16, V, M->yf16.ptr, dm, gb, M->g_lm, dm, true));
         DT_TRY(gemm_rm(ctx, s, false, false, rows, dm, V, d16, V, M->lm_head16, dm, 0.0f, d_yf, dm, true));
     } else {
-        DT_TRY(gemm_rm(ctx, s, true, false, V, dm, rows, gl, V, M->yf.ptr, dm, 1.0f, M->g_lm, dm, false));
+        DT_TRY(gemm_rm(ctx, s, true, false, V, dm, rows, gl, V, M->yf.ptr, dm, gb, M->g_lm, dm, false));
         DT_TRY(gemm_rm(ctx, s, false, false, rows, dm, V, gl, V, M->lm_head, dm, 0.0f, d_yf, dm, false));
     }
     // final norm (OlmoModel.cpp:52): RMSNorm::backward from the saved output y and rms
     DT_TRY(launch_rmsnorm_bwd(d_yf, static_cast<const float*>(M->yf.ptr), static_cast<const float*>(M->rmsf.ptr),
-                              M->final_norm, nullptr, dx, partial, M->g_final, rows, dm, s));
+                              M->final_norm, nullptr, dx, partial, M->g_final, rows, dm, s, !fresh));
     // blocks in reverse (OlmoBlock.cpp:23-30)
     for (int li = M->n_layers - 1; li >= 0; --li) {
         ModelLayer& Ly = M->L[li];
         // d_m = N_pf.backward(d_x)
         DT_TRY(launch_rmsnorm_bwd(dx, static_cast<const float*>(Ly.y_pf.ptr), static_cast<const float*>(Ly.rms_pf.ptr),
-                                  Ly.w_pf, nullptr, dmo, partial, Ly.g_pf, rows, dm, s));
+                                  Ly.w_pf, nullptr, dmo, partial, Ly.g_pf, rows, dm, s, !fresh));
         // MLP backward: dWdown += d_m^T act; d_act = d_m Wdown; d_gu = swiglu'; dW_gu += d_gu^T h;
         // d_h = d_gu W_gu + d_x (the residual, OlmoBlock.cpp:28; GEMM with beta = 1 into a copy of d_x)
         DT_HIP_TRY(hipMemcpyAsync(dh, dx, act * 4, hipMemcpyDeviceToDevice, s));
         if (bf) {
             DT_TRY(launch_f32_to_bf16(dmo, d16, (int64_t)act, s));
-            DT_TRY(gemm_rm(ctx, s, true, false, dm, hid, rows, d16, dm, Ly.act.ptr, hid, 1.0f, Ly.g_down, hid, true));
+            DT_TRY(gemm_rm(ctx, s, true, false, dm, hid, rows, d16, dm, Ly.act.ptr, hid, gb, Ly.g_down, hid, true));
             DT_TRY(gemm_rm(ctx, s, false, false, rows, hid, dm, d16, dm, Ly.w_down16, hid, 0.0f, d_act, hid, true));
         } else {
-            DT_TRY(gemm_rm(ctx, s, true, false, dm, hid, rows, dmo, dm, Ly.act.ptr, hid, 1.0f, Ly.g_down, hid, false));
+            DT_TRY(gemm_rm(ctx, s, true, false, dm, hid, rows, dmo, dm, Ly.act.ptr, hid, gb, Ly.g_down, hid, false));
             DT_TRY(gemm_rm(ctx, s, false, false, rows, hid, dm, dmo, dm, Ly.w_down, hid, 0.0f, d_act, hid, false));
         }
         DT_TRY(launch_swiglu_bwd(d_act, Ly.gu.ptr, M->d_gu.ptr, rows, hid, bf, s));
         const void* hin = bf ? Ly.h16.ptr : Ly.h.ptr;
         const void* wgu = bf ? static_cast<const void*>(Ly.w_gu16) : static_cast<const void*>(Ly.w_gu);
-        DT_TRY(gemm_rm(ctx, s, true, false, 2 * hid, dm, rows, M->d_gu.ptr, 2 * hid, hin, dm, 1.0f, Ly.g_gu, dm, bf));
+        DT_TRY(gemm_rm(ctx, s, true, false, 2 * hid, dm, rows, M->d_gu.ptr, 2 * hid, hin, dm, gb, Ly.g_gu, dm, bf));
         DT_TRY(gemm_rm(ctx, s, false, false, rows, dm, 2 * hid, M->d_gu.ptr, 2 * hid, wgu, dm, 1.0f, dh, dm, bf));
         // d_a = N_pa.backward(d_h); d_x = attn.backward(d_a) + d_h (OlmoBlock.cpp:29-32)
         DT_TRY(launch_rmsnorm_bwd(dh, static_cast<const float*>(Ly.y_pa.ptr), static_cast<const float*>(Ly.rms_pa.ptr),
-                                  Ly.w_pa, nullptr, da, partial, Ly.g_pa, rows, dm, s));
+                                  Ly.w_pa, nullptr, da, partial, Ly.g_pa, rows, dm, s, !fresh));
         DT_TRY(dt_attn_layer_bwd(Ly.attn, da, dxa, B, T, DT_MEM_DEVICE, stream));
         DT_TRY(launch_add(dxa, dh, dx, (int64_t)act, s));
     }
+    M->grad_zero_pending = false;  // every model-level gradient buffer but the embedding's has been written
     // embedding (OlmoModel.cpp:57-66): per distinct token, its positions in order (CSR built here)
     std::vector<int32_t> order(rows);
     for (int i = 0; i < rows; ++i) order[i] = i;
@@ -545,6 +575,21 @@ int dt_model_bwd(dt_model* M, const float* d_logits, int mem, void* stream) {
     return DT_OK;
 }
 
+int dt_model_bwd(dt_model* M, const float* d_logits, int mem, void* stream) {
+    bool writing = false;
+    const bool was_pending = M && M->grad_zero_pending;
+    const int rc = model_bwd(M, d_logits, mem, stream, writing);
+    // a backward that failed after zero_grad, once it had begun writing gradients, may have written some of them:
+    // clear them all (the layers' too), so that they read as the zero_grad left them (the error stays the one
+    // reported)
+    if (rc != DT_OK && writing && was_pending) {
+        for (ModelLayer& Ly : M->L) Ly.attn->grad_zero_pending = true;
+        M->grad_zero_pending = true;
+        (void)model_settle_grads(M, static_cast<hipStream_t>(stream));
+    }
+    return rc;
+}
+
 int dt_model_step(dt_model* M, float lr, void* stream) {
     clear_error();
     if (!M) return set_error(DT_ERR_INVALID_ARG, "model is NULL");
@@ -552,6 +597,7 @@ int dt_model_step(dt_model* M, float lr, void* stream) {
     DT_TRY(check_device_binding(M->ctx));
     hipStream_t s = static_cast<hipStream_t>(stream);
     DT_TRY(ensure_model_grads(M, s));
+    DT_TRY(model_settle_grads(M, s));
     const int64_t dm = M->dm, hid = M->hid, V = M->V;
     // the bf16 copies (once the bf16 mode has made them all) are rewritten from the updated weights in the
     // same pass, so they are current afterwards
@@ -578,18 +624,12 @@ int dt_model_zero_grad(dt_model* M, void* stream) {
     DT_TRY(check_device_binding(M->ctx));
     hipStream_t s = static_cast<hipStream_t>(stream);
     if (!M->g_embed) return ensure_model_grads(M, s);
-    const int64_t dm = M->dm, hid = M->hid, V = M->V;
-    // OlmoModel.cpp:77-83
+    const int64_t dm = M->dm, V = M->V;
+    // OlmoModel.cpp:77-83. The embedding gradient is accumulated by a scatter over the batch's tokens, so it is
+    // cleared here; the others are cleared lazily (the next backward overwrites them, see grad_zero_pending)
     DT_TRY(launch_fill_zero(M->g_embed, V * dm, s));
-    for (ModelLayer& Ly : M->L) {
-        DT_TRY(dt_attn_layer_zero_grad(Ly.attn, stream));
-        DT_TRY(launch_fill_zero(Ly.g_pa, dm, s));
-        DT_TRY(launch_fill_zero(Ly.g_gu, 2 * hid * dm, s));
-        DT_TRY(launch_fill_zero(Ly.g_down, dm * hid, s));
-        DT_TRY(launch_fill_zero(Ly.g_pf, dm, s));
-    }
-    DT_TRY(launch_fill_zero(M->g_final, dm, s));
-    DT_TRY(launch_fill_zero(M->g_lm, V * dm, s));
+    for (ModelLayer& Ly : M->L) DT_TRY(dt_attn_layer_zero_grad(Ly.attn, stream));
+    M->grad_zero_pending = true;
     return DT_OK;
 }
 

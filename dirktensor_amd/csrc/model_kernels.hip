@@ -252,7 +252,7 @@ __global__ __launch_bounds__(256) void rmsnorm_bwd_rows_kernel(const float* dy, 
 // out[c] += sum over b of partial[b][c], in a fixed order: a workgroup takes 64 columns; thread group g (of
 // 4) sums rows g, g+4, g+8, ... in increasing order, then the four sums are added g = 0..3. Deterministic,
 // and 4 x 64 lanes keep many rows in flight instead of one serial chain per column.
-__global__ __launch_bounds__(256) void colsum_kernel(const float* partial, int nblk, int ncols, float* out) {
+__global__ __launch_bounds__(256) void colsum_kernel(const float* partial, int nblk, int ncols, float* out, int accumulate) {
     __shared__ float part[4][64];
     const int cl = threadIdx.x & 63, g = threadIdx.x >> 6;
     const int c = blockIdx.x * 64 + cl;
@@ -263,7 +263,8 @@ __global__ __launch_bounds__(256) void colsum_kernel(const float* partial, int n
     }
     part[g][cl] = s;
     __syncthreads();
-    if (g == 0 && c < ncols) out[c] += ((part[0][cl] + part[1][cl]) + part[2][cl]) + part[3][cl];
+    if (g == 0 && c < ncols)  // (0 + sum when not accumulating: the value a zeroed out[c] would get)
+        out[c] = (accumulate ? out[c] : 0.0f) + (((part[0][cl] + part[1][cl]) + part[2][cl]) + part[3][cl]);
 }
 
 // from d_act and the saved [gate | up] rows: d_gu = [d_gate | d_up] (gu and d_gu fp32, or both bf16)
@@ -402,16 +403,17 @@ int launch_ce_loss(const float* logits, const int32_t* target, float* term, floa
 int rmsnorm_bwd_blocks(int rows) { return (rows + kRowsPerBlock - 1) / kRowsPerBlock; }
 
 int launch_rmsnorm_bwd(const float* dy, const float* y, const float* rms, const float* w, const float* dx_add,
-                       float* dx, float* partial, float* grad_w, int rows, int dm, hipStream_t s) {
+                       float* dx, float* partial, float* grad_w, int rows, int dm, hipStream_t s, bool accumulate) {
     const int nblk = rmsnorm_bwd_blocks(rows);
     hipLaunchKernelGGL(rmsnorm_bwd_rows_kernel, dim3(nblk), dim3(256), 0, s, dy, y, rms, w, dx_add, dx, partial,
                        (int64_t)rows, dm);
     DT_HIP_TRY(hipGetLastError());
-    return launch_colsum(partial, nblk, dm, grad_w, s);
+    return launch_colsum(partial, nblk, dm, grad_w, s, accumulate);
 }
 
-int launch_colsum(const float* partial, int nblk, int ncols, float* out, hipStream_t s) {
-    hipLaunchKernelGGL(colsum_kernel, dim3((ncols + 63) / 64), dim3(256), 0, s, partial, nblk, ncols, out);
+int launch_colsum(const float* partial, int nblk, int ncols, float* out, hipStream_t s, bool accumulate) {
+    hipLaunchKernelGGL(colsum_kernel, dim3((ncols + 63) / 64), dim3(256), 0, s, partial, nblk, ncols, out,
+                       accumulate ? 1 : 0);
     DT_HIP_TRY(hipGetLastError());
     return DT_OK;
 }

@@ -199,15 +199,15 @@ unsigned grid_for(int64_t n) {
 int norm_rope_bwd_blocks(int rows) { return (rows + kRows - 1) / kRows; }
 
 int launch_qk_norm_rope_bwd(const NormRopeBwdArgs& a, int bf16, float* grad_q_w, float* grad_k_w,
-                            hipStream_t stream) {
+                            hipStream_t stream, bool accumulate) {
     const int nblk = norm_rope_bwd_blocks(a.rows);
     dim3 grid(nblk, 2);
     if (bf16) hipLaunchKernelGGL(qk_norm_rope_bwd_kernel<true>, grid, dim3(256), 0, stream, a);
     else hipLaunchKernelGGL(qk_norm_rope_bwd_kernel<false>, grid, dim3(256), 0, stream, a);
     DT_HIP_TRY(hipGetLastError());
     const int C = a.H * 128;  // partial: [q, k][nblk][C]
-    DT_TRY(launch_colsum(a.partial, nblk, C, grad_q_w, stream));
-    return launch_colsum(a.partial + (int64_t)nblk * C, nblk, C, grad_k_w, stream);
+    DT_TRY(launch_colsum(a.partial, nblk, C, grad_q_w, stream, accumulate));
+    return launch_colsum(a.partial + (int64_t)nblk * C, nblk, C, grad_k_w, stream, accumulate);
 }
 
 int launch_sgd(float* w, const float* g, float lr, int64_t n, hipStream_t stream, uint16_t* w16) {

@@ -82,6 +82,40 @@ def test_grads_accumulate_until_zero_grad(gpu, weights):
     assert all(np.count_nonzero(v) == 0 for v in layer.grads().values())
 
 
+@pytest.mark.parametrize("mode,tol", [("fp32", 1e-6), ("bf16", 1e-4)])
+def test_backward_after_zero_grad_overwrites(gpu, weights, mode, tol):
+    """zero_grad leaves the buffers as they are and the next backward writes the gradients instead of adding
+    to them: after backward(x1), zero_grad, backward(x2) the gradients are those of x2 alone (the gradients
+    of a new layer's single backward on x2; the GEMMs then differ only in beta, so the tolerance is tight),
+    a further backward adds to them again, and a step right after zero_grad leaves the weights unchanged."""
+    x1, g1 = synth.normal(2611, (1, 64, 2048)), synth.normal(2612, (1, 64, 2048))
+    x2, g2 = synth.normal(2613, (1, 64, 2048)), synth.normal(2614, (1, 64, 2048))
+    ref = new_layer(weights)
+    run(ref, x2, g2, gpu, mode)
+    only2 = ref.grads()
+    run(ref, x1, g1, gpu, mode)
+    both = ref.grads()
+    layer = new_layer(weights)
+    run(layer, x1, g1, gpu, mode)
+    layer.zero_grad()
+    run(layer, x2, g2, gpu, mode)  # no read of the gradients between zero_grad and this backward
+    run(layer, x1, g1, gpu, mode)
+    got = layer.grads()
+    for k in KEYS:
+        assert rel_err(got[k], both[k]) <= tol, k
+    layer.zero_grad()
+    run(layer, x2, g2, gpu, mode)
+    got = layer.grads()
+    for k in KEYS:
+        assert rel_err(got[k], only2[k]) <= tol, k
+    layer.zero_grad()
+    w0 = layer.weights()
+    layer.step(0.5)
+    w1 = layer.weights()
+    assert all(np.array_equal(w0[k], w1[k]) for k in KEYS)
+    assert all(np.count_nonzero(v) == 0 for v in layer.grads().values())
+
+
 def test_step_is_sgd(gpu, weights):
     """step(lr): w -= lr * grad for all six parameters (OlmoAttention.cpp:314-321), then forward uses them."""
     x = synth.normal(2701, (1, 32, 2048))

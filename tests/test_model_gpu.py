@@ -92,6 +92,37 @@ def test_model_backward(gpu, params, mode, tol):
     assert max(errs.values()) <= tol, worst
 
 
+@pytest.mark.parametrize("mode,tol", [("fp32", 1e-6), ("bf16", 1e-4)])
+def test_backward_after_zero_grad_overwrites(gpu, params, mode, tol):
+    """zero_grad clears the embedding gradient at once and defers the others: the next backward writes them
+    instead of adding to them. backward(t1), zero_grad, backward(t2), backward(t1) equals a new model's
+    backward(t2) then backward(t1) (the GEMMs differ only in beta, so the tolerance is tight); a step right
+    after zero_grad leaves the weights unchanged."""
+    B, T = 1, 40
+    t1, t2 = synth.model_tokens(B, T, VOCAB, seed=6451), synth.model_tokens(B, T, VOCAB, seed=6452)
+    G1 = torch.from_numpy(synth.normal(6453, (B, T, VOCAB), 0.0, 1e-3)).to(gpu)
+    G2 = torch.from_numpy(synth.normal(6454, (B, T, VOCAB), 0.0, 1e-3)).to(gpu)
+    ref = OlmoModel.from_params(params)
+    for t, G in ((t2, G2), (t1, G1)):
+        ref.forward(t, mode=mode)
+        ref.backward(G)
+    want = {k: ref.grad(k) for k in params}
+    model = OlmoModel.from_params(params)
+    model.forward(t1, mode=mode)
+    model.backward(G1)
+    model.zero_grad()
+    for t, G in ((t2, G2), (t1, G1)):  # no read of the gradients in between
+        model.forward(t, mode=mode)
+        model.backward(G)
+    errs = {k: rel_err(model.grad(k), want[k]) for k in params}
+    assert max(errs.values()) <= tol, sorted(errs.items(), key=lambda kv: -kv[1])[:3]
+    model.zero_grad()
+    w0 = {k: model.param(k) for k in params}
+    model.step(0.5)
+    assert all(np.array_equal(model.param(k), w0[k]) for k in params)
+    assert all(np.count_nonzero(model.grad(k)) == 0 for k in params)
+
+
 def test_train_step_like_main_cpp(gpu, params):
     """main.cpp:59-91: forward, ce_loss, its gradient, backward, step(1e-4), zero_grad, forward again; a
     right-padded batch (pad = the ignore index). Losses and updated weights against the oracle."""
