@@ -213,4 +213,8 @@ int launch_rmsnorm_bwd(const float* dy, const float* y, const float* rms, const 
 int launch_swiglu_bwd(const float* d_act, const void* gu, void* d_gu, int rows, int hid, int bf16, hipStream_t s);
 int launch_embed_bwd(const float* dx, const int32_t* uniq, const int32_t* start, const int32_t* pos, int n_uniq,
                      float* g_embed, int dm, hipStream_t s);
+// for each listed row r (rows on the device, each < the table's row count): w[r] -= lr * g[r], or, with
+// zero_rows, g[r] = 0
+int launch_embed_rows(float* w, float* g, const int32_t* rows, int n_rows, int dm, float lr, bool zero_rows,
+                      hipStream_t s);
 }  // namespace dt

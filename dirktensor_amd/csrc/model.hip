@@ -19,6 +19,7 @@
 #include <cmath>
 #include <cstdio>
 #include <cstring>
+#include <iterator>
 #include <map>
 #include <string>
 #include <vector>
@@ -61,6 +62,11 @@ struct dt_model {
     // at once, and the attention layers', which keep their own flag) have not been cleared: they read as zero,
     // the next backward writes them instead of adding to them, and anything else that reads them clears them first
     bool grad_zero_pending = false;
+    // embedding-gradient rows a backward has written since the last zero_grad (sorted; on the device in
+    // embed_rows_dev), or all rows (embed_rows_all): every other row is zero, so step and zero_grad visit only these
+    std::vector<int32_t> embed_rows;
+    bool embed_rows_all = false;
+    DeviceBuffer embed_rows_dev;
     std::vector<ModelLayer> L;
     DeviceBuffer tok, x, x2, yf, yf16, rmsf, logits;
     // saved forward
@@ -278,7 +284,8 @@ int dt_model_destroy(dt_model* M) {
             b->release();
     }
     for (DeviceBuffer* b : {&M->tok, &M->x, &M->x2, &M->yf, &M->yf16, &M->rmsf, &M->logits, &M->d16, &M->dx, &M->dh,
-                            &M->da, &M->dxa, &M->dm_, &M->d_act, &M->d_gu, &M->partial, &M->csr})
+                            &M->da, &M->dxa, &M->dm_, &M->d_act, &M->d_gu, &M->partial, &M->csr,
+                            &M->embed_rows_dev})
         b->release();
     delete M;
     return DT_OK;
@@ -562,6 +569,21 @@ static int model_bwd(dt_model* M, const float* d_logits, int mem, void* stream, 
         }
     start.push_back(rows);
     const size_t nu = uniq.size();
+    if (!M->embed_rows_all) {  // (recorded before the scatter: a superset of the written rows is harmless)
+        std::vector<int32_t> merged;
+        std::set_union(M->embed_rows.begin(), M->embed_rows.end(), uniq.begin(), uniq.end(),
+                       std::back_inserter(merged));
+        // many rows: the dense passes are as cheap; a failed upload: fall back to them as well
+        const bool ok = merged.size() <= (size_t)V / 8 && M->embed_rows_dev.ensure(merged.size() * 4) == DT_OK &&
+                        hipMemcpyAsync(M->embed_rows_dev.ptr, merged.data(), merged.size() * 4,
+                                       hipMemcpyHostToDevice, s) == hipSuccess;
+        if (ok) {  // (the swap keeps the uploaded array alive; the backward ends with a stream synchronisation)
+            M->embed_rows.swap(merged);
+        } else {
+            M->embed_rows_all = true;
+            M->embed_rows.clear();
+        }
+    }
     DT_TRY(M->csr.ensure((nu + nu + 1 + rows) * 4));
     int32_t* dcsr = static_cast<int32_t*>(M->csr.ptr);
     std::vector<int32_t> packed;
@@ -603,8 +625,13 @@ int dt_model_step(dt_model* M, float lr, void* stream) {
     // same pass, so they are current afterwards
     bool copies = M->lm_head16 != nullptr;
     for (const ModelLayer& Ly : M->L) copies = copies && Ly.w_gu16 && Ly.w_down16;
-    // OlmoModel.cpp:69-75
-    DT_TRY(launch_sgd(M->embed, M->g_embed, lr, V * dm, s));
+    // OlmoModel.cpp:69-75. The embedding gradient is zero outside embed_rows, and for lr > 0 w - lr * 0 is w
+    // bit for bit (also for -0, inf and NaN), so only those rows are updated.
+    if (M->embed_rows_all || !(lr > 0.0f))
+        DT_TRY(launch_sgd(M->embed, M->g_embed, lr, V * dm, s));
+    else
+        DT_TRY(launch_embed_rows(M->embed, M->g_embed, static_cast<const int32_t*>(M->embed_rows_dev.ptr),
+                                 (int)M->embed_rows.size(), (int)dm, lr, false, s));
     for (ModelLayer& Ly : M->L) {
         DT_TRY(dt_attn_layer_step(Ly.attn, lr, stream));  // OlmoBlock.cpp:32-37
         DT_TRY(launch_sgd(Ly.w_pa, Ly.g_pa, lr, dm, s));
@@ -627,7 +654,13 @@ int dt_model_zero_grad(dt_model* M, void* stream) {
     const int64_t dm = M->dm, V = M->V;
     // OlmoModel.cpp:77-83. The embedding gradient is accumulated by a scatter over the batch's tokens, so it is
     // cleared here; the others are cleared lazily (the next backward overwrites them, see grad_zero_pending)
-    DT_TRY(launch_fill_zero(M->g_embed, V * dm, s));
+    if (M->embed_rows_all)
+        DT_TRY(launch_fill_zero(M->g_embed, V * dm, s));
+    else  // only the rows a backward wrote can be nonzero
+        DT_TRY(launch_embed_rows(M->embed, M->g_embed, static_cast<const int32_t*>(M->embed_rows_dev.ptr),
+                                 (int)M->embed_rows.size(), (int)dm, 0.0f, true, s));
+    M->embed_rows.clear();
+    M->embed_rows_all = false;
     for (ModelLayer& Ly : M->L) DT_TRY(dt_attn_layer_zero_grad(Ly.attn, stream));
     M->grad_zero_pending = true;
     return DT_OK;

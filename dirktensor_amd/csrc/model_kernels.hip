@@ -429,6 +429,41 @@ int launch_swiglu_bwd(const float* d_act, const void* gu, void* d_gu, int rows, 
     return DT_OK;
 }
 
+namespace {
+// SGD on the listed rows of an embedding table, w -= lr * g (separate product and difference, as sgd4_kernel);
+// with zero_rows set, the rows' gradients are cleared instead
+__global__ __launch_bounds__(256) void embed_rows_kernel(float* w, float* g, const int32_t* rows, int dm, float lr,
+                                                         int zero_rows) {
+#pragma clang fp contract(off)
+    const int64_t base = (int64_t)rows[blockIdx.x] * dm;
+    float4* g4 = reinterpret_cast<float4*>(g + base);
+    float4* w4 = reinterpret_cast<float4*>(w + base);
+    for (int i = threadIdx.x; i < dm / 4; i += 256) {
+        if (zero_rows) {
+            g4[i] = make_float4(0.f, 0.f, 0.f, 0.f);
+        } else {
+            const float4 gv = g4[i];
+            float4 wv = w4[i];
+            wv.x = wv.x - lr * gv.x;
+            wv.y = wv.y - lr * gv.y;
+            wv.z = wv.z - lr * gv.z;
+            wv.w = wv.w - lr * gv.w;
+            w4[i] = wv;
+        }
+    }
+}
+}  // namespace
+
+int launch_embed_rows(float* w, float* g, const int32_t* rows, int n_rows, int dm, float lr, bool zero_rows,
+                      hipStream_t s) {
+    if (n_rows == 0) return DT_OK;
+    if (dm % 4 != 0 || (reinterpret_cast<uintptr_t>(w) | reinterpret_cast<uintptr_t>(g)) % 16 != 0)
+        return set_error(DT_ERR_INVALID_ARG, "embedding rows: d_model %% 4 and 16-byte alignment required");
+    hipLaunchKernelGGL(embed_rows_kernel, dim3(n_rows), dim3(256), 0, s, w, g, rows, dm, lr, zero_rows ? 1 : 0);
+    DT_HIP_TRY(hipGetLastError());
+    return DT_OK;
+}
+
 int launch_embed_bwd(const float* dx, const int32_t* uniq, const int32_t* start, const int32_t* pos, int n_uniq,
                      float* g_embed, int dm, hipStream_t s) {
     if (n_uniq == 0) return DT_OK;

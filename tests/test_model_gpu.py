@@ -123,6 +123,26 @@ def test_backward_after_zero_grad_overwrites(gpu, params, mode, tol):
     assert all(np.count_nonzero(model.grad(k)) == 0 for k in params)
 
 
+@pytest.mark.parametrize("B,T", [(1, 40), (2, 100)])
+def test_embedding_step_and_zero_grad(gpu, params, B, T):
+    """step and zero_grad visit only the embedding rows a backward wrote (up to vocab / 8 distinct rows, the
+    dense passes beyond): the updated table is w - lr * grad on every row, bit for bit, over two backward calls
+    (rows of both batches), and zero_grad leaves the whole gradient zero."""
+    lr = 1e-2
+    model = OlmoModel.from_params(params)
+    for seed in (6461, 6462):
+        tok = synth.model_tokens(B, T, VOCAB, seed=seed)
+        model.forward(tok, mode="fp32")
+        model.backward(torch.from_numpy(synth.normal(seed + 10, (B, T, VOCAB), 0.0, 1e-3)).to(gpu))
+    key = "model.embed_tokens.weight"
+    w, g = model.param(key), model.grad(key)
+    assert np.count_nonzero(np.abs(g).sum(axis=1)) > 0
+    model.step(lr)
+    assert np.array_equal(model.param(key), w - np.float32(lr) * g)
+    model.zero_grad()
+    assert np.count_nonzero(model.grad(key)) == 0
+
+
 def test_train_step_like_main_cpp(gpu, params):
     """main.cpp:59-91: forward, ce_loss, its gradient, backward, step(1e-4), zero_grad, forward again; a
     right-padded batch (pad = the ignore index). Losses and updated weights against the oracle."""
