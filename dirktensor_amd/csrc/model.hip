@@ -625,9 +625,10 @@ int dt_model_step(dt_model* M, float lr, void* stream) {
     // same pass, so they are current afterwards
     bool copies = M->lm_head16 != nullptr;
     for (const ModelLayer& Ly : M->L) copies = copies && Ly.w_gu16 && Ly.w_down16;
-    // OlmoModel.cpp:69-75. The embedding gradient is zero outside embed_rows, and for lr > 0 w - lr * 0 is w
-    // bit for bit (also for -0, inf and NaN), so only those rows are updated.
-    if (M->embed_rows_all || !(lr > 0.0f))
+    // OlmoModel.cpp:69-75. The embedding gradient is +0 outside embed_rows, and for lr >= +0 the product lr * 0
+    // is +0 and w - (+0) is w bit for bit (also for w = -0, inf and NaN), so only those rows are updated; a
+    // negative lr or -0 would turn w = -0 into +0 there, so it takes the dense pass.
+    if (M->embed_rows_all || std::signbit(lr))
         DT_TRY(launch_sgd(M->embed, M->g_embed, lr, V * dm, s));
     else
         DT_TRY(launch_embed_rows(M->embed, M->g_embed, static_cast<const int32_t*>(M->embed_rows_dev.ptr),

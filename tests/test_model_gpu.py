@@ -123,12 +123,11 @@ def test_backward_after_zero_grad_overwrites(gpu, params, mode, tol):
     assert all(np.count_nonzero(model.grad(k)) == 0 for k in params)
 
 
-@pytest.mark.parametrize("B,T", [(1, 40), (2, 100)])
-def test_embedding_step_and_zero_grad(gpu, params, B, T):
-    """step and zero_grad visit only the embedding rows a backward wrote (up to vocab / 8 distinct rows, the
-    dense passes beyond): the updated table is w - lr * grad on every row, bit for bit, over two backward calls
-    (rows of both batches), and zero_grad leaves the whole gradient zero."""
-    lr = 1e-2
+@pytest.mark.parametrize("B,T,lr", [(1, 40, 1e-2), (1, 40, 0.0), (1, 40, -1e-2), (2, 100, 1e-2)])
+def test_embedding_step_and_zero_grad(gpu, params, B, T, lr):
+    """step and zero_grad visit only the embedding rows a backward wrote (up to vocab / 8 distinct rows and
+    lr >= +0; the dense passes otherwise): the updated table is w - lr * grad on every row, bit for bit, over
+    two backward calls (rows of both batches), and zero_grad leaves the whole gradient zero."""
     model = OlmoModel.from_params(params)
     for seed in (6461, 6462):
         tok = synth.model_tokens(B, T, VOCAB, seed=seed)
