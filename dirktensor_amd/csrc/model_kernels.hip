@@ -138,6 +138,9 @@ __global__ __launch_bounds__(256) void swiglu_bf16x8_kernel(const uint16_t* gu, 
 
 // One row of logits: target[row] >= 0 is the next token (a loss term), -1 none (no loss, zero gradient).
 // term[row] = log(sum exp(l - max)) - (l[target] - max); grad row (nullable) = (softmax - onehot) * inv_count.
+// kVec4: V % 4 == 0 and 16-byte aligned rows, read and written as float4 (HBM bound: two reads of the row
+// and one write of the gradient).
+template <bool kVec4>
 __global__ __launch_bounds__(256) void ce_rows_kernel(const float* logits, const int32_t* target, float* term,
                                                       float* grad, int V, float inv_count) {
     __shared__ float red_m[4], red_s[4];
@@ -153,13 +156,25 @@ __global__ __launch_bounds__(256) void ce_rows_kernel(const float* logits, const
     }
     // online (max, sum of exp) per thread, then combined over the workgroup
     float m = -__builtin_huge_valf(), s = 0.0f;
-    for (int i = threadIdx.x; i < V; i += 256) {
-        const float x = l[i];
-        if (x > m) {
-            s = s * expf(m - x) + 1.0f;
-            m = x;
-        } else {
-            s += expf(x - m);
+    if constexpr (kVec4) {
+        for (int i = threadIdx.x; i < V / 4; i += 256) {
+            const float4 x = reinterpret_cast<const float4*>(l)[i];
+            const float xm = fmaxf(fmaxf(x.x, x.y), fmaxf(x.z, x.w));
+            if (xm > m) {
+                s = s * expf(m - xm);
+                m = xm;
+            }
+            s += (expf(x.x - m) + expf(x.y - m)) + (expf(x.z - m) + expf(x.w - m));
+        }
+    } else {
+        for (int i = threadIdx.x; i < V; i += 256) {
+            const float x = l[i];
+            if (x > m) {
+                s = s * expf(m - x) + 1.0f;
+                m = x;
+            } else {
+                s += expf(x - m);
+            }
         }
     }
 #pragma unroll
@@ -181,10 +196,22 @@ __global__ __launch_bounds__(256) void ce_rows_kernel(const float* logits, const
     if (threadIdx.x == 0) term[row] = logf(se) - (l[tgt] - mx);
     if (g) {
         const float inv = 1.0f / se;
-        for (int i = threadIdx.x; i < V; i += 256) {
-            float p = expf(l[i] - mx) * inv;
-            if (i == tgt) p -= 1.0f;
-            g[i] = p * inv_count;
+        if constexpr (kVec4) {
+            for (int i = threadIdx.x; i < V / 4; i += 256) {
+                const float4 x = reinterpret_cast<const float4*>(l)[i];
+                float p[4] = {expf(x.x - mx) * inv, expf(x.y - mx) * inv, expf(x.z - mx) * inv, expf(x.w - mx) * inv};
+#pragma unroll
+                for (int e = 0; e < 4; ++e)
+                    if (4 * i + e == tgt) p[e] -= 1.0f;
+                reinterpret_cast<float4*>(g)[i] =
+                    make_float4(p[0] * inv_count, p[1] * inv_count, p[2] * inv_count, p[3] * inv_count);
+            }
+        } else {
+            for (int i = threadIdx.x; i < V; i += 256) {
+                float p = expf(l[i] - mx) * inv;
+                if (i == tgt) p -= 1.0f;
+                g[i] = p * inv_count;
+            }
         }
     }
 }
@@ -393,7 +420,9 @@ int launch_swiglu(const void* gu, void* act, int rows, int hid, int bf16, hipStr
 int launch_ce_loss(const float* logits, const int32_t* target, float* term, float* grad, float* loss, int rows, int V,
                    int count, hipStream_t s) {
     const float inv = count > 0 ? 1.0f / (float)count : 0.0f;
-    hipLaunchKernelGGL(ce_rows_kernel, dim3(rows), dim3(256), 0, s, logits, target, term, grad, V, inv);
+    const bool vec = V % 4 == 0 && ((uintptr_t)logits | (uintptr_t)grad) % 16 == 0;
+    if (vec) hipLaunchKernelGGL(ce_rows_kernel<true>, dim3(rows), dim3(256), 0, s, logits, target, term, grad, V, inv);
+    else hipLaunchKernelGGL(ce_rows_kernel<false>, dim3(rows), dim3(256), 0, s, logits, target, term, grad, V, inv);
     DT_HIP_TRY(hipGetLastError());
     hipLaunchKernelGGL(ce_reduce_kernel, dim3(1), dim3(256), 0, s, term, (int64_t)rows, inv, loss);
     DT_HIP_TRY(hipGetLastError());
