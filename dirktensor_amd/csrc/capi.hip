@@ -772,18 +772,36 @@ int attn_layer_settle_grads(dt_attn_layer* L, hipStream_t s) {
     return DT_OK;
 }
 
+bool attn_layer_grads_complete(const dt_attn_layer* L) { return L->g_qkv && L->g_o && L->g_qn && L->g_kn; }
+
+void attn_layer_free_grads(dt_attn_layer* L) {
+    for (float** p : {&L->g_qkv, &L->g_o, &L->g_qn, &L->g_kn})
+        if (*p) {
+            (void)hipFree(*p);
+            *p = nullptr;
+        }
+}
+
+// The four gradient buffers exist together or not at all: a failed allocation frees what was allocated, so
+// no later call sees g_qkv set with another slot null.
 int attn_layer_ensure_grads(dt_attn_layer* L, hipStream_t s) {
-    if (L->g_qkv) return DT_OK;
+    if (attn_layer_grads_complete(L)) return DT_OK;
+    attn_layer_free_grads(L);
     const size_t dm = L->d_model;
-    DT_HIP_TRY(hipMalloc(&L->g_qkv, 3 * dm * dm * 4));
-    DT_HIP_TRY(hipMalloc(&L->g_o, dm * dm * 4));
-    DT_HIP_TRY(hipMalloc(&L->g_qn, dm * 4));
-    DT_HIP_TRY(hipMalloc(&L->g_kn, dm * 4));
-    DT_TRY(launch_fill_zero(L->g_qkv, (int64_t)(3 * dm * dm), s));
-    DT_TRY(launch_fill_zero(L->g_o, (int64_t)(dm * dm), s));
-    DT_TRY(launch_fill_zero(L->g_qn, (int64_t)dm, s));
-    DT_TRY(launch_fill_zero(L->g_kn, (int64_t)dm, s));
-    return DT_OK;
+    auto alloc_all = [&]() -> int {
+        DT_HIP_TRY(hipMalloc(&L->g_qkv, 3 * dm * dm * 4));
+        DT_HIP_TRY(hipMalloc(&L->g_o, dm * dm * 4));
+        DT_HIP_TRY(hipMalloc(&L->g_qn, dm * 4));
+        DT_HIP_TRY(hipMalloc(&L->g_kn, dm * 4));
+        DT_TRY(launch_fill_zero(L->g_qkv, (int64_t)(3 * dm * dm), s));
+        DT_TRY(launch_fill_zero(L->g_o, (int64_t)(dm * dm), s));
+        DT_TRY(launch_fill_zero(L->g_qn, (int64_t)dm, s));
+        DT_TRY(launch_fill_zero(L->g_kn, (int64_t)dm, s));
+        return DT_OK;
+    };
+    const int rc = alloc_all();
+    if (rc != DT_OK) attn_layer_free_grads(L);
+    return rc;
 }
 
 extern "C" {

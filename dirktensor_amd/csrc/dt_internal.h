@@ -193,7 +193,9 @@ struct dt_attn_layer {
 
 // zero-initialised attention layer (weights set afterwards), and its gradient buffers (allocated zeroed)
 int attn_layer_alloc(dt_ctx* ctx, int d_model, int n_heads, dt_attn_layer** out);
-int attn_layer_ensure_grads(dt_attn_layer* L, hipStream_t s);
+int attn_layer_ensure_grads(dt_attn_layer* L, hipStream_t s);  // all four buffers, or none on failure
+bool attn_layer_grads_complete(const dt_attn_layer* L);
+void attn_layer_free_grads(dt_attn_layer* L);
 // clears the gradient buffers when a zero_grad is pending (they are then zero in memory as well)
 int attn_layer_settle_grads(dt_attn_layer* L, hipStream_t s);
 

@@ -159,21 +159,51 @@ std::vector<std::string> param_names(int n_layers) {
     return v;
 }
 
+// every gradient slot of the model (its own and its blocks'; the attention layers keep theirs)
+std::vector<float**> model_grad_slots(dt_model* M) {
+    std::vector<float**> v = {&M->g_embed, &M->g_final, &M->g_lm};
+    for (ModelLayer& Ly : M->L)
+        for (float** p : {&Ly.g_pa, &Ly.g_pf, &Ly.g_gu, &Ly.g_down}) v.push_back(p);
+    return v;
+}
+
+// The gradient buffers exist as a whole set or not at all: a failed allocation frees what was allocated and
+// leaves every slot null, so no later backward, step or zero_grad sees a half-made set.
 int ensure_model_grads(dt_model* M, hipStream_t s) {
-    if (M->g_embed) return DT_OK;
+    bool complete = true;
+    for (float** p : model_grad_slots(M)) complete = complete && *p;
+    for (ModelLayer& Ly : M->L) complete = complete && attn_layer_grads_complete(Ly.attn);
+    if (complete) return DT_OK;
     const size_t dm = M->dm, hid = M->hid, V = M->V;
-    DT_TRY(alloc_f32(&M->g_embed, V * dm));
-    DT_TRY(alloc_f32(&M->g_final, dm));
-    DT_TRY(alloc_f32(&M->g_lm, V * dm));
-    for (ModelLayer& Ly : M->L) {
-        DT_TRY(attn_layer_ensure_grads(Ly.attn, s));
-        DT_TRY(alloc_f32(&Ly.g_pa, dm));
-        DT_TRY(alloc_f32(&Ly.g_pf, dm));
-        DT_TRY(alloc_f32(&Ly.g_gu, 2 * hid * dm));
-        DT_TRY(alloc_f32(&Ly.g_down, dm * hid));
+    auto alloc_all = [&]() -> int {
+        DT_TRY(alloc_f32(&M->g_embed, V * dm));
+        DT_TRY(alloc_f32(&M->g_final, dm));
+        DT_TRY(alloc_f32(&M->g_lm, V * dm));
+        for (ModelLayer& Ly : M->L) {
+            DT_TRY(attn_layer_ensure_grads(Ly.attn, s));
+            DT_TRY(alloc_f32(&Ly.g_pa, dm));
+            DT_TRY(alloc_f32(&Ly.g_pf, dm));
+            DT_TRY(alloc_f32(&Ly.g_gu, 2 * hid * dm));
+            DT_TRY(alloc_f32(&Ly.g_down, dm * hid));
+        }
+        DT_HIP_TRY(hipDeviceSynchronize());  // the hipMemsets above are not stream-ordered with s
+        return DT_OK;
+    };
+    for (float** p : model_grad_slots(M))  // a partial set cannot be left from an earlier call, but be sure
+        if (*p) {
+            (void)hipFree(*p);
+            *p = nullptr;
+        }
+    const int rc = alloc_all();
+    if (rc != DT_OK) {
+        for (float** p : model_grad_slots(M))
+            if (*p) {
+                (void)hipFree(*p);
+                *p = nullptr;
+            }
+        for (ModelLayer& Ly : M->L) attn_layer_free_grads(Ly.attn);
     }
-    DT_HIP_TRY(hipDeviceSynchronize());  // the hipMemsets above are not stream-ordered with s
-    return DT_OK;
+    return rc;
 }
 
 // clears the gradient buffers of the model and of its attention layers when a zero_grad is pending

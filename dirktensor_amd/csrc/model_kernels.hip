@@ -138,6 +138,10 @@ __global__ __launch_bounds__(256) void swiglu_bf16x8_kernel(const uint16_t* gu, 
 
 // One row of logits: target[row] >= 0 is the next token (a loss term), -1 none (no loss, zero gradient).
 // term[row] = log(sum exp(l - max)) - (l[target] - max); grad row (nullable) = (softmax - onehot) * inv_count.
+// inv_count is NaN when no position has a target: the reference then divides by zero (CrossEntropyLoss.cpp:40,
+// main.cpp:88), so the loss and every gradient element are NaN, the rows without a target included.
+// grad may alias logits (main.cpp turns probs into the gradient in place): every element is read and then
+// written by the same thread, and l[target] is read before any thread writes.
 // kVec4: V % 4 == 0 and 16-byte aligned rows, read and written as float4 (HBM bound: two reads of the row
 // and one write of the gradient).
 template <bool kVec4>
@@ -151,9 +155,10 @@ __global__ __launch_bounds__(256) void ce_rows_kernel(const float* logits, const
     if (tgt < 0) {
         if (threadIdx.x == 0) term[row] = 0.0f;
         if (g)
-            for (int i = threadIdx.x; i < V; i += 256) g[i] = 0.0f;
+            for (int i = threadIdx.x; i < V; i += 256) g[i] = 0.0f * inv_count;
         return;
     }
+    const float l_tgt = threadIdx.x == 0 ? l[tgt] : 0.0f;  // before the barrier: the gradient may overwrite it
     // online (max, sum of exp) per thread, then combined over the workgroup
     float m = -__builtin_huge_valf(), s = 0.0f;
     if constexpr (kVec4) {
@@ -193,7 +198,7 @@ __global__ __launch_bounds__(256) void ce_rows_kernel(const float* logits, const
     for (int k = 1; k < 4; ++k) mx = fmaxf(mx, red_m[k]);
     float se = 0.0f;
     for (int k = 0; k < 4; ++k) se += red_s[k] * expf(red_m[k] - mx);
-    if (threadIdx.x == 0) term[row] = logf(se) - (l[tgt] - mx);
+    if (threadIdx.x == 0) term[row] = logf(se) - (l_tgt - mx);
     if (g) {
         const float inv = 1.0f / se;
         if constexpr (kVec4) {
@@ -419,7 +424,7 @@ int launch_swiglu(const void* gu, void* act, int rows, int hid, int bf16, hipStr
 
 int launch_ce_loss(const float* logits, const int32_t* target, float* term, float* grad, float* loss, int rows, int V,
                    int count, hipStream_t s) {
-    const float inv = count > 0 ? 1.0f / (float)count : 0.0f;
+    const float inv = count > 0 ? 1.0f / (float)count : __builtin_nanf("");  // 0 / 0 as in the reference
     const bool vec = V % 4 == 0 && ((uintptr_t)logits | (uintptr_t)grad) % 16 == 0;
     if (vec) hipLaunchKernelGGL(ce_rows_kernel<true>, dim3(rows), dim3(256), 0, s, logits, target, term, grad, V, inv);
     else hipLaunchKernelGGL(ce_rows_kernel<false>, dim3(rows), dim3(256), 0, s, logits, target, term, grad, V, inv);

@@ -69,6 +69,12 @@ int dt_version(void);
 /*
  * Context: owns the device binding, the RoPE tables, the rocBLAS handle and the
  * host-memory staging buffers. Not thread-safe: use one per host thread.
+ * Its workspaces (the hipBLASLt split-K buffer, the attention backward's row
+ * statistics, the staging buffers) are shared by every call made with it, so
+ * calls on one context must be ordered: issue them on one stream, or make a
+ * stream wait (an event) for the previous call's stream before the next call.
+ * Two calls on one context running at the same time on different streams race
+ * on those workspaces. Use one context per stream for concurrent work.
  * No reference counterpart: the reference keeps this state in file-scope
  * statics (OlmoAttention.cpp:34-36) and in TBB's global pool.
  */
@@ -238,7 +244,11 @@ int dt_model_zero_grad(dt_model* model, void* stream);
  * logits [B, T, V] against tokens[b][s+1] (a host array), skipping targets equal
  * to ignore_index; *loss is written to host memory. d_logits (nullable)
  * receives the gradient main.cpp:62-80 builds from it: (softmax - onehot) /
- * count at the positions with a target, 0 elsewhere.
+ * count at the positions with a target, 0 elsewhere. d_logits may be the same
+ * buffer as logits (main.cpp turns probs into the gradient in place). When no
+ * position has a target (T == 1, or every next token is ignore_index) the
+ * reference divides 0 by 0 (CrossEntropyLoss.cpp:40, main.cpp:88): *loss and
+ * every d_logits element are NaN here too.
  */
 int dt_ce_loss(dt_ctx* ctx, const float* logits, const int32_t* tokens, int B, int T, int V, int ignore_index,
                float* loss, float* d_logits, int mem, void* stream);

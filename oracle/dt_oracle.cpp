@@ -655,12 +655,15 @@ float oracle_ce_loss(const float* logits, const int32_t* tokens, int B, int T, i
                 g[tgt] -= 1.0f;
             }
         }
-    if (d_logits && count > 0) {
-        const float inv = 1.0f / (float)count;
+    // with no target at all the reference divides 0 by 0 (CrossEntropyLoss.cpp:40; main.cpp:88 divides the
+    // zeroed probs by a zero count): the loss and every gradient element are NaN
+    const float nan = std::numeric_limits<float>::quiet_NaN();
+    if (d_logits) {
+        const float inv = count > 0 ? 1.0f / (float)count : nan;
         for (size_t i = 0; i < (size_t)B * T * V; ++i) d_logits[i] *= inv;
     }
     if (count_out) *count_out = count;
-    return count > 0 ? (float)(total / count) : 0.0f;
+    return count > 0 ? (float)(total / count) : nan;
 }
 
 

@@ -67,6 +67,37 @@ def test_ce_loss_and_gradient(gpu, on_device, V):
     assert ce_loss(src, tok, PAD) == loss
 
 
+@pytest.mark.parametrize("V", [1000, 999])
+def test_ce_loss_gradient_in_place(gpu, V):
+    """d_logits == logits, as main.cpp reuses probs for the gradient (main.cpp:62-80): same loss and gradient
+    as with separate buffers."""
+    from dirktensor_amd import _capi, default_context
+
+    B, T = 2, 33
+    logits = synth.normal(6211, (B, T, V), 0.0, 3.0)
+    tok = synth.model_tokens(B, T, V, seed=6212)
+    tok[0, 20:] = PAD
+    ref_loss, ref_g = oracle.ce_loss(logits, tok, PAD, with_grad=True)
+    buf = torch.from_numpy(logits).to(gpu)
+    loss = np.zeros(1, np.float32)
+    tok32 = np.ascontiguousarray(tok, np.int32)
+    _capi.call("dt_ce_loss", default_context(0).handle, buf.data_ptr(), tok32.ctypes.data, B, T, V, PAD,
+               loss.ctypes.data, buf.data_ptr(), _capi.DT_MEM_DEVICE, torch.cuda.current_stream().cuda_stream)
+    assert abs(float(loss[0]) - ref_loss) <= 1e-5 * abs(ref_loss)
+    assert rel_err(to_np(buf), ref_g) <= 1e-5
+
+
+def test_ce_loss_without_targets_is_nan(gpu):
+    """Every next token ignored: the reference's 0 / 0 (CrossEntropyLoss.cpp:40, main.cpp:88), NaN loss and
+    gradient, like the oracle."""
+    V = 64
+    logits = synth.normal(6221, (2, 9, V))
+    tok = np.full((2, 9), PAD, np.int32)
+    tok[:, 0] = 3
+    loss, g = ce_loss(torch.from_numpy(logits).to(gpu), tok, PAD, with_grad=True)
+    assert np.isnan(loss) and bool(torch.isnan(g).all())
+
+
 def test_model_loss_full_vocab_shape(gpu):
     """ce_loss over the reference's vocab width (100352 logits per row) on a short sequence."""
     V = 100352

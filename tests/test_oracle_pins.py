@@ -422,6 +422,22 @@ def pin_ce_torch():
     return abs(loss - ref.item()) <= 1e-5 * abs(ref.item()) and rel(g, lt.grad.numpy()) <= 1e-5
 
 
+def pin_ce_no_targets():
+    """With no target at all (every next token ignored, or T = 1) the reference divides 0 by 0
+    (CrossEntropyLoss.cpp:40, main.cpp:88): loss NaN and every gradient element NaN. torch's mean over zero
+    terms is NaN as well."""
+    B, T, V, pad = 2, 9, 30, 4
+    logits = synth.normal(3103, (B, T, V))
+    tok = np.full((B, T), pad, np.int32)
+    tok[:, 0] = 1  # only position 0 is a real token; it is never a target
+    loss, g = oracle.ce_loss(logits, tok, pad, with_grad=True)
+    ref = F.cross_entropy(torch.from_numpy(logits[:, :-1]).double().reshape(-1, V),
+                          torch.from_numpy(tok[:, 1:]).long().reshape(-1), ignore_index=pad)
+    loss1, g1 = oracle.ce_loss(logits[:, :1], tok[:, :1], pad, with_grad=True)  # T = 1: no position has a target
+    return (np.isnan(loss) and np.isnan(ref.item()) and bool(np.all(np.isnan(g))) and np.isnan(loss1)
+            and bool(np.all(np.isnan(g1))))
+
+
 PINS = {
     "flash_textbook_causal": lambda: pin_flash_textbook(True),
     "flash_textbook_full": lambda: pin_flash_textbook(False),
@@ -438,6 +454,7 @@ PINS = {
     "flash_bwd_autograd_causal": lambda: pin_flash_bwd_autograd(True),
     "flash_bwd_autograd_full": lambda: pin_flash_bwd_autograd(False),
     "flash_bwd_finite_difference": pin_flash_bwd_finite_difference,
+    "ce_no_targets": pin_ce_no_targets,
     "flash_bwd_invariants": pin_flash_bwd_invariants,
     "rope_bwd_adjoint": pin_rope_bwd_adjoint,
     "rope_bwd_autograd": pin_rope_bwd_autograd,
