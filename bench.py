@@ -9,10 +9,17 @@ causal attention at the OLMo-2-1B head shape, B=1, T=4096, H=16, D=128, bf16
 Q/K/V/O with fp32 accumulation, Q/K/V ~ N(0,1) from seeds 1001-1003, already
 resident in HBM. Prints one JSON line: causal-attention TFLOP/s over the
 algorithmic work 2*B*H*D*T*(T+1) (unmasked pairs only, QK^T and PV, 2 flops
-per MAC), the prefill tokens/s of the attention core, the roofline fraction of
-the MFMA peak, and the CPU baseline: the oracle's restatement of the
-reference's flash_attention_forward (FlashAttention.cpp:24-182) timed on this
-host.
+per MAC), the tokens/s of the attention core, the roofline fraction of the
+MFMA peak, per-launch statistics, the peak re-derived from this device, and
+the CPU baseline: the oracle's restatement of the reference's
+flash_attention_forward (FlashAttention.cpp:24-182) timed on this host. The
+default line also carries the same workload in fp32 exact mode ("fp32_exact")
+and the end-to-end OLMo-2-1B prefill at T=2048 ("prefill",
+"prefill_tok_per_s"); --no-extras skips those two.
+
+Before the warm-up, every workload runs a clock-settle phase of about 100 ms
+of back-to-back launches ("clock_settle" in the line): the shader clock of an
+idle MI355X takes 30-50 ms of load to reach its sustained value.
 
 Other workloads (each prints one line of the same shape):
   flash_bwd    one dt_flash_attn_bwd (FlashAttention.cpp:185-359) at the same
@@ -44,43 +51,80 @@ from pathlib import Path
 ROOT = Path(__file__).resolve().parent
 sys.path.insert(0, str(ROOT))
 
-PEAK_TFLOPS = {"bf16": 2500.0, "fp32": 157.3}  # MI355X dense MFMA peaks
+PEAK_TFLOPS = {"bf16": 2500.0, "fp32": 157.3}  # MI355X dense MFMA peaks (AMD's published figures)
+FLOP_PER_CLK_PER_CU = {"bf16": 4096, "fp32": 256}  # dense MFMA rate of one gfx950 compute unit
 SCALE = 0.08838834764831845  # 1/sqrt(128) as fp32 (OlmoAttention.cpp:91)
+SETTLE_MS = 100.0  # clock-settle phase: back-to-back launches before the warm-up (see main)
+ORACLE_FLAGS = "-O3 -march=x86-64-v3 -ffast-math -fno-finite-math-only"  # oracle/Makefile (the reference: -ffast-math)
 
 
 def algorithmic_flops(B: int, T: int, H: int, D: int) -> int:
     return 2 * B * H * D * T * (T + 1)
 
 
+def cpu_model() -> str:
+    try:
+        for ln in open("/proc/cpuinfo"):
+            if ln.startswith("model name"):
+                return ln.split(":", 1)[1].strip()
+    except OSError:  # pragma: no cover
+        pass
+    return "unknown"
+
+
 def cpu_baseline(T: int, H: int, D: int, budget_s: float = 10.0) -> dict:
     """Times the oracle (the CPU restatement of FlashAttention.cpp:24-182) on the full workload,
-    repeated until ``budget_s`` has passed (at least 2 runs), threads = min(B*H, usable cores)."""
+    repeated until ``budget_s`` has passed (at least 2 runs), threads = min(B*H, usable cores) like the
+    reference's TBB loop over (b, h); then on one thread over 2 of the 16 heads (the per-head work is
+    identical, so the full single-thread time is 8x that), also median of repeated runs."""
     import numpy as np
 
     import oracle
     from dirktensor_amd import synth
 
     Q, K, V = synth.qkv(1, T, H)
-    try:
-        cores = len(os.sched_getaffinity(0))
-    except AttributeError:  # pragma: no cover
-        cores = os.cpu_count() or 1
-    threads = max(1, min(H, cores, 16))
-    times = []
-    t_start = time.perf_counter()
-    while len(times) < 2 or (time.perf_counter() - t_start < budget_s and len(times) < 50):
-        t0 = time.perf_counter()
-        oracle.flash_attention_forward(Q, K, V, SCALE, True, nthreads=threads)
-        times.append(time.perf_counter() - t0)
-    med = float(np.median(times))
+    threads, cores = _threads(H)
+    med, n = _time_cpu(lambda: oracle.flash_attention_forward(Q, K, V, SCALE, True, nthreads=threads), budget_s)
+    hs = 2
+    Q1, K1, V1 = (np.ascontiguousarray(x[:, :, :hs]) for x in (Q, K, V))
+    med1, n1 = _time_cpu(lambda: oracle.flash_attention_forward(Q1, K1, V1, SCALE, True, nthreads=1),
+                         max(budget_s / 2, 1.0))
     return {
         "value": algorithmic_flops(1, T, H, D) / med / 1e12,
         "unit": "TFLOP/s",
         "cores": threads,
         "kind": "port",
         "sample": f"oracle flash_attention_forward fp32, B=1 T={T} H={H} D={D} causal, full workload x "
-                  f"{len(times)} runs (median {med * 1e3:.1f} ms), {threads} threads of {cores} usable",
+                  f"{n} runs (median {med * 1e3:.1f} ms), {threads} threads of {cores} usable",
+        "cpu_model": cpu_model(),
+        "compile_flags": ORACLE_FLAGS,
+        "fast_math": True,
+        "one_thread": {"value": algorithmic_flops(1, T, hs, D) / med1 / 1e12, "unit": "TFLOP/s",
+                       "sample": f"{hs} of {H} heads x {n1} runs (median {med1 * 1e3:.1f} ms) on 1 thread"},
     }
+
+
+def device_peak(mode: str) -> dict:
+    """The MFMA peak re-derived from this device: compute units x dense MFMA flop per clock per CU x the
+    maximum shader clock that rocminfo reports for the gfx950 agent (published: 256 CUs, 2400 MHz)."""
+    import subprocess
+
+    cus, mhz, src = 256, 2400, "published (256 CUs, 2400 MHz)"
+    try:
+        out = subprocess.run(["rocminfo"], capture_output=True, text=True, timeout=20).stdout
+        for agent in out.split("Agent ")[1:]:
+            if "gfx950" not in agent:
+                continue
+            c = [int(ln.split(":")[1]) for ln in agent.splitlines() if ln.strip().startswith("Compute Unit:")]
+            f = [int(ln.split(":")[1]) for ln in agent.splitlines() if ln.strip().startswith("Max Clock Freq. (MHz):")]
+            if c and f:
+                cus, mhz, src = c[0], f[0], "rocminfo"
+            break
+    except Exception:  # noqa: BLE001 - the published figures stand in
+        pass
+    peak = cus * FLOP_PER_CLK_PER_CU[mode] * mhz * 1e6 / 1e12
+    return {"cus": cus, "max_sclk_mhz": mhz, "flop_per_clk_per_cu": FLOP_PER_CLK_PER_CU[mode],
+            "peak_tflops": round(peak, 1), "source": src}
 
 
 def load_traffic(mode: str, T: int):
@@ -123,19 +167,80 @@ def copy_calibration(mib: int, steps: int, warmup: int) -> int:
     return 0
 
 
+def _events(n):
+    import torch
+
+    return [torch.cuda.Event(enable_timing=True) for _ in range(n)]
+
+
+def settle_clock(step, stream, target_ms: float = SETTLE_MS) -> dict:
+    """Clock-settle phase, run before the warm-up whatever --warmup says. The MI355X shader clock ramps from
+    about 1.6 GHz to about 2.0 GHz over the first 30-50 ms of sustained load (measured in-kernel with s_memtime
+    against s_memrealtime), so back-to-back launches totalling ``target_ms`` of GPU time put the warm-up and
+    the timed region at the clock a sustained workload runs at. Reported as its own key, next to warmup."""
+    import torch
+
+    e0, e1 = _events(2)
+    e0.record(stream)
+    for _ in range(5):
+        step()
+    e1.record(stream)
+    torch.cuda.synchronize()
+    per = max(e0.elapsed_time(e1) / 5, 1e-3)
+    n = int(min(max(target_ms / per, 1), 20000))
+    e0.record(stream)
+    for _ in range(n):
+        step()
+    e1.record(stream)
+    torch.cuda.synchronize()
+    return {"launches": 5 + n, "gpu_ms": round(5 * per + e0.elapsed_time(e1), 2)}
+
+
+def time_steps(step, stream, steps: int) -> tuple:
+    """ms per step over ``steps`` back-to-back steps, HIP events on the launch stream; and the wall time."""
+    import torch
+
+    torch.cuda.synchronize()
+    e0, e1 = _events(2)
+    wall0 = time.perf_counter()
+    e0.record(stream)
+    for _ in range(steps):
+        step()
+    e1.record(stream)
+    torch.cuda.synchronize()
+    return e0.elapsed_time(e1) / steps, time.perf_counter() - wall0
+
+
+def launch_stats(step, stream, n: int, flops: float) -> dict:
+    """Per-launch durations from an event pair around each of ``n`` launches (a separate pass after the timed
+    region, so the events do not perturb it): median, min and p90 in microseconds, TFLOP/s at the median."""
+    import numpy as np
+    import torch
+
+    ev = _events(n + 1)
+    ev[0].record(stream)
+    for i in range(n):
+        step()
+        ev[i + 1].record(stream)
+    torch.cuda.synchronize()
+    us = np.array([ev[i].elapsed_time(ev[i + 1]) * 1e3 for i in range(n)])
+    med = float(np.median(us))
+    return {"n": n, "median_us": round(med, 2), "min_us": round(float(us.min()), 2),
+            "p90_us": round(float(np.percentile(us, 90)), 2), "median_tflops": round(flops / (med * 1e-6) / 1e12, 1)}
+
+
 def main() -> int:
     ap = argparse.ArgumentParser(description=__doc__, formatter_class=argparse.RawDescriptionHelpFormatter)
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=200)
-    # The MI355X shader clock ramps from about 1.6 GHz to about 2.0 GHz over the first 30-50 ms of
-    # sustained load (measured in-kernel with s_memtime against s_memrealtime); 500 launches of the
-    # T=4096 workload (about 45 ms) put the timed region at the settled clock a sustained workload runs at.
-    ap.add_argument("--warmup", type=int, default=500)
+    ap.add_argument("--warmup", type=int, default=20)
     ap.add_argument("--T", type=int, default=4096)
     ap.add_argument("--mode", choices=["bf16", "fp32"], default="bf16")
     ap.add_argument("--workload", choices=["flash_fwd", "flash_bwd", "ragged_fwd", "layer_fwd", "layer_train",
                                            "model_fwd", "model_train"], default="flash_fwd")
     ap.add_argument("--cpu-budget", type=float, default=10.0, help="seconds of CPU-baseline timing (0 = skip)")
+    ap.add_argument("--no-extras", action="store_true",
+                    help="default workload only: skip the fp32 exact-mode and end-to-end prefill figures")
     ap.add_argument("--copy-mib", type=int, default=0,
                     help="instead of attention, time a plain copy kernel over this many MiB (counter calibration)")
     args = ap.parse_args()
@@ -152,27 +257,18 @@ def main() -> int:
         return copy_calibration(args.copy_mib, args.steps, args.warmup)
 
     import dirktensor_amd as dt
-    from dirktensor_amd import _capi, synth
 
     dev = torch.device("cuda:0")
     stream = torch.cuda.current_stream(dev)
     ctx = dt.default_context(0)
     wl = WORKLOADS[args.workload](args, dev, stream, ctx)
 
+    settle = settle_clock(wl["step"], stream)
     for _ in range(args.warmup):
         wl["step"]()
-    torch.cuda.synchronize()
-    # events recorded on the stream the kernels are launched on (torch's current stream)
-    ev0 = torch.cuda.Event(enable_timing=True)
-    ev1 = torch.cuda.Event(enable_timing=True)
-    wall0 = time.perf_counter()
-    ev0.record(stream)
-    for _ in range(args.steps):
-        wl["step"]()
-    ev1.record(stream)
-    torch.cuda.synchronize()
-    wall = time.perf_counter() - wall0
-    ms = ev0.elapsed_time(ev1) / args.steps
+    # the timed region: exactly --steps steps, synchronised on both sides, events on the launch stream
+    ms, wall = time_steps(wl["step"], stream, args.steps)
+    stats = launch_stats(wl["step"], stream, max(args.steps, 50), wl["flops"]) if wl.get("stats", True) else None
 
     tflops = wl["flops"] / (ms * 1e-3) / 1e12
     peak = PEAK_TFLOPS[args.mode]
@@ -185,6 +281,7 @@ def main() -> int:
         "n_gpus": 1,
         "steps": args.steps,
         "warmup": args.warmup,
+        "clock_settle": settle,
         "ms_per_step": round(ms, 5),
         "higher_is_better": True,
         "scaling": "weak",
@@ -196,14 +293,68 @@ def main() -> int:
         "pct_of_peak": round(100.0 * tflops / peak, 2),
         "parity_rel_err": parity,
         "wall_s_timed_region": round(wall, 4),
+        "stats": stats,
+        "peak_derivation": device_peak(args.mode),
         "roofline": {"bound": "mfma", "achieved": round(tflops, 3), "peak": peak, "unit": "TFLOP/s",
                      "frac": round(tflops / peak, 4), "traffic": wl.get("traffic")},
         "cpu_baseline": cpu,
     }
     if args.workload == "flash_fwd":
+        line["attn_core_tok_per_s"] = line["tok_per_s"]  # tokens/s of the attention core alone, not prefill
+    if args.workload == "model_fwd":
         line["prefill_tok_per_s"] = line["tok_per_s"]
+    if args.workload == "flash_fwd" and args.mode == "bf16" and not args.no_extras:
+        line["fp32_exact"] = _extra(lambda: extra_fp32_exact(args, dev, stream, ctx))
+        line["prefill"] = _extra(lambda: extra_prefill(args, dev, stream, ctx))
+        if isinstance(line["prefill"], dict) and "prefill_tok_per_s" in line["prefill"]:
+            line["prefill_tok_per_s"] = line["prefill"]["prefill_tok_per_s"]
     print(json.dumps(line), flush=True)
     return 0
+
+
+def _extra(fn):
+    """An extra figure of the default line; a failure is reported in its place, not raised."""
+    try:
+        return fn()
+    except Exception as e:  # noqa: BLE001
+        return {"error": f"{type(e).__name__}: {e}"}
+
+
+def extra_fp32_exact(args, dev, stream, ctx) -> dict:
+    """The reference's own precision: the same attention workload in fp32 exact mode (fp32 MFMA), timed like
+    the headline (the clock is already settled), with its parity against the oracle on two heads."""
+    a = argparse.Namespace(**{**vars(args), "mode": "fp32"})
+    wl = wl_flash_fwd(a, dev, stream, ctx)
+    for _ in range(5):
+        wl["step"]()
+    steps = 20
+    ms, _ = time_steps(wl["step"], stream, steps)
+    tf = wl["flops"] / (ms * 1e-3) / 1e12
+    return {"value": round(tf, 2), "unit": "TFLOP/s", "steps": steps, "ms_per_step": round(ms, 4),
+            "pct_of_fp32_peak": round(100.0 * tf / PEAK_TFLOPS["fp32"], 2),
+            "peak": PEAK_TFLOPS["fp32"], "parity_rel_err": wl["parity"](), "tolerance": 1e-4,
+            "config": wl["config"]["workload"]}
+
+
+def extra_prefill(args, dev, stream, ctx) -> dict:
+    """End-to-end prefill (OlmoModel::forward, OlmoModel.cpp:25-48) at the OLMo-2-1B shape, tokens [1, 2048],
+    bf16 mode, weights drawn on the device: tokens/s over the whole forward (embedding to logits), with the
+    logits' parity against the oracle's fp32 forward."""
+    import gc
+
+    a = argparse.Namespace(**{**vars(args), "T": 2048, "mode": "bf16"})
+    wl = wl_model_fwd(a, dev, stream, ctx)
+    for _ in range(3):
+        wl["step"]()
+    steps = 10
+    ms, _ = time_steps(wl["step"], stream, steps)
+    T = wl["config"]["T"]
+    out = {"prefill_tok_per_s": round(T / (ms * 1e-3), 1), "ms_per_forward": round(ms, 3), "steps": steps,
+           "tflops": round(wl["flops"] / (ms * 1e-3) / 1e12, 1), "parity_rel_err": wl["parity"](),
+           "tolerance": 2e-2, "config": wl["config"]["workload"] + ", 16 layers, d_model 2048, MLP 8192, vocab 100352"}
+    wl["release"]()
+    gc.collect()
+    return out
 
 
 def _threads(limit: int) -> tuple:
@@ -459,8 +610,8 @@ def wl_layer_train(args, dev, stream, ctx):
 
 
 def _model_setup(args, dev, n_layers=16, vocab=100352, hidden=8192, d=2048):
-    """The end-to-end model at the OLMo-2-1B shape with weights drawn on the device (seeded torch.Generator:
-    matrices ~ N(0, 0.02) rounded to bf16, norm weights ~ 1 + N(0, 0.01)); host copies for the oracle."""
+    """The end-to-end model at the OLMo-2-1B shape with weights drawn on the device
+    (synth.device_model_params, seed 5100); host copies for the oracle."""
     import ctypes
 
     import torch
@@ -468,26 +619,12 @@ def _model_setup(args, dev, n_layers=16, vocab=100352, hidden=8192, d=2048):
     import dirktensor_amd as dt
     from dirktensor_amd import OlmoModel, _capi, synth
 
-    gen = torch.Generator(device=dev)
-    gen.manual_seed(5100)
     ctx = dt.default_context(0)
     h = ctypes.c_void_p()
     _capi.call("dt_model_create", ctx.handle, n_layers, d, d // 128, hidden, vocab, ctypes.byref(h))
     model = OlmoModel(ctx=ctx, _handle=h, _dims=(n_layers, d, hidden, vocab))
-    shapes = {"self_attn.q_proj": (d, d), "self_attn.k_proj": (d, d), "self_attn.v_proj": (d, d),
-              "self_attn.o_proj": (d, d), "self_attn.q_norm": (d,), "self_attn.k_norm": (d,),
-              "post_attention_layernorm": (d,), "mlp.gate_proj": (hidden, d), "mlp.up_proj": (hidden, d),
-              "mlp.down_proj": (d, hidden), "post_feedforward_layernorm": (d,)}
-    names = [("model.embed_tokens.weight", (vocab, d))]
-    for i in range(n_layers):
-        names += [(f"model.layers.{i}.{n}.weight", shp) for n, shp in shapes.items()]
-    names += [("model.norm.weight", (d,)), ("lm_head.weight", (vocab, d))]
     host = {}
-    for name, shp in names:
-        if len(shp) == 1:
-            w = 1.0 + 0.01 * torch.randn(shp, generator=gen, device=dev)
-        else:
-            w = (0.02 * torch.randn(shp, generator=gen, device=dev)).bfloat16().float()
+    for name, w in synth.device_model_params(dev, n_layers, vocab, hidden, d):
         torch.cuda.synchronize()
         _capi.call("dt_model_set_param", model.handle, name.encode(), w.data_ptr(), w.numel(), _capi.DT_MEM_DEVICE)
         host[name] = w.cpu().numpy()
@@ -536,7 +673,12 @@ def wl_model_fwd(args, dev, stream, ctx):
                 "sample": f"oracle OlmoModel::forward fp32, 16 layers, tokens [1,{T}], vocab 100352, one full run "
                 f"({sec:.1f} s), {threads} threads of {cores} usable"}
 
-    return dict(step=step, flops=gemm + attn, tokens=T, parity=parity, cpu=cpu,
+    def release():  # frees the model's device memory and the host copies (the default line's extra)
+        model.close()
+        host.clear()
+        box.clear()
+
+    return dict(step=step, flops=gemm + attn, tokens=T, parity=parity, cpu=cpu, release=release,
                 metric=f"end-to-end prefill tok/s + TFLOP/s, OLMo-2-1B (16 layers, vocab 100352) T={T}",
                 data="synthetic (tokens ~ U[0,100352) seed 5001; weights drawn on the device, torch.Generator seed "
                      "5100: matrices N(0,0.02) rounded to bf16, norms 1+N(0,0.01))",

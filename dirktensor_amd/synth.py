@@ -138,6 +138,38 @@ def model_params(n_layers: int = 16, vocab: int = 100352, hidden: int = 8192, d_
     return out
 
 
+def model_param_shapes(n_layers: int = 16, vocab: int = 100352, hidden: int = 8192, d_model: int = 2048) -> list:
+    """(name, shape) of every OLMo-2 parameter in creation order (the order model_params draws them in)."""
+    d = d_model
+    shapes = {"self_attn.q_proj": (d, d), "self_attn.k_proj": (d, d), "self_attn.v_proj": (d, d),
+              "self_attn.o_proj": (d, d), "self_attn.q_norm": (d,), "self_attn.k_norm": (d,),
+              "post_attention_layernorm": (d,), "mlp.gate_proj": (hidden, d), "mlp.up_proj": (hidden, d),
+              "mlp.down_proj": (d, hidden), "post_feedforward_layernorm": (d,)}
+    names = [("model.embed_tokens.weight", (vocab, d))]
+    for i in range(n_layers):
+        names += [(f"model.layers.{i}.{n}.weight", shapes[n]) for n in MODEL_LAYER_PARAMS]
+    names += [("model.norm.weight", (d,)), ("lm_head.weight", (vocab, d))]
+    return names
+
+
+def device_model_params(device, n_layers: int = 16, vocab: int = 100352, hidden: int = 8192, d_model: int = 2048,
+                        seed: int = 5100):
+    """The OLMo-2-1B-sized weights drawn on the GPU (numpy's seeded draw of 1.48 B values takes minutes):
+    yields (name, fp32 device tensor) in creation order from one seeded torch.Generator on ``device``;
+    matrices ~ N(0, 0.02) rounded to bf16-representable fp32, norm weights ~ 1 + N(0, 0.01). The same seed
+    gives the same weights on the same torch build."""
+    import torch
+
+    gen = torch.Generator(device=device)
+    gen.manual_seed(seed)
+    for name, shape in model_param_shapes(n_layers, vocab, hidden, d_model):
+        if len(shape) == 1:
+            w = 1.0 + 0.01 * torch.randn(shape, generator=gen, device=device)
+        else:
+            w = (0.02 * torch.randn(shape, generator=gen, device=device)).bfloat16().float()
+        yield name, w
+
+
 def model_tokens(B: int = 1, T: int = 2048, vocab: int = 100352, seed: int = 5001) -> np.ndarray:
     """Token ids ~ U[0, vocab) for the end-to-end workloads, int32 [B, T]."""
     return uniform_int(seed, B * T, 0, vocab - 1).astype(np.int32).reshape(B, T)
