@@ -181,19 +181,19 @@ def settle_clock(step, stream, target_ms: float = SETTLE_MS) -> dict:
     import torch
 
     e0, e1 = _events(2)
-    e0.record(stream)
-    for _ in range(5):
-        step()
-    e1.record(stream)
-    torch.cuda.synchronize()
-    per = max(e0.elapsed_time(e1) / 5, 1e-3)
-    n = int(min(max(target_ms / per, 1), 20000))
-    e0.record(stream)
-    for _ in range(n):
-        step()
-    e1.record(stream)
-    torch.cuda.synchronize()
-    return {"launches": 5 + n, "gpu_ms": round(5 * per + e0.elapsed_time(e1), 2)}
+    launches, gpu_ms, batch = 0, 0.0, 5
+    while gpu_ms < target_ms and launches < 20000:
+        e0.record(stream)
+        for _ in range(batch):
+            step()
+        e1.record(stream)
+        torch.cuda.synchronize()
+        t = e0.elapsed_time(e1)
+        launches += batch
+        gpu_ms += t
+        # the next batch covers what remains (at least one launch), at the rate just measured
+        batch = int(min(max((target_ms - gpu_ms) / max(t / batch, 1e-3), 1), 20000 - launches)) or 1
+    return {"launches": launches, "gpu_ms": round(gpu_ms, 2)}
 
 
 def time_steps(step, stream, steps: int) -> tuple:
