@@ -46,6 +46,8 @@ SIGNATURES = {
                                    ctypes.c_float, _c_int, _vp, _c_int, _c_int, _vp]),
     "dt_flash_attn_bwd": (_c_int, [_vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _c_int, _c_int, _c_int,
                                    _c_int, ctypes.c_float, _c_int, _c_int, _c_int, _vp]),
+    "dt_flash_attn_bwd_noalloc": (_c_int, [_vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _c_int, _c_int,
+                                           _c_int, _c_int, ctypes.c_float, _c_int, _c_int, _vp]),
     "dt_qk_norm_rope_fwd": (_c_int, [_vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _c_int, _c_int, _c_int, _c_int,
                                      _c_int, _c_int, _c_int, _c_int, _vp]),
     "dt_attn_layer_create": (_c_int, [_vp, _vp, _vp, _vp, _vp, _vp, _vp, _c_int, _c_int, _c_int, ctypes.POINTER(_vp)]),

@@ -319,7 +319,7 @@ extern "C" {
 
 const char* dt_last_error(void) { return t_err.c_str(); }
 
-int dt_version(void) { return 2; }
+int dt_version(void) { return 3; }
 
 int dt_ctx_create(int device, dt_ctx** out) {
     clear_error();
@@ -330,6 +330,7 @@ int dt_ctx_create(int device, dt_ctx** out) {
     DT_HIP_TRY(hipGetDeviceCount(&count));
     if (device >= count) return set_error(DT_ERR_INVALID_ARG, "device %d >= device count %d", device, count);
     DT_HIP_TRY(hipSetDevice(device));
+    DT_TRY(noalloc_setup(device));  // this device's address of the no-alloc entry point's scratch array
     dt_ctx* c = new dt_ctx();
     c->device = device;
     int rc = rope_upload(c, DT_ROPE_THETA, DT_MAX_SEQ_LEN);

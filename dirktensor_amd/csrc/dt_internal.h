@@ -144,6 +144,9 @@ int gemm_rm_bf16(dt_ctx* ctx, hipStream_t s, bool ta, bool tb, int M, int N, int
 // .npy reader (v1-v3 headers, little-endian fp32, C order)
 int read_npy_f32(const std::string& path, std::vector<float>& out, std::vector<size_t>& shape);
 bool aligned16(const void* p);
+// once per device, with it current (dt_ctx_create): looks up that device's address of the scratch array of
+// dt_flash_attn_bwd_noalloc (noalloc.hip)
+int noalloc_setup(int device);
 int check_device_binding(dt_ctx* ctx);
 
 }  // namespace dt

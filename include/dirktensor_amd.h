@@ -124,6 +124,22 @@ int dt_flash_attn_bwd(dt_ctx* ctx, const void* d_o, const void* o, const float* 
                       float scale, int causal, int dtype, int mem, void* stream);
 
 /*
+ * dt_flash_attn_bwd without any allocation. No counterpart in the reference:
+ * it is for callers that cannot allocate device memory during the call (code
+ * under HIP graph capture, serving loops, harnesses that forbid hipMalloc).
+ * Same arguments and results as dt_flash_attn_bwd with mem = DT_MEM_DEVICE
+ * (device pointers only, stream-ordered), the same kernels, bit-identical
+ * output. The backward's row statistics go to a fixed device array of 8 MiB
+ * per GPU, set up by dt_ctx_create and held until the process ends, so
+ * B*T*H must be at most 1048576 (DT_ERR_UNSUPPORTED above that). Every call
+ * on one GPU shares that array: calls that overlap in time on one GPU (on
+ * different streams or host threads) race and must be ordered by the caller.
+ */
+int dt_flash_attn_bwd_noalloc(dt_ctx* ctx, const void* d_o, const void* o, const float* m, const float* l,
+                              const void* q, const void* k, const void* v, void* d_q, void* d_k, void* d_v, int B,
+                              int T, int H, int D, float scale, int causal, int dtype, void* stream);
+
+/*
  * Fused q/k RMSNorm + RoPE (replaces RMSNorm::forward for q_norm/k_norm,
  * RMSNorm.cpp:15-22, plus apply_rope, OlmoAttention.cpp:111-146, as called at
  * OlmoAttention.cpp:70,76,87-88).

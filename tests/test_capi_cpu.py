@@ -34,7 +34,7 @@ def test_every_declared_symbol_is_exported_and_bound():
     for n in names:
         assert hasattr(lib, n), f"{n} declared in the header but not exported"
     assert sorted(C.SIGNATURES) == names, "ctypes signature table and header disagree"
-    assert lib.dt_version() == 2
+    assert lib.dt_version() == 3
 
 
 def flash(**kw):
