@@ -158,14 +158,17 @@ __device__ __forceinline__ void dma_offsets(uint32_t (&voff)[4], int lane, int w
 // stalls every other step on the DMA just issued). stage_barrier() waits for them explicitly before any
 // wave reads the stage they fill. M0 holds the wave-uniform LDS destination (an operand bound to M0, so
 // the compiler sets it and knows it changed); lane i writes 16 (or 4) bytes at M0 + 16*i (4*i).
+// The compiler cannot insert the wait states the hardware needs before these instructions (5 after a VALU
+// write of an SGPR they read, such as a v_readlane reload of the descriptor; 1 after an SALU write of
+// M0), since it does not see inside the asm: s_nop 4 provides them.
 __device__ __forceinline__ uint32_t lds_addr(const void* p) {
     return (uint32_t)(uintptr_t)(const __attribute__((address_space(3))) void*)p;
 }
 __device__ __forceinline__ void dma16(uint32_t lds, uint32_t voff, __amdgpu_buffer_rsrc_t r) {
-    asm volatile("buffer_load_dwordx4 %0, %1, 0 offen lds" ::"v"(voff), "s"(r), "{m0}"(lds) : "memory");
+    asm volatile("s_nop 4\n\tbuffer_load_dwordx4 %0, %1, 0 offen lds" ::"v"(voff), "s"(r), "{m0}"(lds) : "memory");
 }
 __device__ __forceinline__ void dma4(uint32_t lds, uint32_t voff, __amdgpu_buffer_rsrc_t r) {
-    asm volatile("buffer_load_dword %0, %1, 0 offen lds" ::"v"(voff), "s"(r), "{m0}"(lds) : "memory");
+    asm volatile("s_nop 4\n\tbuffer_load_dword %0, %1, 0 offen lds" ::"v"(voff), "s"(r), "{m0}"(lds) : "memory");
 }
 // rows r0 .. T-1 of a [T][ld] bf16 tensor -> one LDS tile (rows past T arrive as zeros)
 __device__ __forceinline__ void dma_tile(uint8_t* tile, const uint16_t* base, int r0, int T, int ld,

@@ -90,12 +90,15 @@ __device__ __forceinline__ __amdgpu_buffer_rsrc_t make_rsrc(const void* base, ui
 // for them before reading the other LDS stage; stage_barrier() waits for them before any wave reads the
 // stage they fill. M0 (an operand bound to M0) holds the wave-uniform LDS destination; lane i writes 16
 // (or 4) bytes at M0 + 16*i (4*i).
+// The compiler cannot insert the wait states the hardware needs before these instructions (5 after a VALU
+// write of an SGPR they read, such as a v_readlane reload of the descriptor; 1 after an SALU write of M0),
+// since it does not see inside the asm: s_nop 4 provides them.
 __device__ __forceinline__ uint32_t lds_addr(const void* p) { return (uint32_t)(uintptr_t)(const lds_void*)p; }
 __device__ __forceinline__ void dma16(uint32_t lds, uint32_t voff, __amdgpu_buffer_rsrc_t r) {
-    asm volatile("buffer_load_dwordx4 %0, %1, 0 offen lds" ::"v"(voff), "s"(r), "{m0}"(lds) : "memory");
+    asm volatile("s_nop 4\n\tbuffer_load_dwordx4 %0, %1, 0 offen lds" ::"v"(voff), "s"(r), "{m0}"(lds) : "memory");
 }
 __device__ __forceinline__ void dma4(uint32_t lds, uint32_t voff, __amdgpu_buffer_rsrc_t r) {
-    asm volatile("buffer_load_dword %0, %1, 0 offen lds" ::"v"(voff), "s"(r), "{m0}"(lds) : "memory");
+    asm volatile("s_nop 4\n\tbuffer_load_dword %0, %1, 0 offen lds" ::"v"(voff), "s"(r), "{m0}"(lds) : "memory");
 }
 // this wave's LDS DMA and LDS accesses are complete before any wave passes it
 __device__ __forceinline__ void stage_barrier() { asm volatile("s_waitcnt vmcnt(0) lgkmcnt(0)\n\ts_barrier" ::: "memory"); }

@@ -31,9 +31,15 @@ struct RaggedOrder {
     uint16_t order[kMaxRaggedBatch];  // sequences by decreasing length (stable)
 };
 
-// the item index a workgroup takes in round `round` of the snake walk
+// The item index a workgroup takes in round `round` of the snake walk. Workgroup w runs on XCD w % 8
+// (workgroups are dealt to the eight XCDs in turn). In even rounds it takes item round*G + w, whose
+// (batch, head) index is congruent to w mod 8 when B*H and G are multiples of 8; in odd rounds it takes
+// the item mirrored across the round, of the partner w ^ 7 (same cost rank: w ^ 7 differs from w only in
+// its low three bits), whose (batch, head) index is again congruent to w mod 8. So every item of one head
+// runs on one XCD and the head's K/V rows pass through one L2.
 __device__ __forceinline__ int snake_item(int round, int G, int w) {
-    return (round & 1) ? (round + 1) * G - 1 - w : round * G + w;
+    const int wo = (G & 7) == 0 ? (w ^ 7) : w;
+    return (round & 1) ? (round + 1) * G - 1 - wo : round * G + w;
 }
 
 __device__ __forceinline__ Item decode_item(int k, int n_qt, int BH, int H) {
