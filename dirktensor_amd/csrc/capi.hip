@@ -7,6 +7,8 @@
 // shape checks are compiled-out asserts, CMakeLists.txt:68, and T > 8192 is
 // undefined behaviour there, OlmoAttention.cpp:129).
 
+#include "flash_items.h"
+
 #include <hipblaslt/hipblaslt.h>
 #include <rocblas/rocblas.h>
 
@@ -100,15 +102,33 @@ static int validate_seq_lens(const int32_t* seq_lens, int B, int T) {
     return DT_OK;
 }
 
-static int run_flash(dt_ctx* ctx, const FlashArgs& fa, const int32_t* seq_lens, int dtype, hipStream_t s) {
-    (void)ctx;
+static int run_flash(dt_ctx* ctx, const FlashArgs& fa_in, const int32_t* seq_lens, int dtype, hipStream_t s) {
     SeqLens sl;
     const SeqLens* lp = nullptr;
     if (seq_lens) {
-        std::memcpy(sl.len, seq_lens, sizeof(int32_t) * fa.B);
+        std::memcpy(sl.len, seq_lens, sizeof(int32_t) * fa_in.B);
         lp = &sl;
     }
-    return dtype == DT_BF16 ? launch_flash_fwd_bf16(fa, lp, s) : launch_flash_fwd_f32(fa, lp, s);
+    FlashArgs fa = fa_in;
+    fa.split_ws = nullptr;
+    fa.split_cnt = nullptr;
+    fa.split_slots = 0;
+    if (dtype != DT_BF16) return launch_flash_fwd_f32(fa, lp, s);
+    // the workspace for items split across workgroups, grown to what this launch uses (counters start zero)
+    int items = 0;
+    DT_TRY(flash_fwd_split_items(fa, lp, &items));
+    if (items > 0) {
+        const size_t cnt_bytes = sizeof(int) * (size_t)items;
+        if (ctx->fwd_split_cnt.bytes < cnt_bytes) {
+            DT_TRY(ctx->fwd_split_cnt.ensure(cnt_bytes));
+            DT_HIP_TRY(hipMemsetAsync(ctx->fwd_split_cnt.ptr, 0, ctx->fwd_split_cnt.bytes, s));
+        }
+        DT_TRY(ctx->fwd_split.ensure(sizeof(float) * (size_t)items * kMaxParts * kPartialFloats));
+        fa.split_ws = static_cast<float*>(ctx->fwd_split.ptr);
+        fa.split_cnt = static_cast<int*>(ctx->fwd_split_cnt.ptr);
+        fa.split_slots = items;
+    }
+    return launch_flash_fwd_bf16(fa, lp, s);
 }
 
 // ---------------- rocBLAS helpers ----------------
@@ -350,6 +370,8 @@ int dt_ctx_destroy(dt_ctx* ctx) {
     if (ctx->rope_sin) (void)hipFree(ctx->rope_sin);
     for (auto& b : ctx->stage) b.release();
     ctx->bwd_stats.release();
+    ctx->fwd_split.release();
+    ctx->fwd_split_cnt.release();
     if (ctx->blas) rocblas_destroy_handle(static_cast<rocblas_handle>(ctx->blas));
     if (ctx->lt) {
         LtCache* lc = static_cast<LtCache*>(ctx->lt);

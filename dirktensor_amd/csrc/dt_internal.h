@@ -56,10 +56,17 @@ struct FlashArgs {
     float scale;
     int causal;
     int ragged;  // 1 when seq_lens are used
+    // workspace of items split across workgroups (the context's; see flash_items.h): partial results and
+    // one counter per split item, the counters zero between launches
+    float* split_ws;
+    int* split_cnt;
+    int split_slots;  // capacity of the workspace in split items (0: none, nothing is split)
 };
 
 int launch_flash_fwd_f32(const FlashArgs& a, const SeqLens* lens, hipStream_t stream);
 int launch_flash_fwd_bf16(const FlashArgs& a, const SeqLens* lens, hipStream_t stream);
+// split items a launch of the bf16 forward would use (the workspace capacity it needs, in items)
+int flash_fwd_split_items(const FlashArgs& a, const SeqLens* lens, int* n_items);
 
 // Arguments of one attention-core backward (FlashAttention.cpp:185-359). Row strides in elements.
 struct FlashBwdArgs {
@@ -163,6 +170,8 @@ struct dt_ctx {
     void* blas = nullptr;        // rocblas_handle, created on first use
     void* lt = nullptr;          // hipBLASLt handle and per-shape plans (capi.hip), created on first use
     dt::DeviceBuffer lt_ws;      // hipBLASLt workspace (split-K partial sums)
+    dt::DeviceBuffer fwd_split;  // attention forward: partial results of items split across workgroups
+    dt::DeviceBuffer fwd_split_cnt;  // and their counters (zeroed when allocated; each launch leaves them zero)
 };
 
 // OlmoAttention on the device (OlmoAttention.h:10-42): weights, forward state kept for backward, gradients.

@@ -5,12 +5,13 @@
 //
 // Work decomposition
 //   * An item is 128 queries of one (batch, head). A persistent grid of at most
-//     one workgroup per CU walks the items in "snake" order over a list sorted
-//     by causal cost (item k of round j: j*G + w on even rounds, (j+1)*G-1-w on
-//     odd ones), so a workgroup pairs a long query tile with a short one; at
-//     T = 4096, H = 16 every workgroup gets 33 key tiles of work. In a ragged
-//     batch the list holds only the tiles that start before their sequence's
-//     end, in the same cost order, followed by the padding tiles.
+//     one workgroup per CU walks a list of work units (flash_items.h) in "snake"
+//     order over decreasing causal cost, so a workgroup pairs a long query tile
+//     with a short one; at T = 4096, H = 16 every workgroup gets 33 key tiles of
+//     work. When the largest item costs at least twice a workgroup's fair share
+//     (few heads, e.g. a tensor-parallel shard), items are split into parts of
+//     consecutive key tiles on different workgroups; each part writes its
+//     partial (m, l, O) to a workspace and the last one to finish merges them.
 //   * A workgroup has 8 waves in two groups of 4. Both groups hold the same 128
 //     queries (32 per wave) and split the key tiles: group g takes 64-key tiles
 //     g, g+2, g+4, ... At the end group 1 hands its partial (max, sum, O) to
@@ -77,6 +78,7 @@ typedef short shortx4 __attribute__((ext_vector_type(4)));
 typedef short shortx8 __attribute__((ext_vector_type(8)));
 typedef __attribute__((address_space(3))) shortx4 lds_shortx4;
 typedef __attribute__((address_space(3))) void lds_void;
+typedef unsigned v4u32 __attribute__((ext_vector_type(4)));
 
 constexpr int kD = 128;
 constexpr int kBM = kItemRows;  // queries per item
@@ -249,15 +251,27 @@ __device__ __forceinline__ void tile_step(Acc& A, const bf16x8 (&qf)[8], const u
     });
 }
 
+// 16 bytes to / from a buffer with device-scope coherence (cache policy sc1): the access goes through to
+// the memory all XCDs share instead of stopping in this XCD's L2.
+constexpr int kCoherent = 16;  // sc1
+__device__ __forceinline__ void store_coherent(float4 v, __amdgpu_buffer_rsrc_t r, uint32_t off) {
+    __builtin_amdgcn_raw_buffer_store_b128(__builtin_bit_cast(v4u32, v), r, off, 0, kCoherent);
+}
+__device__ __forceinline__ float4 load_coherent(__amdgpu_buffer_rsrc_t r, uint32_t off) {
+    return __builtin_bit_cast(float4, __builtin_amdgcn_raw_buffer_load_b128(r, off, 0, kCoherent));
+}
+
 // Barrier for the double-buffered loop: this wave's LDS DMA and LDS accesses are
 // complete before any wave passes it.
 __device__ __forceinline__ void stage_barrier() { asm volatile("s_waitcnt vmcnt(0) lgkmcnt(0)\n\ts_barrier" ::: "memory"); }
 // Barrier over LDS accesses only: vector memory requests in flight are not waited for.
 __device__ __forceinline__ void lds_barrier() { asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory"); }
 
-__global__ __launch_bounds__(kThreads, 1) void flash_fwd_bf16_kernel(FlashArgs a, SeqLens lens, RaggedOrder ro) {
+__global__ __launch_bounds__(kThreads, 1) void flash_fwd_bf16_kernel(FlashArgs a, Schedule sc) {
     __shared__ __attribute__((aligned(1024))) Stage stage0;
     __shared__ __attribute__((aligned(1024))) Stage stage1;
+    __shared__ int last_part;  // this workgroup completes a split item
+    __shared__ int cum_lds[kMaxKinds + 1];  // the schedule's unit counts (searched once per unit)
 
     const int tid = threadIdx.x;
     const int lane = tid & 63;
@@ -311,19 +325,23 @@ __global__ __launch_bounds__(kThreads, 1) void flash_fwd_bf16_kernel(FlashArgs a
     }
 
     const int T = a.T;
-    const int n_qt = (T + kBM - 1) / kBM;
-    const int BH = a.B * a.H;
-    const int n_items = n_qt * BH;
     const int G = gridDim.x;
     const float c = a.scale * kLog2e;
 
-    for (int round = 0;; ++round) {
-        const int k_item = snake_item(round, G, (int)blockIdx.x);
-        if (k_item >= n_items) break;
-        const Item itm = a.ragged ? decode_item_ragged(k_item, n_qt, a.H, ro) : decode_item(k_item, n_qt, BH, a.H);
-        const int b = itm.b, h = itm.h;
-        const int L = a.ragged ? lens.len[b] : T;
-        const int q0 = itm.qt * kBM;
+    // a unit is decoded one round ahead (a search of the kind table, a chain of scalar loads), while the
+    // previous unit's first tile is on its way
+    if (!sc.dense) {
+        for (int j = tid; j <= sc.n_kinds; j += kThreads) cum_lds[j] = sc.cum[j];
+        __syncthreads();
+    }
+    int k_unit = snake_item(0, G, (int)blockIdx.x);
+    Unit u_next = decode_unit(k_unit < sc.n_units ? k_unit : 0, sc, a.H, cum_lds);
+    for (int round = 0; k_unit < sc.n_units; ++round) {
+        const Unit u = u_next;
+        const int k_next = snake_item(round + 1, G, (int)blockIdx.x);
+        const int b = u.b, h = u.h;
+        const int L = u.L;
+        const int q0 = u.qt * kBM;
         const int qw0 = q0 + wq * 32;
         const int qrow = qw0 + ln;
 
@@ -343,12 +361,17 @@ __global__ __launch_bounds__(kThreads, 1) void flash_fwd_bf16_kernel(FlashArgs a
                     if (a.l) a.l[stat_base + (int64_t)qrow * a.H] = 0.0f;
                 }
             }
+            k_unit = k_next;
+            if (k_next < sc.n_units) u_next = decode_unit(k_next, sc, a.H, cum_lds);
             continue;  // no LDS was touched: no barrier needed
         }
 
         const int k_end = a.causal ? min(q0 + kBM, L) : L;
-        const int n_tiles = (k_end + kBN - 1) / kBN;
-        const int n_iter = (n_tiles + 1) / 2;
+        // this unit's key tiles t0 .. t1-1: the whole item, or part u.part of S tiles (the last one the rest)
+        const int n_item_tiles = (k_end + kBN - 1) / kBN;
+        const int t0 = u.parts > 1 ? u.part * sc.S : 0;
+        const int t1 = u.parts > 1 ? min(t0 + sc.S, n_item_tiles) : n_item_tiles;
+        const int n_iter = max(t1 - t0 + 1, 0) / 2;
 
         // K (kv = 0) or V (kv = 1) of tile kt of this group -> one LDS stage, straight from HBM
         auto dma = [&](Stage& stg, int kv, int kt) {
@@ -362,9 +385,9 @@ __global__ __launch_bounds__(kThreads, 1) void flash_fwd_bf16_kernel(FlashArgs a
         };
         // The first tile streams into stage0 and the item's 128 query rows into stage1 (free until step 0),
         // both as whole 256-byte rows; rows past T arrive as zeros.
-        if (grp < n_tiles) {
-            dma(stage0, 0, grp);
-            dma(stage0, 1, grp);
+        if (t0 + grp < t1) {
+            dma(stage0, 0, t0 + grp);
+            dma(stage0, 1, t0 + grp);
         }
         uint8_t* Qs = &stage1[0][0][0];  // 128 rows x 256 bytes (group 0's K and V areas of stage1)
         {
@@ -374,6 +397,7 @@ __global__ __launch_bounds__(kThreads, 1) void flash_fwd_bf16_kernel(FlashArgs a
                 __builtin_amdgcn_raw_ptr_buffer_load_lds(rq, (lds_void*)(Qs + i * 8192 + wave * 1024), 16, qoff[i], 0, 0,
                                                          0);
         }
+        if (k_next < sc.n_units) u_next = decode_unit(k_next, sc, a.H, cum_lds);
 
         bf16x8 qf[8];  // filled from the Q tile once it has landed
         Acc A;
@@ -390,13 +414,13 @@ __global__ __launch_bounds__(kThreads, 1) void flash_fwd_bf16_kernel(FlashArgs a
         // Step on stage `cur` (tile kt) while the group's next tile kn streams into `nxt`: its K at the start
         // of the step, its V after the softmax, so the V rows do not compete with this step's K reads.
         auto step = [&](const Stage& cur, Stage& nxt, int kt, int kn) {
-            const bool dn = kn < n_tiles;
+            const bool dn = kn < t1;
             if (dn) dma(nxt, 0, kn);
             auto mid = [&]() {
                 if (dn) dma(nxt, 1, kn);
             };
             const int k0 = kt * kBN;
-            if (kt >= n_tiles || (a.causal && k0 > qw0 + 31)) {  // nothing of this tile is visible
+            if (kt >= t1 || (a.causal && k0 > qw0 + 31)) {  // nothing of this tile is visible
                 mid();
                 return;
             }
@@ -420,11 +444,11 @@ __global__ __launch_bounds__(kThreads, 1) void flash_fwd_bf16_kernel(FlashArgs a
         lds_barrier();  // every wave holds its Q fragment before step 0's DMA refills stage1
         for (int it = 0; it < n_iter; it += 2) {
             // even step: compute from stage0 while the group's next tile streams into stage1
-            step(stage0, stage1, 2 * it + grp, 2 * (it + 1) + grp);
+            step(stage0, stage1, t0 + 2 * it + grp, t0 + 2 * (it + 1) + grp);
             stage_barrier();
             if (it + 1 >= n_iter) break;
             // odd step: compute from stage1 while the tile after it streams into stage0
-            step(stage1, stage0, 2 * (it + 1) + grp, 2 * (it + 2) + grp);
+            step(stage1, stage0, t0 + 2 * (it + 1) + grp, t0 + 2 * (it + 2) + grp);
             stage_barrier();
         }
 
@@ -444,6 +468,11 @@ __global__ __launch_bounds__(kThreads, 1) void flash_fwd_bf16_kernel(FlashArgs a
             xs[128 + lane] = A.l;
         }
         __syncthreads();
+        // part p's partial result in the workspace (split items), and a float4's byte offset in it
+        auto partial_rsrc = [&](int part) {
+            return make_rsrc(a.split_ws + ((size_t)u.slot * kMaxParts + part) * kPartialFloats, (uint32_t)(kPartialFloats * 4));
+        };
+        auto pslot = [&](int k) { return (uint32_t)(((wq * 17 + k) * 64 + lane) * 16); };
         if (grp == 0) {
             const float m1s = xs[lane];
             const float m1t = xs[64 + lane];
@@ -453,11 +482,37 @@ __global__ __launch_bounds__(kThreads, 1) void flash_fwd_bf16_kernel(FlashArgs a
             const float a1 = (m1s == kNegInf) ? 0.0f : exp2f(m1s - ms);
             const float l = A.l * a0 + l1 * a1;
             const float mt = fmaxf(A.m_t, m1t);
-            if (qrow < T) {
-                const bool valid = qrow < L && l > 0.0f;
-                const float inv = valid ? 1.0f / l : 0.0f;
-                const float s0 = a0 * inv, s1 = a1 * inv;
-                uint16_t* op = Og + (int64_t)qrow * a.ldo;
+            if (u.parts == 1) {
+                if (qrow < T) {
+                    const bool valid = qrow < L && l > 0.0f;
+                    const float inv = valid ? 1.0f / l : 0.0f;
+                    const float s0 = a0 * inv, s1 = a1 * inv;
+                    uint16_t* op = Og + (int64_t)qrow * a.ldo;
+#pragma unroll
+                    for (int db = 0; db < 4; ++db)
+#pragma unroll
+                        for (int I = 0; I < 4; ++I) {
+                            float v[4];
+#pragma unroll
+                            for (int r = 0; r < 4; ++r) {
+                                const int i = 4 * I + r;
+                                v[r] = A.o[db][i] * s0 + xo[(16 * db + i) * 64 + lane] * s1;
+                            }
+                            uint2 w;
+                            w.x = pack_bf16x2(v[0], v[1]);
+                            w.y = pack_bf16x2(v[2], v[3]);
+                            *reinterpret_cast<uint2*>(&op[32 * db + 8 * I + 4 * hh]) = w;
+                        }
+                    if (hh == 0) {
+                        if (a.m) a.m[stat_base + (int64_t)qrow * a.H] = valid ? mt * (1.0f / kLog2e) : kNegInf;
+                        if (a.l) a.l[stat_base + (int64_t)qrow * a.H] = valid ? l * exp2f(ms - mt) : 0.0f;
+                    }
+                }
+            } else {
+                // this part's O relative to ms, both groups' keys, and (m_s, m_t, l) -> its workspace slot in
+                // register order: float4 k = 4*db + I of lane `lane` of wave wq at ((wq*17 + k)*64 + lane)*16
+                // bytes, k = 16 the statistics (1 KB contiguous per store instruction)
+                const __amdgpu_buffer_rsrc_t rp = partial_rsrc(u.part);
 #pragma unroll
                 for (int db = 0; db < 4; ++db)
 #pragma unroll
@@ -466,22 +521,90 @@ __global__ __launch_bounds__(kThreads, 1) void flash_fwd_bf16_kernel(FlashArgs a
 #pragma unroll
                         for (int r = 0; r < 4; ++r) {
                             const int i = 4 * I + r;
-                            v[r] = A.o[db][i] * s0 + xo[(16 * db + i) * 64 + lane] * s1;
+                            v[r] = A.o[db][i] * a0 + xo[(16 * db + i) * 64 + lane] * a1;
                         }
-                        uint2 w;
-                        w.x = pack_bf16x2(v[0], v[1]);
-                        w.y = pack_bf16x2(v[2], v[3]);
-                        *reinterpret_cast<uint2*>(&op[32 * db + 8 * I + 4 * hh]) = w;
+                        store_coherent(make_float4(v[0], v[1], v[2], v[3]), rp, pslot(4 * db + I));
                     }
-                if (hh == 0) {
-                    if (a.m) a.m[stat_base + (int64_t)qrow * a.H] = valid ? mt * (1.0f / kLog2e) : kNegInf;
-                    if (a.l) a.l[stat_base + (int64_t)qrow * a.H] = valid ? l * exp2f(ms - mt) : 0.0f;
+                store_coherent(make_float4(ms, mt, l, 0.0f), rp, pslot(16));
+            }
+        }
+        if (u.parts > 1) {  // the same for every wave of the workgroup
+            // The last of the item's parts to arrive merges them all, in part order, from the workspace; the
+            // counter goes back to zero for the next launch. The partials are written and read with device-scope
+            // coherent accesses (sc1: through to, and from, the memory every XCD sees), so no L2 write-back or
+            // invalidate is needed: a partial is complete once its stores are (vmcnt), before it is counted.
+            asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+            __syncthreads();
+            if (tid == 0) {
+                const int prev = __hip_atomic_fetch_add(&a.split_cnt[u.slot], 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+                const int last = prev == u.parts - 1;
+                if (last) __hip_atomic_store(&a.split_cnt[u.slot], 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+                last_part = last;
+            }
+            __syncthreads();
+            if (last_part) {
+                // group g merges dims 64g .. 64g+63 (float4 k = 8g .. 8g+7). The statistics of every part and the
+                // O values of parts 0 and 1 are requested together (a third part's after them)
+                float4 st[kMaxParts], x[2][8];
+#pragma unroll
+                for (int p = 0; p < kMaxParts; ++p)
+                    if (p < u.parts) st[p] = load_coherent(partial_rsrc(p), pslot(16));
+#pragma unroll
+                for (int p = 0; p < 2; ++p)
+#pragma unroll
+                    for (int j = 0; j < 8; ++j) x[p][j] = load_coherent(partial_rsrc(p), pslot(8 * grp + j));
+                float ms = kNegInf, mt = kNegInf;
+#pragma unroll
+                for (int p = 0; p < kMaxParts; ++p)
+                    if (p < u.parts) {
+                        ms = fmaxf(ms, st[p].x);
+                        mt = fmaxf(mt, st[p].y);
+                    }
+                float l = 0.0f;
+                float4 acc[8];
+#pragma unroll
+                for (int j = 0; j < 8; ++j) acc[j] = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
+                auto accumulate = [&](int p, const float4 (&xp)[8]) {  // in part order
+                    const float ap = (st[p].x == kNegInf) ? 0.0f : exp2f(st[p].x - ms);
+                    l += st[p].z * ap;
+#pragma unroll
+                    for (int j = 0; j < 8; ++j) {
+                        acc[j].x += xp[j].x * ap;
+                        acc[j].y += xp[j].y * ap;
+                        acc[j].z += xp[j].z * ap;
+                        acc[j].w += xp[j].w * ap;
+                    }
+                };
+                accumulate(0, x[0]);
+                accumulate(1, x[1]);
+                if (u.parts > 2) {
+#pragma unroll
+                    for (int j = 0; j < 8; ++j) x[0][j] = load_coherent(partial_rsrc(2), pslot(8 * grp + j));
+                    accumulate(2, x[0]);
+                }
+                if (qrow < T) {
+                    const bool valid = qrow < L && l > 0.0f;
+                    const float inv = valid ? 1.0f / l : 0.0f;
+                    uint16_t* op = Og + (int64_t)qrow * a.ldo;
+#pragma unroll
+                    for (int j = 0; j < 8; ++j) {  // k = 8*grp + j = 4*db + I
+                        const int k = 8 * grp + j;
+                        uint2 w;
+                        w.x = pack_bf16x2(acc[j].x * inv, acc[j].y * inv);
+                        w.y = pack_bf16x2(acc[j].z * inv, acc[j].w * inv);
+                        *reinterpret_cast<uint2*>(&op[32 * (k >> 2) + 8 * (k & 3) + 4 * hh]) = w;
+                    }
+                    if (grp == 0 && hh == 0) {
+                        if (a.m) a.m[stat_base + (int64_t)qrow * a.H] = valid ? mt * (1.0f / kLog2e) : kNegInf;
+                        if (a.l) a.l[stat_base + (int64_t)qrow * a.H] = valid ? l * exp2f(ms - mt) : 0.0f;
+                    }
                 }
             }
         }
         // group 0 has read the exchange (its LDS reads are complete) before the next item's DMA may overwrite
         // it; the output stores need not have completed
         lds_barrier();
+        k_unit = k_next;
     }
 }
 
@@ -504,18 +627,41 @@ int persistent_grid(int64_t n_items, int* grid) {
     return DT_OK;
 }
 
-int launch_flash_fwd_bf16(const FlashArgs& a, const SeqLens* lens, hipStream_t stream) {
+static int plan(const FlashArgs& a, const SeqLens* lens, int* grid, Schedule* sc) {
     SeqLens sl;
     if (a.ragged) sl = *lens;
     else sl.len[0] = a.T;
+    // the schedule is planned for one workgroup per CU; the grid is then at most one per unit
+    int cus = 0;
+    DT_TRY(persistent_grid(0x7fffffff, &cus));
+    build_schedule(a, sl, cus, true, sc);
+    *grid = sc->n_units < cus ? sc->n_units : cus;
+    return DT_OK;
+}
+
+int flash_fwd_split_items(const FlashArgs& a, const SeqLens* lens, int* n_items) {
+    int grid = 0;
+    Schedule sc;
+    DT_TRY(plan(a, lens, &grid, &sc));
+    *n_items = sc.n_slots;
+    return DT_OK;
+}
+
+int launch_flash_fwd_bf16(const FlashArgs& a, const SeqLens* lens, hipStream_t stream) {
     if (a.ldk != a.ldv) return set_error(DT_ERR_UNSUPPORTED, "bf16 kernel needs equal K and V row strides");
     if ((int64_t)a.T * a.ldk * 2 >= ((int64_t)1 << 31) || (int64_t)a.T * a.ldq * 2 >= ((int64_t)1 << 31))
         return set_error(DT_ERR_UNSUPPORTED, "Q/K/V extent of one sequence exceeds 2 GiB");
     int grid = 0;
-    DT_TRY(persistent_grid((int64_t)((a.T + kBM - 1) / kBM) * a.B * a.H, &grid));
-    RaggedOrder ro;
-    build_ragged_order(a, sl, &ro);
-    hipLaunchKernelGGL(flash_fwd_bf16_kernel, dim3(grid), dim3(kThreads), 0, stream, a, sl, ro);
+    Schedule sc;
+    DT_TRY(plan(a, lens, &grid, &sc));
+    if (sc.n_slots > 0 && (sc.n_slots > a.split_slots || !a.split_ws || !a.split_cnt)) {  // no room: whole items
+        SeqLens sl;
+        if (a.ragged) sl = *lens;
+        else sl.len[0] = a.T;
+        build_schedule(a, sl, grid, false, &sc);
+        grid = sc.n_units < grid ? sc.n_units : grid;
+    }
+    hipLaunchKernelGGL(flash_fwd_bf16_kernel, dim3(grid), dim3(kThreads), 0, stream, a, sc);
     DT_HIP_TRY(hipGetLastError());
     return DT_OK;
 }

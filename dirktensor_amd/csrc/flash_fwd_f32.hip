@@ -97,7 +97,7 @@ __device__ __forceinline__ void stage_barrier() { asm volatile("s_waitcnt vmcnt(
 // LDS accesses only: vector memory requests in flight (output stores) are not waited for
 __device__ __forceinline__ void lds_barrier() { asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory"); }
 
-__global__ __launch_bounds__(kThreads, 1) void flash_fwd_f32_kernel(FlashArgs a, SeqLens lens, RaggedOrder ro) {
+__global__ __launch_bounds__(kThreads, 1) void flash_fwd_f32_kernel(FlashArgs a, Schedule sc) {
     __shared__ __attribute__((aligned(1024))) Stage stage0;
     __shared__ __attribute__((aligned(1024))) Stage stage1;
 
@@ -121,19 +121,16 @@ __global__ __launch_bounds__(kThreads, 1) void flash_fwd_f32_kernel(FlashArgs a,
     }
 
     const int T = a.T;
-    const int n_qt = (T + kBM - 1) / kBM;
-    const int BH = a.B * a.H;
-    const int n_items = n_qt * BH;
     const int G = gridDim.x;
     const float c = a.scale * kLog2e;
 
     for (int round = 0;; ++round) {
-        const int k_item = snake_item(round, G, (int)blockIdx.x);
-        if (k_item >= n_items) break;
-        const Item itm = a.ragged ? decode_item_ragged(k_item, n_qt, a.H, ro) : decode_item(k_item, n_qt, BH, a.H);
-        const int b = itm.b, h = itm.h;
-        const int L = a.ragged ? lens.len[b] : T;  // valid keys / rows of this sequence
-        const int q0 = itm.qt * kBM;
+        const int k_unit = snake_item(round, G, (int)blockIdx.x);
+        if (k_unit >= sc.n_units) break;
+        const Unit u = decode_unit(k_unit, sc, a.H, sc.cum);  // a whole item: this kernel's schedules split nothing
+        const int b = u.b, h = u.h;
+        const int L = u.L;  // valid keys / rows of this sequence
+        const int q0 = u.qt * kBM;
         const int qw0 = q0 + wq * 32;  // first query of this wave
         const int qrow = qw0 + ln;
 
@@ -370,9 +367,9 @@ int launch_flash_fwd_f32(const FlashArgs& a, const SeqLens* lens, hipStream_t st
         return set_error(DT_ERR_UNSUPPORTED, "K/V extent of one sequence exceeds 2 GiB");
     int grid = 0;
     DT_TRY(persistent_grid((int64_t)((a.T + kBM - 1) / kBM) * a.B * a.H, &grid));
-    RaggedOrder ro;
-    build_ragged_order(a, sl, &ro);
-    hipLaunchKernelGGL(flash_fwd_f32_kernel, dim3(grid), dim3(kThreads), 0, stream, a, sl, ro);
+    Schedule sc;
+    build_schedule(a, sl, grid, false, &sc);
+    hipLaunchKernelGGL(flash_fwd_f32_kernel, dim3(grid), dim3(kThreads), 0, stream, a, sc);
     DT_HIP_TRY(hipGetLastError());
     return DT_OK;
 }

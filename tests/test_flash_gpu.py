@@ -114,6 +114,29 @@ def test_config4_ragged(gpu, mode):
     check_stats(m[valid], l[valid], m_ref[valid], l_ref[valid], tol)
 
 
+@pytest.mark.parametrize("B,T,H,lens", [(1, 4096, 2, None), (1, 2048, 4, None), (3, 1000, 5, [1000, 7, 129]),
+                                        (2, 3000, 3, [3000, 2900])])
+def test_split_items(gpu, B, T, H, lens):
+    """Shapes whose bf16 schedule splits the longest query tiles' keys across workgroups (up to three parts,
+    merged by the last part to finish): against the oracle, and bit-identical on a second call (the merge
+    order is fixed and the per-item counters return to zero)."""
+    Q, K, V = synth.qkv(B, T, H, seeds=(31 + T, 32 + T, 33 + T))
+    if lens is None:
+        O_ref, m_ref, l_ref = oracle.flash_attention_forward(Q, K, V, SCALE)
+        valid = np.ones((B, T), bool)
+    else:
+        lens = np.asarray(lens, np.int32)
+        O_ref, m_ref, l_ref = oracle.flash_attention_ragged(Q, K, V, lens, SCALE)
+        valid = np.arange(T)[None, :] < lens[:, None]
+    O, m, l = gpu_flash(Q, K, V, gpu, "bf16", seq_lens=lens)
+    assert rel_err(O[valid], O_ref[valid]) <= TOL_BF16
+    check_stats(m[valid], l[valid], m_ref[valid], l_ref[valid], TOL_BF16)
+    if lens is not None:
+        assert np.all(O[~valid] == 0.0) and np.all(m[~valid] == -np.inf) and np.all(l[~valid] == 0.0)
+    O2, m2, l2 = gpu_flash(Q, K, V, gpu, "bf16", seq_lens=lens)
+    assert np.array_equal(O2, O) and np.array_equal(m2, m) and np.array_equal(l2, l)
+
+
 @pytest.mark.parametrize("mode", ["fp32", "bf16"])
 def test_properties_full_size(gpu, mode):
     """Size-independent checks at T=4096, H=16: row 0 returns V[0] exactly (one key, p=1, l=1);
