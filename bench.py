@@ -235,6 +235,8 @@ def main() -> int:
     ap.add_argument("--steps", type=int, default=200)
     ap.add_argument("--warmup", type=int, default=20)
     ap.add_argument("--T", type=int, default=4096)
+    ap.add_argument("--H", type=int, default=16,
+                    help="heads (flash_fwd / flash_bwd; 2 is one GPU's share of 16 heads split 8 ways)")
     ap.add_argument("--mode", choices=["bf16", "fp32"], default="bf16")
     ap.add_argument("--workload", choices=["flash_fwd", "flash_bwd", "ragged_fwd", "layer_fwd", "layer_train",
                                            "model_fwd", "model_train"], default="flash_fwd")
@@ -303,7 +305,7 @@ def main() -> int:
         line["attn_core_tok_per_s"] = line["tok_per_s"]  # tokens/s of the attention core alone, not prefill
     if args.workload == "model_fwd":
         line["prefill_tok_per_s"] = line["tok_per_s"]
-    if args.workload == "flash_fwd" and args.mode == "bf16" and not args.no_extras:
+    if args.workload == "flash_fwd" and args.mode == "bf16" and args.H == 16 and not args.no_extras:
         line["fp32_exact"] = _extra(lambda: extra_fp32_exact(args, dev, stream, ctx))
         line["prefill"] = _extra(lambda: extra_prefill(args, dev, stream, ctx))
         if isinstance(line["prefill"], dict) and "prefill_tok_per_s" in line["prefill"]:
@@ -390,7 +392,7 @@ def wl_flash_fwd(args, dev, stream, ctx):
 
     from dirktensor_amd import _capi, synth
 
-    B, T, H, D = 1, args.T, 16, 128
+    B, T, H, D = 1, args.T, args.H, 128
     tdt = torch.bfloat16 if args.mode == "bf16" else torch.float32
     dtype = _capi.DT_BF16 if args.mode == "bf16" else _capi.DT_FP32_EXACT
     Qn, Kn, Vn = synth.qkv(B, T, H)
@@ -429,7 +431,7 @@ def wl_flash_bwd(args, dev, stream, ctx):
     import oracle
     from dirktensor_amd import _capi, synth
 
-    B, T, H, D = 1, args.T, 16, 128
+    B, T, H, D = 1, args.T, args.H, 128
     tdt = torch.bfloat16 if args.mode == "bf16" else torch.float32
     dtype = _capi.DT_BF16 if args.mode == "bf16" else _capi.DT_FP32_EXACT
     Qn, Kn, Vn = synth.qkv(B, T, H)
