@@ -86,6 +86,7 @@ constexpr int kBN = 64;        // keys per tile
 constexpr int kThreads = 512;  // 8 waves
 constexpr int kRowBytes = 256;               // one K or V row (128 bf16), unpadded
 constexpr int kTileBytes = kBN * kRowBytes;  // 16 KB per tensor per tile
+constexpr int kObufRow = kRowBytes + 16;     // a row of the output staging tile
 constexpr float kLog2e = 1.4426950408889634f;
 constexpr float kNegInf = -__builtin_huge_valf();
 constexpr float kRescaleLog2 = 8.0f;
@@ -456,13 +457,16 @@ __global__ __launch_bounds__(kThreads, 1) void flash_fwd_bf16_kernel(FlashArgs a
         // (no DMA is in flight now)
         A.m_t = max_halves(A.m_t);
         A.l = sum_halves(A.l);
-        float* xo = reinterpret_cast<float*>(&stage0[0][0][0]) + wq * (64 * 64);
+        // group 1's O of block wq: float4 k = 4*db + I of lane `lane` at xo[k*64 + lane] (16 KB per wave)
+        float4* xo = reinterpret_cast<float4*>(&stage0[0][0][0]) + wq * (16 * 64);
         float* xs = reinterpret_cast<float*>(&stage1[0][0][0]) + wq * (3 * 64);
+        uint8_t* obuf = &stage1[0][0][0] + 4096;  // the output tile on its way to HBM (128 x 272 bytes, after xs)
         if (grp == 1) {
 #pragma unroll
             for (int db = 0; db < 4; ++db)
 #pragma unroll
-                for (int i = 0; i < 16; ++i) xo[(16 * db + i) * 64 + lane] = A.o[db][i];
+                for (int I = 0; I < 4; ++I)
+                    xo[(4 * db + I) * 64 + lane] = make_float4(A.o[db][4 * I], A.o[db][4 * I + 1], A.o[db][4 * I + 2], A.o[db][4 * I + 3]);
             xs[lane] = A.m_s;
             xs[64 + lane] = A.m_t;
             xs[128 + lane] = A.l;
@@ -483,26 +487,30 @@ __global__ __launch_bounds__(kThreads, 1) void flash_fwd_bf16_kernel(FlashArgs a
             const float l = A.l * a0 + l1 * a1;
             const float mt = fmaxf(A.m_t, m1t);
             if (u.parts == 1) {
-                if (qrow < T) {
+                {
+                    // the output rows go to LDS (row-major, rows padded to 272 bytes so the 32 rows a write
+                    // instruction touches fall in different banks) and from there to HBM as whole rows, below
                     const bool valid = qrow < L && l > 0.0f;
                     const float inv = valid ? 1.0f / l : 0.0f;
                     const float s0 = a0 * inv, s1 = a1 * inv;
-                    uint16_t* op = Og + (int64_t)qrow * a.ldo;
+                    const int orow = 32 * wq + ln;
 #pragma unroll
                     for (int db = 0; db < 4; ++db)
 #pragma unroll
                         for (int I = 0; I < 4; ++I) {
+                            const float4 x1 = xo[(4 * db + I) * 64 + lane];
+                            const float x1v[4] = {x1.x, x1.y, x1.z, x1.w};
                             float v[4];
 #pragma unroll
-                            for (int r = 0; r < 4; ++r) {
-                                const int i = 4 * I + r;
-                                v[r] = A.o[db][i] * s0 + xo[(16 * db + i) * 64 + lane] * s1;
-                            }
+                            for (int r = 0; r < 4; ++r) v[r] = A.o[db][4 * I + r] * s0 + x1v[r] * s1;
                             uint2 w;
                             w.x = pack_bf16x2(v[0], v[1]);
                             w.y = pack_bf16x2(v[2], v[3]);
-                            *reinterpret_cast<uint2*>(&op[32 * db + 8 * I + 4 * hh]) = w;
+                            *reinterpret_cast<uint2*>(obuf + orow * kObufRow + 16 * (4 * db + I) + 8 * hh) = w;
                         }
+                }
+                if (qrow < T) {
+                    const bool valid = qrow < L && l > 0.0f;
                     if (hh == 0) {
                         if (a.m) a.m[stat_base + (int64_t)qrow * a.H] = valid ? mt * (1.0f / kLog2e) : kNegInf;
                         if (a.l) a.l[stat_base + (int64_t)qrow * a.H] = valid ? l * exp2f(ms - mt) : 0.0f;
@@ -517,15 +525,25 @@ __global__ __launch_bounds__(kThreads, 1) void flash_fwd_bf16_kernel(FlashArgs a
                 for (int db = 0; db < 4; ++db)
 #pragma unroll
                     for (int I = 0; I < 4; ++I) {
+                        const float4 x1 = xo[(4 * db + I) * 64 + lane];
+                        const float x1v[4] = {x1.x, x1.y, x1.z, x1.w};
                         float v[4];
 #pragma unroll
-                        for (int r = 0; r < 4; ++r) {
-                            const int i = 4 * I + r;
-                            v[r] = A.o[db][i] * a0 + xo[(16 * db + i) * 64 + lane] * a1;
-                        }
+                        for (int r = 0; r < 4; ++r) v[r] = A.o[db][4 * I + r] * a0 + x1v[r] * a1;
                         store_coherent(make_float4(v[0], v[1], v[2], v[3]), rp, pslot(4 * db + I));
                     }
                 store_coherent(make_float4(ms, mt, l, 0.0f), rp, pslot(16));
+            }
+        }
+        if (u.parts == 1) {  // the item's 128 output rows: 16 lanes per 256-byte row, 4 rows per store instruction
+            lds_barrier();
+            const int nrows = min(kBM, T - q0);
+#pragma unroll
+            for (int j = 0; j < 4; ++j) {
+                const int ch = j * kThreads + tid;  // 16-byte chunk ch % 16 of row ch / 16
+                const int r = ch >> 4, c = ch & 15;
+                const uint4 w = *reinterpret_cast<const uint4*>(obuf + r * kObufRow + 16 * c);
+                if (r < nrows) *reinterpret_cast<uint4*>(&Og[(int64_t)(q0 + r) * a.ldo + 8 * c]) = w;
             }
         }
         if (u.parts > 1) {  // the same for every wave of the workgroup
