@@ -63,6 +63,8 @@ struct FlashArgs {
     int split_slots;  // capacity of the workspace in split items (0: none, nothing is split)
 };
 
+// one workgroup per CU of the current device, at most n_items (0x7fffffff: the CU count)
+int persistent_grid(int64_t n_items, int* grid);
 int launch_flash_fwd_f32(const FlashArgs& a, const SeqLens* lens, hipStream_t stream);
 int launch_flash_fwd_bf16(const FlashArgs& a, const SeqLens* lens, hipStream_t stream);
 // split items a launch of the bf16 forward would use (the workspace capacity it needs, in items)

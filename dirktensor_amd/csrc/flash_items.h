@@ -172,7 +172,4 @@ inline void build_schedule(const FlashArgs& a, const SeqLens& sl, int G, bool sp
 // (each costs more than total / G).
 constexpr size_t kPartialFloats = (size_t)kItemRows * 136;
 
-// Persistent grid size: one workgroup per CU of the current device (at most the item count).
-int persistent_grid(int64_t n_items, int* grid);
-
 }  // namespace dt
