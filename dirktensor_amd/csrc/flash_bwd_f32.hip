@@ -228,9 +228,8 @@ struct DkdvStage {
     float delta[kTile];
 };
 
-__global__ __launch_bounds__(kThreads, 1) void flash_bwd_dkdv_f32_kernel(FlashBwdArgs a) {
-    __shared__ __attribute__((aligned(1024))) DkdvStage stg[2];
-
+// dK and dV of key block kb_own of (batch, head) bh
+__device__ __forceinline__ void dkdv_block(const FlashBwdArgs& a, int kb_own, int bh, DkdvStage (&stg)[2]) {
     const int tid = threadIdx.x;
     const int lane = tid & 63;
     const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
@@ -239,10 +238,6 @@ __global__ __launch_bounds__(kThreads, 1) void flash_bwd_dkdv_f32_kernel(FlashBw
     const int T = a.T;
     const float c = a.scale * kLog2e;
 
-    // one key block per workgroup, in decreasing causal cost (key block 0 sees every query tile): the
-    // hardware hands the next workgroup to the first CU that frees up, a longest-first schedule
-    const int kb_own = (int)blockIdx.x / (a.B * a.H);
-    const int bh = (int)blockIdx.x % (a.B * a.H);
     const int b = bh / a.H, h = bh % a.H;
 
     const float* Qg = static_cast<const float*>(a.q) + (int64_t)b * T * a.ld_qkv + (int64_t)h * kD;
@@ -321,9 +316,8 @@ struct DqStage {
     uint8_t v[kTileBytes];
 };
 
-__global__ __launch_bounds__(kThreads, 1) void flash_bwd_dq_f32_kernel(FlashBwdArgs a) {
-    __shared__ __attribute__((aligned(1024))) DqStage stg[2];
-
+// dQ of query block qb_own of (batch, head) bh
+__device__ __forceinline__ void dq_block(const FlashBwdArgs& a, int qb_own, int bh, DqStage (&stg)[2]) {
     const int tid = threadIdx.x;
     const int lane = tid & 63;
     const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
@@ -332,11 +326,6 @@ __global__ __launch_bounds__(kThreads, 1) void flash_bwd_dq_f32_kernel(FlashBwdA
     const int T = a.T;
     const float c = a.scale * kLog2e;
 
-    const int nqb = (T + kBlk - 1) / kBlk;
-    // one query block per workgroup, in decreasing causal cost (the last query block sees every key
-    // tile): the hardware hands the next workgroup to the first CU that frees up, a longest-first schedule
-    const int qb_own = nqb - 1 - (int)blockIdx.x / (a.B * a.H);
-    const int bh = (int)blockIdx.x % (a.B * a.H);
     const int b = bh / a.H, h = bh % a.H;
 
     const float* Qg = static_cast<const float*>(a.q) + (int64_t)b * T * a.ld_qkv + (int64_t)h * kD;
@@ -398,6 +387,29 @@ __global__ __launch_bounds__(kThreads, 1) void flash_bwd_dq_f32_kernel(FlashBwdA
     }
 }
 
+// One 128-row block per workgroup, listed in decreasing causal cost, so that the hardware, which hands
+// the next workgroup to the first CU that frees up, runs a longest-first schedule.
+// pass = 0 (dK/dV) or 1 (dQ): one pass per launch; workgroup BH*j + bh takes, for (batch, head) bh,
+//   key block j (dK/dV; key block 0 sees every query tile) or query block n-1-j (dQ).
+// pass = 2: both passes in one launch; workgroup 2*BH*j + BH*kind + bh takes the dK/dV of key block j
+//   (kind 0) or the dQ of query block n-1-j (kind 1), which see the same number of tiles under
+//   causality, so the list stays in decreasing cost and the two passes share the CUs.
+union BwdLds {
+    DkdvStage kv[2];
+    DqStage q[2];
+};
+
+__global__ __launch_bounds__(kThreads, 1) void flash_bwd_f32_kernel(FlashBwdArgs a, int pass) {
+    __shared__ __attribute__((aligned(1024))) BwdLds lds;
+    const int BH = a.B * a.H;
+    const int n = (a.T + kBlk - 1) / kBlk;
+    const int j = (int)blockIdx.x / (pass == 2 ? 2 * BH : BH);
+    const int kind = pass == 2 ? ((int)blockIdx.x / BH) & 1 : pass;
+    const int bh = (int)blockIdx.x % BH;
+    if (kind == 0) dkdv_block(a, j, bh, lds.kv);
+    else dq_block(a, n - 1 - j, bh, lds.q);
+}
+
 }  // namespace
 
 int launch_flash_bwd_f32(const FlashBwdArgs& a, hipStream_t stream) {
@@ -405,12 +417,19 @@ int launch_flash_bwd_f32(const FlashBwdArgs& a, hipStream_t stream) {
     if ((int64_t)a.T * ld * 4 >= ((int64_t)1 << 31))
         return set_error(DT_ERR_UNSUPPORTED, "Q/K/V/dO extent of one sequence exceeds 2 GiB");
     DT_TRY(launch_flash_bwd_prep(a, 0, stream));
-    const int64_t grid = (int64_t)((a.T + kBlk - 1) / kBlk) * a.B * a.H;  // one 128-row block per workgroup
-    if (grid > 0x7fffffff) return set_error(DT_ERR_UNSUPPORTED, "too many workgroups");
-    hipLaunchKernelGGL(flash_bwd_dkdv_f32_kernel, dim3((unsigned)grid), dim3(kThreads), 0, stream, a);
-    DT_HIP_TRY(hipGetLastError());
-    hipLaunchKernelGGL(flash_bwd_dq_f32_kernel, dim3((unsigned)grid), dim3(kThreads), 0, stream, a);
-    DT_HIP_TRY(hipGetLastError());
+    const int64_t blocks = (int64_t)((a.T + kBlk - 1) / kBlk) * a.B * a.H;  // per pass, one per workgroup
+    if (2 * blocks > 0x7fffffff) return set_error(DT_ERR_UNSUPPORTED, "too many workgroups");
+    int cus = 0;
+    DT_TRY(persistent_grid(0x7fffffff, &cus));
+    if (blocks <= cus) {  // the passes share one launch (at most one block per CU and pass)
+        hipLaunchKernelGGL(flash_bwd_f32_kernel, dim3((unsigned)(2 * blocks)), dim3(kThreads), 0, stream, a, 2);
+        DT_HIP_TRY(hipGetLastError());
+    } else {
+        for (int pass = 0; pass < 2; ++pass) {
+            hipLaunchKernelGGL(flash_bwd_f32_kernel, dim3((unsigned)blocks), dim3(kThreads), 0, stream, a, pass);
+            DT_HIP_TRY(hipGetLastError());
+        }
+    }
     return DT_OK;
 }
 
