@@ -24,6 +24,7 @@ constexpr int kItemRows = 128;  // queries per item
 constexpr int kMaxQTiles = 64;  // T <= 8192
 constexpr int kMaxKinds = 256;
 constexpr int kMaxParts = 3;
+constexpr int kMinPartTiles = 16;  // 64-key tiles
 
 // Kernel argument (3.6 KB).
 struct Schedule {
@@ -127,10 +128,14 @@ inline void build_schedule(const FlashArgs& a, const SeqLens& sl, int G, bool sp
     // partial result goes through the workspace), which measured as costly as the imbalance it removes at
     // B*H = 16, T = 2048 (largest item 1.9x the share), while few heads (a tensor-parallel shard) leave most
     // CUs idle without it.
+    // A part is at least kMinPartTiles tiles: its end (partial stores, counter, merge through memory) costs
+    // about three steps, too much for small items (B=1, T=512, H=16 split into 3-tile parts took 14.7 µs
+    // against 5 whole).
     int S = 0;
     if (split && a.causal && G > 0) {
         const int64_t fair = (total + G - 1) / G;
-        if (cmax >= 2 * fair) S = (int)std::max<int64_t>(fair, (cmax + kMaxParts - 1) / kMaxParts);
+        if (cmax >= 2 * fair)
+            S = (int)std::max<int64_t>(std::max<int64_t>(fair, kMinPartTiles), (cmax + kMaxParts - 1) / kMaxParts);
         if (S >= cmax) S = 0;
     }
     sc->S = S;

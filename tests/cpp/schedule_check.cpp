@@ -113,6 +113,7 @@ int main() {
         fails += check(1, 2048, 16, 0, {}, cus);
         fails += check(4, 777, 3, 0, {777, 1, 300, 500}, cus);
         fails += check(256, 8192, 1, 1, r256, cus);
+        fails += check(3, 4096, 2, 1, {4096, 2500, 129}, cus);
     }
     return fails != 0;
 }
