@@ -25,6 +25,8 @@ DT_BF16 = 1
 DT_MEM_DEVICE = 0
 DT_MEM_HOST = 1
 
+DT_OPT_QKV_FUSED = 1
+
 HEAD_DIM = 128
 MAX_SEQ_LEN = 8192
 D_MODEL = 2048
@@ -41,6 +43,7 @@ SIGNATURES = {
     "dt_version": (_c_int, []),
     "dt_ctx_create": (_c_int, [_c_int, ctypes.POINTER(_vp)]),
     "dt_ctx_destroy": (_c_int, [_vp]),
+    "dt_ctx_set_option": (_c_int, [_vp, _c_int, _c_int]),
     "dt_rope_table_init": (_c_int, [_vp, ctypes.c_float, _c_int]),
     "dt_flash_attn_fwd": (_c_int, [_vp, _vp, _vp, _vp, _vp, _vp, _vp, _c_int, _c_int, _c_int, _c_int,
                                    ctypes.c_float, _c_int, _vp, _c_int, _c_int, _vp]),

@@ -57,6 +57,11 @@ class Context:
     def rope_table_init(self, theta: float, max_seq_len: int) -> None:
         C.call("dt_rope_table_init", self.handle, float(theta), int(max_seq_len))
 
+    def set_qkv_fused(self, fused: bool) -> None:
+        """Layer forwards on this context: fused QKV projection + q/k norm + RoPE kernel (True), or one library
+        GEMM followed by the separate norm + RoPE kernel (False, the default)."""
+        C.call("dt_ctx_set_option", self.handle, C.DT_OPT_QKV_FUSED, int(bool(fused)))
+
 
 _default_ctx: dict = {}
 

@@ -131,6 +131,21 @@ static int run_flash(dt_ctx* ctx, const FlashArgs& fa_in, const int32_t* seq_len
     return launch_flash_fwd_bf16(fa, lp, s);
 }
 
+// The fused projection + norm + RoPE launch with the context's workspace (counters start zero).
+static int run_qkv_fused(dt_ctx* ctx, QkvArgs qa, int f32, hipStream_t s) {
+    size_t ss_bytes = 0, cnt_bytes = 0;
+    DT_TRY(qkv_norm_rope_workspace(qa.rows, qa.H, &ss_bytes, &cnt_bytes));
+    if (ctx->qkv_cnt.bytes < cnt_bytes) {
+        DT_TRY(ctx->qkv_cnt.ensure(cnt_bytes));
+        DT_HIP_TRY(hipMemsetAsync(ctx->qkv_cnt.ptr, 0, ctx->qkv_cnt.bytes, s));
+    }
+    DT_TRY(ctx->qkv_ss.ensure(ss_bytes));
+    qa.ss = static_cast<float*>(ctx->qkv_ss.ptr);
+    qa.ss_bytes = (int64_t)ctx->qkv_ss.bytes;
+    qa.cnt = static_cast<int*>(ctx->qkv_cnt.ptr);
+    return launch_qkv_norm_rope(qa, f32, s);
+}
+
 // ---------------- rocBLAS helpers ----------------
 static const char* blas_status_str(rocblas_status st) { return rocblas_status_to_string(st); }
 
@@ -362,6 +377,17 @@ int dt_ctx_create(int device, dt_ctx** out) {
     return DT_OK;
 }
 
+int dt_ctx_set_option(dt_ctx* ctx, int option, int value) {
+    clear_error();
+    if (!ctx) return set_error(DT_ERR_INVALID_ARG, "ctx is NULL");
+    if (option == DT_OPT_QKV_FUSED) {
+        if (value != 0 && value != 1) return set_error(DT_ERR_INVALID_ARG, "DT_OPT_QKV_FUSED takes 0 or 1, not %d", value);
+        ctx->qkv_fused = value;
+        return DT_OK;
+    }
+    return set_error(DT_ERR_INVALID_ARG, "unknown context option %d", option);
+}
+
 int dt_ctx_destroy(dt_ctx* ctx) {
     clear_error();
     if (!ctx) return DT_OK;
@@ -372,6 +398,8 @@ int dt_ctx_destroy(dt_ctx* ctx) {
     ctx->bwd_stats.release();
     ctx->fwd_split.release();
     ctx->fwd_split_cnt.release();
+    ctx->qkv_ss.release();
+    ctx->qkv_cnt.release();
     if (ctx->blas) rocblas_destroy_handle(static_cast<rocblas_handle>(ctx->blas));
     if (ctx->lt) {
         LtCache* lc = static_cast<LtCache*>(ctx->lt);
@@ -721,19 +749,27 @@ int dt_attn_layer_fwd(dt_attn_layer* L, const float* x, float* out, int B, int T
         float* qkv = static_cast<float*>(L->qkv_pre.ptr);
         DT_TRY(L->attn.ensure(act * 4));
         float* attn = static_cast<float*>(L->attn.ptr);
-        // Q|K|V = x [Wq;Wk;Wv]^T in one N = 3*d_model GEMM (OlmoAttention.cpp:68,74,80)
-        DT_TRY(gemm_xwt(ctx, s, rows, 3 * dm, dm, xd, dm, L->w_qkv, dm, qkv, 3 * dm, false));
-        // q/k norm + RoPE (OlmoAttention.cpp:70,76,87-88): in place, or into att32 (with V copied beside them)
-        // when the pre-norm projections must survive for the norms' backward
+        // the attention input: in place of the projections, or in att32 when the pre-norm projections must
+        // survive for the norms' backward
         float* att = qkv;
         if (save_for_backward) {
             DT_TRY(L->att32.ensure(act * 3 * 4));
             att = static_cast<float*>(L->att32.ptr);
         }
-        NormRopeArgs na{qkv, qkv + dm, save_for_backward ? qkv + 2 * dm : nullptr, L->q_norm, L->k_norm, att,
-                        att + dm, att + 2 * dm, rms, rms ? rms + rows : nullptr, ctx->rope_cos, ctx->rope_sin, rows, T,
-                        H, 3 * dm, 3 * dm, DT_RMS_EPS};
-        DT_TRY(launch_qk_norm_rope(na, 0, s));
+        if (ctx->qkv_fused && H % 4 == 0) {  // (the fused kernel needs H % 4 == 0)
+            // x [Wq;Wk;Wv]^T, q/k norm and RoPE in one kernel (OlmoAttention.cpp:63-88)
+            QkvArgs qa{xd, L->w_qkv, L->q_norm, L->k_norm, att, save_for_backward ? qkv : nullptr, rms,
+                       ctx->rope_cos, ctx->rope_sin, nullptr, 0, nullptr, rows, T, H, dm, 3 * dm, 3 * dm, DT_RMS_EPS};
+            DT_TRY(run_qkv_fused(ctx, qa, 1, s));
+        } else {
+            // Q|K|V = x [Wq;Wk;Wv]^T in one N = 3*d_model GEMM (OlmoAttention.cpp:68,74,80)
+            DT_TRY(gemm_xwt(ctx, s, rows, 3 * dm, dm, xd, dm, L->w_qkv, dm, qkv, 3 * dm, false));
+            // q/k norm + RoPE (OlmoAttention.cpp:70,76,87-88), with V copied beside them into att32
+            NormRopeArgs na{qkv, qkv + dm, save_for_backward ? qkv + 2 * dm : nullptr, L->q_norm, L->k_norm, att,
+                            att + dm, att + 2 * dm, rms, rms ? rms + rows : nullptr, ctx->rope_cos, ctx->rope_sin,
+                            rows, T, H, 3 * dm, 3 * dm, DT_RMS_EPS};
+            DT_TRY(launch_qk_norm_rope(na, 0, s));
+        }
         FlashArgs fa{att, att + dm, att + 2 * dm, attn, st_m, st_l, B, T, H, 3 * dm, 3 * dm, 3 * dm, dm,
                      scale, 1, seq_lens ? 1 : 0};
         DT_TRY(run_flash(ctx, fa, seq_lens, DT_FP32_EXACT, s));  // OlmoAttention.cpp:94
@@ -758,13 +794,21 @@ int dt_attn_layer_fwd(dt_attn_layer* L, const float* x, float* out, int B, int T
         uint16_t* qkv16 = static_cast<uint16_t*>(L->qkv16.ptr);
         uint16_t* attn16 = static_cast<uint16_t*>(L->attn.ptr);
         DT_TRY(launch_f32_to_bf16(xd, x16, (int64_t)act, s));
-        // the projections leave the GEMM as bf16 (fp32 accumulation, one rounding): the norm kernel reads half
-        // the bytes, and the norms' backward reads the same bf16 rows
-        DT_TRY(gemm_rm_bf16(ctx, s, false, true, rows, 3 * dm, dm, x16, dm, L->w_qkv16, dm, pre16, 3 * dm));
-        NormRopeArgs na{pre16, pre16 + dm, pre16 + 2 * dm, L->q_norm, L->k_norm, qkv16, qkv16 + dm, qkv16 + 2 * dm,
-                        rms, rms ? rms + rows : nullptr, ctx->rope_cos, ctx->rope_sin, rows, T, H, 3 * dm, 3 * dm,
-                        DT_RMS_EPS};
-        DT_TRY(launch_qk_norm_rope(na, 1, s, 1));
+        if (ctx->qkv_fused && H % 4 == 0) {  // (the fused kernel needs H % 4 == 0)
+            // x [Wq;Wk;Wv]^T, q/k norm and RoPE in one kernel (OlmoAttention.cpp:63-88); the pre-norm q|k rows
+            // (bf16) only when the norms' backward will read them
+            QkvArgs qa{x16, L->w_qkv16, L->q_norm, L->k_norm, qkv16, save_for_backward ? pre16 : nullptr, rms,
+                       ctx->rope_cos, ctx->rope_sin, nullptr, 0, nullptr, rows, T, H, dm, 3 * dm, 3 * dm, DT_RMS_EPS};
+            DT_TRY(run_qkv_fused(ctx, qa, 0, s));
+        } else {
+            // the projections leave the GEMM as bf16 (fp32 accumulation, one rounding): the norm kernel reads
+            // half the bytes, and the norms' backward reads the same bf16 rows
+            DT_TRY(gemm_rm_bf16(ctx, s, false, true, rows, 3 * dm, dm, x16, dm, L->w_qkv16, dm, pre16, 3 * dm));
+            NormRopeArgs na{pre16, pre16 + dm, pre16 + 2 * dm, L->q_norm, L->k_norm, qkv16, qkv16 + dm,
+                            qkv16 + 2 * dm, rms, rms ? rms + rows : nullptr, ctx->rope_cos, ctx->rope_sin, rows, T, H,
+                            3 * dm, 3 * dm, DT_RMS_EPS};
+            DT_TRY(launch_qk_norm_rope(na, 1, s, 1));
+        }
         FlashArgs fa{qkv16, qkv16 + dm, qkv16 + 2 * dm, attn16, st_m, st_l, B, T, H, 3 * dm, 3 * dm, 3 * dm,
                      dm, scale, 1, seq_lens ? 1 : 0};
         DT_TRY(run_flash(ctx, fa, seq_lens, DT_BF16, s));

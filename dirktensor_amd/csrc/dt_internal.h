@@ -114,6 +114,28 @@ struct NormRopeArgs {
 };
 int launch_qk_norm_rope(const NormRopeArgs& a, int out_bf16, hipStream_t stream, int in_bf16 = 0);
 
+// Fused x [Wq;Wk;Wv]^T -> rope(norm(q)) | rope(norm(k)) | v (qkv_proj.hip). x, w, out and pre share one
+// element type: bf16, or fp32 when launched with f32.
+struct QkvArgs {
+    const void* x;  // [rows][ldx]: the layer input rows (d_model = H*128 used)
+    const void* w;  // [3*d_model][d_model]: Wq, Wk, Wv rows
+    const float* q_w;  // q_norm / k_norm weights [d_model]
+    const float* k_w;
+    void* out;    // [rows][ld_out]: rotated, normalised q | k, then v
+    void* pre;    // nullable: [rows][ld_pre], the pre-norm q | k (v columns untouched)
+    float* rms;   // nullable: [2][rows], q then k
+    const float* rope_cos;  // [>= T][64]
+    const float* rope_sin;
+    float* ss;         // workspace: per-row, per-head partial sums of squares
+    int64_t ss_bytes;  // its size (qkv_norm_rope_workspace)
+    int* cnt;          // workspace: group counters, zero between launches
+    int rows, T, H;
+    int ldx, ld_out, ld_pre;  // elements
+    float eps;
+};
+int qkv_norm_rope_workspace(int rows, int H, size_t* ss_bytes, size_t* cnt_bytes);
+int launch_qkv_norm_rope(const QkvArgs& a, int f32, hipStream_t stream);
+
 // Backward of the fused q/k RMSNorm + RoPE (OlmoAttention.cpp:234-244): dq/dk rows are rewritten in place
 // from d(rope output) to d(pre-norm projection); the norm-weight gradients are accumulated (+=).
 struct NormRopeBwdArgs {
@@ -174,6 +196,9 @@ struct dt_ctx {
     dt::DeviceBuffer lt_ws;      // hipBLASLt workspace (split-K partial sums)
     dt::DeviceBuffer fwd_split;  // attention forward: partial results of items split across workgroups
     dt::DeviceBuffer fwd_split_cnt;  // and their counters (zeroed when allocated; each launch leaves them zero)
+    dt::DeviceBuffer qkv_ss;   // fused QKV projection: per-row, per-head sums of squares
+    dt::DeviceBuffer qkv_cnt;  // and its group counters (zeroed when allocated; each launch leaves them zero)
+    int qkv_fused = 0;         // DT_OPT_QKV_FUSED
 };
 
 // OlmoAttention on the device (OlmoAttention.h:10-42): weights, forward state kept for backward, gradients.

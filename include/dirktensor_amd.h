@@ -82,6 +82,19 @@ int dt_ctx_create(int device, dt_ctx** out);
 int dt_ctx_destroy(dt_ctx* ctx);
 
 /*
+ * Context options (no reference counterpart).
+ *   DT_OPT_QKV_FUSED  0 (default): dt_attn_layer_fwd (and the model forward)
+ *                     runs the Q/K/V projection as one library GEMM, then the
+ *                     q/k RMSNorm + RoPE kernel; 1: one fused kernel computes
+ *                     the projection, the norms and RoPE (OlmoAttention.cpp:63-88;
+ *                     same results within the mode's tolerance, slower on
+ *                     MI355X at the OLMo-2 shapes).
+ * Returns DT_ERR_INVALID_ARG for an unknown option or value.
+ */
+#define DT_OPT_QKV_FUSED 1
+int dt_ctx_set_option(dt_ctx* ctx, int option, int value);
+
+/*
  * Builds the RoPE sin/cos tables on the host in fp64, casts them to fp32 and
  * uploads them (replaces compute_rope_buffers, OlmoAttention.cpp:18-36).
  * dt_ctx_create already calls it with (DT_ROPE_THETA, DT_MAX_SEQ_LEN).

@@ -59,3 +59,65 @@ def test_load_from_npy_folder(gpu, weights, layer, tmp_path):
     b = layer.forward(x)
     torch.cuda.synchronize()
     assert torch.equal(a, b)
+
+
+@pytest.fixture(scope="module")
+def fused_ctx(gpu):
+    """A context whose layer forwards run the fused projection + q/k norm + RoPE kernel."""
+    from dirktensor_amd import Context
+
+    ctx = Context(0)
+    ctx.set_qkv_fused(True)
+    return ctx
+
+
+@pytest.fixture(scope="module")
+def fused_layer(gpu, weights, fused_ctx):
+    w = weights
+    return OlmoAttention.from_weights(w["wq"], w["wk"], w["wv"], w["wo"], w["q_norm"], w["k_norm"], ctx=fused_ctx)
+
+
+@pytest.mark.parametrize("mode", ["fp32", "bf16"])
+@pytest.mark.parametrize("B,T", [(1, 512), (1, 130), (2, 2048)])
+def test_fused_qkv_projection(gpu, weights, layer, fused_layer, mode, B, T):
+    """The fused projection + q/k norm + RoPE kernel (OlmoAttention.cpp:63-88) against the two-launch path and,
+    at T<=512, the oracle; rows not a multiple of the 128-row tile (T=130) and several tile rounds (B*T=4096);
+    repeated calls are bit-identical (the per-row sums are added in a fixed order)."""
+    x = torch.from_numpy(synth.normal(2301 + T, (B, T, 2048))).to(gpu)
+    a = fused_layer.forward(x, mode=mode)
+    a2 = fused_layer.forward(x, mode=mode)
+    b = layer.forward(x, mode=mode)
+    torch.cuda.synchronize()
+    assert torch.isfinite(a).all()
+    assert torch.equal(a, a2)
+    tol = TOL_FP32 if mode == "fp32" else TOL_BF16
+    err = rel_err(to_np(a), to_np(b))
+    print(f"fused vs two-launch {mode} B={B} T={T}: rel err {err:.3e}")
+    assert err <= tol
+    if B == 1 and T <= 512:
+        w = weights
+        ref = oracle.attention_layer_forward(to_np(x), w["wq"], w["wk"], w["wv"], w["wo"], w["q_norm"], w["k_norm"])
+        err = rel_err(to_np(a), ref)
+        print(f"fused {mode} B={B} T={T}: rel err vs oracle {err:.3e}")
+        assert err <= tol
+
+
+@pytest.mark.parametrize("mode", ["fp32", "bf16"])
+def test_fused_qkv_saved_state_backward(gpu, weights, fused_layer, mode):
+    """The fused forward's saved state (pre-norm q|k, rms, rotated q|k|v) drives the layer backward: d_x and the
+    six weight gradients match the oracle's OlmoAttention::backward (OlmoAttention.cpp:193-312) at T=128."""
+    w = weights
+    x = synth.normal(2401, (1, 128, 2048))
+    g = synth.normal(2402, (1, 128, 2048))
+    fused_layer.zero_grad()
+    fused_layer.forward(torch.from_numpy(x).to(gpu), mode=mode)
+    dx = fused_layer.backward(torch.from_numpy(g).to(gpu))
+    grads = fused_layer.grads()
+    torch.cuda.synchronize()
+    ref_dx, ref_g = oracle.attention_layer_backward(x, w["wq"], w["wk"], w["wv"], w["wo"], w["q_norm"], w["k_norm"], g)
+    tol = TOL_FP32 if mode == "fp32" else TOL_BF16
+    errs = {"dx": rel_err(to_np(dx), ref_dx)}
+    for k in ref_g:
+        errs[k] = rel_err(to_np(grads[k]), ref_g[k])
+    print(f"fused saved state {mode}: " + " ".join(f"{k} {v:.2e}" for k, v in errs.items()))
+    assert max(errs.values()) <= tol
