@@ -243,9 +243,9 @@ def main() -> int:
     ap.add_argument("--cpu-budget", type=float, default=10.0, help="seconds of CPU-baseline timing (0 = skip)")
     ap.add_argument("--no-extras", action="store_true",
                     help="default workload only: skip the fp32 exact-mode and end-to-end prefill figures")
-    ap.add_argument("--qkv", choices=["fused", "gemm"], default="gemm",
-                    help="layer/model forwards: fused QKV projection + q/k norm + RoPE kernel, or the library GEMM "
-                    "followed by the separate norm + RoPE kernel")
+    ap.add_argument("--qkv", choices=["auto", "fused", "gemm"], default="auto",
+                    help="layer/model forwards: fused QKV projection + q/k norm + RoPE kernel, the library GEMM "
+                    "followed by the separate norm + RoPE kernel, or auto (fused where its tiles fit one round)")
     ap.add_argument("--copy-mib", type=int, default=0,
                     help="instead of attention, time a plain copy kernel over this many MiB (counter calibration)")
     args = ap.parse_args()
@@ -266,7 +266,7 @@ def main() -> int:
     dev = torch.device("cuda:0")
     stream = torch.cuda.current_stream(dev)
     ctx = dt.default_context(0)
-    ctx.set_qkv_fused(args.qkv == "fused")
+    ctx.set_qkv_path(args.qkv)
     wl = WORKLOADS[args.workload](args, dev, stream, ctx)
 
     settle = settle_clock(wl["step"], stream)
@@ -306,7 +306,8 @@ def main() -> int:
         "cpu_baseline": cpu,
     }
     if args.workload.startswith(("layer", "model")):
-        line["config"]["qkv_projection"] = "fused kernel" if args.qkv == "fused" else "library GEMM + norm/RoPE kernel"
+        line["config"]["qkv_projection"] = {"fused": "fused kernel", "gemm": "library GEMM + norm/RoPE kernel",
+                                            "auto": "auto (fused kernel when its tiles fit one round)"}[args.qkv]
     if args.workload == "flash_fwd":
         line["attn_core_tok_per_s"] = line["tok_per_s"]  # tokens/s of the attention core alone, not prefill
     if args.workload == "model_fwd":

@@ -26,6 +26,9 @@ DT_MEM_DEVICE = 0
 DT_MEM_HOST = 1
 
 DT_OPT_QKV_FUSED = 1
+DT_QKV_GEMM = 0
+DT_QKV_FUSED = 1
+DT_QKV_AUTO = 2
 
 HEAD_DIM = 128
 MAX_SEQ_LEN = 8192

@@ -57,10 +57,14 @@ class Context:
     def rope_table_init(self, theta: float, max_seq_len: int) -> None:
         C.call("dt_rope_table_init", self.handle, float(theta), int(max_seq_len))
 
-    def set_qkv_fused(self, fused: bool) -> None:
-        """Layer forwards on this context: fused QKV projection + q/k norm + RoPE kernel (True), or one library
-        GEMM followed by the separate norm + RoPE kernel (False, the default)."""
-        C.call("dt_ctx_set_option", self.handle, C.DT_OPT_QKV_FUSED, int(bool(fused)))
+    def set_qkv_path(self, path: str) -> None:
+        """How layer forwards on this context compute the Q/K/V projection with the q/k norms and RoPE: "fused"
+        (one fused kernel), "gemm" (library GEMM, then the norm + RoPE kernel) or "auto" (the default: fused
+        where its tiles fit one round on the device's CUs)."""
+        values = {"gemm": C.DT_QKV_GEMM, "fused": C.DT_QKV_FUSED, "auto": C.DT_QKV_AUTO}
+        if path not in values:
+            raise ValueError(f"unknown QKV path {path!r}: expected one of {sorted(values)}")
+        C.call("dt_ctx_set_option", self.handle, C.DT_OPT_QKV_FUSED, values[path])
 
 
 _default_ctx: dict = {}

@@ -131,18 +131,19 @@ static int run_flash(dt_ctx* ctx, const FlashArgs& fa_in, const int32_t* seq_len
     return launch_flash_fwd_bf16(fa, lp, s);
 }
 
-// The fused projection + norm + RoPE launch with the context's workspace (counters start zero).
+// The fused projection + norm + RoPE launch with the context's workspace (zeroed when allocated, so no
+// entry carries a live epoch) and the next epoch (never 0).
 static int run_qkv_fused(dt_ctx* ctx, QkvArgs qa, int f32, hipStream_t s) {
-    size_t ss_bytes = 0, cnt_bytes = 0;
-    DT_TRY(qkv_norm_rope_workspace(qa.rows, qa.H, &ss_bytes, &cnt_bytes));
-    if (ctx->qkv_cnt.bytes < cnt_bytes) {
-        DT_TRY(ctx->qkv_cnt.ensure(cnt_bytes));
-        DT_HIP_TRY(hipMemsetAsync(ctx->qkv_cnt.ptr, 0, ctx->qkv_cnt.bytes, s));
+    size_t ss_bytes = 0;
+    DT_TRY(qkv_norm_rope_workspace(qa.rows, qa.H, &ss_bytes));
+    if (ctx->qkv_ss.bytes < ss_bytes) {
+        DT_TRY(ctx->qkv_ss.ensure(ss_bytes));
+        DT_HIP_TRY(hipMemsetAsync(ctx->qkv_ss.ptr, 0, ctx->qkv_ss.bytes, s));
     }
-    DT_TRY(ctx->qkv_ss.ensure(ss_bytes));
-    qa.ss = static_cast<float*>(ctx->qkv_ss.ptr);
+    if (++ctx->qkv_epoch == 0) ctx->qkv_epoch = 1;
+    qa.ss = static_cast<uint64_t*>(ctx->qkv_ss.ptr);
     qa.ss_bytes = (int64_t)ctx->qkv_ss.bytes;
-    qa.cnt = static_cast<int*>(ctx->qkv_cnt.ptr);
+    qa.epoch = ctx->qkv_epoch;
     return launch_qkv_norm_rope(qa, f32, s);
 }
 
@@ -381,7 +382,9 @@ int dt_ctx_set_option(dt_ctx* ctx, int option, int value) {
     clear_error();
     if (!ctx) return set_error(DT_ERR_INVALID_ARG, "ctx is NULL");
     if (option == DT_OPT_QKV_FUSED) {
-        if (value != 0 && value != 1) return set_error(DT_ERR_INVALID_ARG, "DT_OPT_QKV_FUSED takes 0 or 1, not %d", value);
+        if (value != DT_QKV_GEMM && value != DT_QKV_FUSED && value != DT_QKV_AUTO)
+            return set_error(DT_ERR_INVALID_ARG, "DT_OPT_QKV_FUSED takes DT_QKV_GEMM, DT_QKV_FUSED or DT_QKV_AUTO, not %d",
+                             value);
         ctx->qkv_fused = value;
         return DT_OK;
     }
@@ -399,7 +402,6 @@ int dt_ctx_destroy(dt_ctx* ctx) {
     ctx->fwd_split.release();
     ctx->fwd_split_cnt.release();
     ctx->qkv_ss.release();
-    ctx->qkv_cnt.release();
     if (ctx->blas) rocblas_destroy_handle(static_cast<rocblas_handle>(ctx->blas));
     if (ctx->lt) {
         LtCache* lc = static_cast<LtCache*>(ctx->lt);
@@ -739,6 +741,8 @@ int dt_attn_layer_fwd(dt_attn_layer* L, const float* x, float* out, int B, int T
         DT_TRY(ctx->stage[1].ensure(act * 4));
         od = static_cast<float*>(ctx->stage[1].ptr);
     }
+    bool fused = ctx->qkv_fused == DT_QKV_FUSED && H % 4 == 0;  // (the fused kernel needs H % 4 == 0)
+    if (ctx->qkv_fused == DT_QKV_AUTO) DT_TRY(qkv_fused_one_round(rows, H, &fused));
     float* rms = save_for_backward ? static_cast<float*>(L->rms.ptr) : nullptr;
     float* st_m = save_for_backward ? static_cast<float*>(L->stats.ptr) : nullptr;
     float* st_l = save_for_backward ? st_m + (size_t)rows * H : nullptr;
@@ -756,10 +760,10 @@ int dt_attn_layer_fwd(dt_attn_layer* L, const float* x, float* out, int B, int T
             DT_TRY(L->att32.ensure(act * 3 * 4));
             att = static_cast<float*>(L->att32.ptr);
         }
-        if (ctx->qkv_fused && H % 4 == 0) {  // (the fused kernel needs H % 4 == 0)
+        if (fused) {
             // x [Wq;Wk;Wv]^T, q/k norm and RoPE in one kernel (OlmoAttention.cpp:63-88)
             QkvArgs qa{xd, L->w_qkv, L->q_norm, L->k_norm, att, save_for_backward ? qkv : nullptr, rms,
-                       ctx->rope_cos, ctx->rope_sin, nullptr, 0, nullptr, rows, T, H, dm, 3 * dm, 3 * dm, DT_RMS_EPS};
+                       ctx->rope_cos, ctx->rope_sin, nullptr, 0, 0, rows, T, H, dm, 3 * dm, 3 * dm, DT_RMS_EPS};
             DT_TRY(run_qkv_fused(ctx, qa, 1, s));
         } else {
             // Q|K|V = x [Wq;Wk;Wv]^T in one N = 3*d_model GEMM (OlmoAttention.cpp:68,74,80)
@@ -794,11 +798,11 @@ int dt_attn_layer_fwd(dt_attn_layer* L, const float* x, float* out, int B, int T
         uint16_t* qkv16 = static_cast<uint16_t*>(L->qkv16.ptr);
         uint16_t* attn16 = static_cast<uint16_t*>(L->attn.ptr);
         DT_TRY(launch_f32_to_bf16(xd, x16, (int64_t)act, s));
-        if (ctx->qkv_fused && H % 4 == 0) {  // (the fused kernel needs H % 4 == 0)
+        if (fused) {
             // x [Wq;Wk;Wv]^T, q/k norm and RoPE in one kernel (OlmoAttention.cpp:63-88); the pre-norm q|k rows
             // (bf16) only when the norms' backward will read them
             QkvArgs qa{x16, L->w_qkv16, L->q_norm, L->k_norm, qkv16, save_for_backward ? pre16 : nullptr, rms,
-                       ctx->rope_cos, ctx->rope_sin, nullptr, 0, nullptr, rows, T, H, dm, 3 * dm, 3 * dm, DT_RMS_EPS};
+                       ctx->rope_cos, ctx->rope_sin, nullptr, 0, 0, rows, T, H, dm, 3 * dm, 3 * dm, DT_RMS_EPS};
             DT_TRY(run_qkv_fused(ctx, qa, 0, s));
         } else {
             // the projections leave the GEMM as bf16 (fp32 accumulation, one rounding): the norm kernel reads

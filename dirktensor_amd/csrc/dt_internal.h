@@ -126,15 +126,17 @@ struct QkvArgs {
     float* rms;   // nullable: [2][rows], q then k
     const float* rope_cos;  // [>= T][64]
     const float* rope_sin;
-    float* ss;         // workspace: per-row, per-head partial sums of squares
+    uint64_t* ss;      // workspace: per-row, per-head partial sums of squares, tagged with the epoch
     int64_t ss_bytes;  // its size (qkv_norm_rope_workspace)
-    int* cnt;          // workspace: group counters, zero between launches
+    uint32_t epoch;    // nonzero, different from the previous launch's on the same workspace
     int rows, T, H;
     int ldx, ld_out, ld_pre;  // elements
     float eps;
 };
-int qkv_norm_rope_workspace(int rows, int H, size_t* ss_bytes, size_t* cnt_bytes);
+int qkv_norm_rope_workspace(int rows, int H, size_t* ss_bytes);
 int launch_qkv_norm_rope(const QkvArgs& a, int f32, hipStream_t stream);
+// the fused kernel's tiles for rows x (3 H heads) fit one round on this device's CUs
+int qkv_fused_one_round(int rows, int H, bool* fits);
 
 // Backward of the fused q/k RMSNorm + RoPE (OlmoAttention.cpp:234-244): dq/dk rows are rewritten in place
 // from d(rope output) to d(pre-norm projection); the norm-weight gradients are accumulated (+=).
@@ -196,9 +198,9 @@ struct dt_ctx {
     dt::DeviceBuffer lt_ws;      // hipBLASLt workspace (split-K partial sums)
     dt::DeviceBuffer fwd_split;  // attention forward: partial results of items split across workgroups
     dt::DeviceBuffer fwd_split_cnt;  // and their counters (zeroed when allocated; each launch leaves them zero)
-    dt::DeviceBuffer qkv_ss;   // fused QKV projection: per-row, per-head sums of squares
-    dt::DeviceBuffer qkv_cnt;  // and its group counters (zeroed when allocated; each launch leaves them zero)
-    int qkv_fused = 0;         // DT_OPT_QKV_FUSED
+    dt::DeviceBuffer qkv_ss;   // fused QKV projection: per-row, per-head sums of squares (zeroed when allocated)
+    uint32_t qkv_epoch = 0;    // the tag of its last launch
+    int qkv_fused = DT_QKV_AUTO;  // DT_OPT_QKV_FUSED
 };
 
 // OlmoAttention on the device (OlmoAttention.h:10-42): weights, forward state kept for backward, gradients.

@@ -27,14 +27,14 @@
 // their rotate-half partners (d, d+64) of one row. A q or k tile computes its rows' sums of squares
 // over the head's 128 columns and publishes them; the H tiles of the same row block and tensor run in
 // the same round on different workgroups (the grid is at most one workgroup per CU, so every workgroup is
-// resident at once), wait for each other at a counter, and each then adds the H partial sums of its rows
-// in head order:
+// resident at once). Each published sum is one 64-bit word tagged with the launch's epoch (a number the
+// host changes every launch), so a reader polls the H words of its row until all carry this epoch: no
+// counters, no fences. The row's sum is then added in a fixed order and
 // rms = sqrt(sum / d_model + eps), y = (x / rms) * w, out[d] = y[d] cos - y[d+64] sin,
-// out[d+64] = y[d+64] cos + y[d] sin, the reference's rounding order. The partial sums are written and
-// read with device-scope coherent accesses (they cross XCDs); the counters return to zero before the
-// kernel ends. A wait that does not end within a bounded spin (about a second: a workgroup kept from its
-// CU that long, e.g. by another persistent kernel occupying CUs) gives up and writes NaN rows instead of
-// hanging.
+// out[d+64] = y[d+64] cos + y[d] sin, the reference's rounding order. The words are written and read with
+// device-scope coherent accesses (they cross XCDs). A wait that does not end within a bounded spin (about
+// a second: a workgroup kept from its CU that long, e.g. by another persistent kernel occupying CUs)
+// gives up and writes NaN rows instead of hanging.
 
 #include "dt_internal.h"
 
@@ -49,6 +49,7 @@ typedef float floatx4 __attribute__((ext_vector_type(4)));
 typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
 typedef __bf16 bf16x2 __attribute__((ext_vector_type(2)));
 typedef float floatx2 __attribute__((ext_vector_type(2)));
+typedef unsigned v2u32 __attribute__((ext_vector_type(2)));
 
 constexpr int kTile = 128;               // rows and columns of a work tile
 constexpr int kThreads = 512;            // 8 waves
@@ -59,7 +60,7 @@ constexpr int kLdsBytes = 2 * kTile * kRStride * 4;  // two fp32 tiles; holds 2 
 static_assert(kLdsBytes >= 8 * kOpBytes, "the epilogue tiles must cover the stages");
 constexpr int kBufferDword3 = 0x00020000;  // raw buffer, 32-bit data format (gfx9 family)
 constexpr int kCoherent = 16;              // cache policy sc1: device-scope coherent access
-constexpr int kSpinLimit = 1 << 20;        // polls (each a coherent load and s_sleep 1, ~1 s in all) before a group wait gives up
+constexpr int kSpinLimit = 1 << 20;        // polls (coherent loads and s_sleep 1, ~1 s in all) before a wait gives up
 
 __device__ __forceinline__ uint32_t pack_bf16x2(float lo, float hi) {
     bf16x2 r = __builtin_convertvector((floatx2){lo, hi}, bf16x2);
@@ -152,7 +153,6 @@ __device__ __forceinline__ void store4(void* base, int64_t idx, float4 v) {  // 
 template <bool kF32>
 __global__ __launch_bounds__(kThreads, 1) void qkv_norm_rope_kernel(QkvArgs a) {
     __shared__ __attribute__((aligned(1024))) uint8_t lds[kLdsBytes];
-    __shared__ int timed_out;
     constexpr int es = kF32 ? 4 : 2;  // bytes per element of x, W and the outputs
 
     const int tid = threadIdx.x;
@@ -288,45 +288,49 @@ __global__ __launch_bounds__(kThreads, 1) void qkv_norm_rope_kernel(QkvArgs a) {
             }
             ss += __shfl_xor(ss, 1, 64);
             ss += __shfl_xor(ss, 2, 64);
-            // this head's sum of squares of row grow -> ss[grow][which][head]
-            const uint32_t srow = (uint32_t)((grow * 2 + which) * H) * 4u;
-            if (qd == 0 && valid)
-                __builtin_amdgcn_raw_buffer_store_b32(__builtin_bit_cast(uint32_t, ss), rss, srow + 4u * head, 0,
+            // this head's sum of squares of row grow -> ss[grow][which][head], as one 64-bit word tagged with the
+            // launch's epoch (the word is written whole, so a reader sees the old entry or the new one)
+            const uint32_t srow = (uint32_t)((grow * 2 + which) * H) * 8u;
+            if (qd == 0 && valid) {
+                const uint64_t word = ((uint64_t)a.epoch << 32) | __builtin_bit_cast(uint32_t, ss);
+                __builtin_amdgcn_raw_buffer_store_b64(__builtin_bit_cast(v2u32, word), rss, srow + 8u * head, 0,
                                                       kCoherent);
-            // wait for the other H - 1 tiles of this row block and tensor (same round, other workgroups)
-            asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
-            __syncthreads();
-            if (tid == 0) {
-                int* arrive = a.cnt + 2 * (2 * rb + which);
-                int* depart = arrive + 1;
-                __hip_atomic_fetch_add(arrive, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-                int spins = 0, to = 0;
-                while (__hip_atomic_load(arrive, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) < H) {
-                    __builtin_amdgcn_s_sleep(1);
-                    if (++spins >= kSpinLimit) {
-                        to = 1;
+            }
+            if (valid) {
+                // the other H - 1 tiles of this row block and tensor run in the same round on other workgroups:
+                // thread qd polls heads 4qd .. 4qd+3 of its row until all four carry this launch's epoch
+                float part = 0.0f;
+                bool ok = false;
+                for (int spins = 0; spins < kSpinLimit; ++spins) {
+                    bool all = true;
+                    float sum = 0.0f;
+                    for (int h = 4 * qd; h < H; h += 16) {  // heads 4qd + 16j .. +3: each head once (H % 4 == 0)
+                        // (the loaded vectors are bit-cast whole: extracting elements 0 and 2 of the builtin's
+                        // result directly makes this compiler narrow the load to one dword and read it twice)
+                        const uint4 p0 = __builtin_bit_cast(
+                            uint4, __builtin_amdgcn_raw_buffer_load_b128(rss, srow + 8u * h, 0, kCoherent));
+                        const uint4 p1 = __builtin_bit_cast(
+                            uint4, __builtin_amdgcn_raw_buffer_load_b128(rss, srow + 8u * h + 16u, 0, kCoherent));
+                        all = all && p0.y == a.epoch && p0.w == a.epoch && p1.y == a.epoch && p1.w == a.epoch;
+                        sum += __builtin_bit_cast(float, p0.x);
+                        sum += __builtin_bit_cast(float, p0.z);
+                        sum += __builtin_bit_cast(float, p1.x);
+                        sum += __builtin_bit_cast(float, p1.z);
+                    }
+                    if (all) {
+                        part = sum;
+                        ok = true;
                         break;
                     }
+                    __builtin_amdgcn_s_sleep(1);
                 }
-                // every member has seen the full count before the last one to leave resets the pair
-                if (!to && __hip_atomic_fetch_add(depart, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) == H - 1) {
-                    __hip_atomic_store(arrive, 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-                    __hip_atomic_store(depart, 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-                }
-                timed_out = to;
-            }
-            __syncthreads();
-            if (valid) {
-                float tot = 0.0f;
-                for (int h4 = 0; h4 < H; h4 += 4) {  // head order, 4 sums per coherent load (H % 4 == 0)
-                    const float4 p = __builtin_bit_cast(
-                        float4, __builtin_amdgcn_raw_buffer_load_b128(rss, srow + 4u * h4, 0, kCoherent));
-                    tot += p.x;
-                    tot += p.y;
-                    tot += p.z;
-                    tot += p.w;
-                }
-                const float rms = timed_out ? __builtin_nanf("") : sqrtf(tot / (float)dm + a.eps);
+                // the row's total, added in the same order by its four threads: (q0 + q1) + (q2 + q3)
+                part += __shfl_xor(part, 1, 64);
+                part += __shfl_xor(part, 2, 64);
+                const bool all_ok =
+                    __shfl_xor((int)ok, 1, 64) & __shfl_xor((int)ok, 2, 64) & __shfl_xor((int)ok, 3, 64) & (int)ok;
+                const float tot = part;
+                const float rms = all_ok ? sqrtf(tot / (float)dm + a.eps) : __builtin_nanf("");
                 if (a.rms && qd == 0) a.rms[(int64_t)which * a.rows + grow] = rms;
                 const int t = (int)(grow % a.T);
                 const float* cs = a.rope_cos + (int64_t)t * 64 + 16 * qd;
@@ -361,10 +365,17 @@ __global__ __launch_bounds__(kThreads, 1) void qkv_norm_rope_kernel(QkvArgs a) {
 
 }  // namespace
 
-int qkv_norm_rope_workspace(int rows, int H, size_t* ss_bytes, size_t* cnt_bytes) {
+int qkv_norm_rope_workspace(int rows, int H, size_t* ss_bytes) {
     const int64_t n_rb = ((int64_t)rows + kTile - 1) / kTile;
-    *ss_bytes = (size_t)(n_rb * kTile) * 2 * H * sizeof(float);
-    *cnt_bytes = (size_t)n_rb * 4 * sizeof(int);
+    *ss_bytes = (size_t)(n_rb * kTile) * 2 * H * sizeof(uint64_t);
+    return DT_OK;
+}
+
+int qkv_fused_one_round(int rows, int H, bool* fits) {
+    int cus = 0;
+    DT_TRY(persistent_grid(0x7fffffff, &cus));
+    const int64_t n_tiles = ((int64_t)rows + kTile - 1) / kTile * 3 * H;
+    *fits = H >= 4 && H % 4 == 0 && n_tiles <= (cus / H) * (int64_t)H;
     return DT_OK;
 }
 
@@ -377,8 +388,9 @@ int launch_qkv_norm_rope(const QkvArgs& a, int f32, hipStream_t stream) {
         return set_error(DT_ERR_INVALID_ARG, "fused QKV: row strides below the row width");
     if ((int64_t)kTile * a.ldx * es >= ((int64_t)1 << 31) || (int64_t)kTile * dm * es >= ((int64_t)1 << 31))
         return set_error(DT_ERR_UNSUPPORTED, "fused QKV: a 128-row band exceeds 2 GiB");
-    size_t ssb = 0, cb = 0;
-    DT_TRY(qkv_norm_rope_workspace(a.rows, a.H, &ssb, &cb));
+    if (a.epoch == 0) return set_error(DT_ERR_INVALID_ARG, "fused QKV: epoch 0 is reserved");
+    size_t ssb = 0;
+    DT_TRY(qkv_norm_rope_workspace(a.rows, a.H, &ssb));
     if (ssb >= ((size_t)1 << 31) || a.ss_bytes < (int64_t)ssb)
         return set_error(DT_ERR_UNSUPPORTED, "fused QKV: partial-sum workspace too small or above 2 GiB");
     int cus = 0;

@@ -83,15 +83,23 @@ int dt_ctx_destroy(dt_ctx* ctx);
 
 /*
  * Context options (no reference counterpart).
- *   DT_OPT_QKV_FUSED  0 (default): dt_attn_layer_fwd (and the model forward)
- *                     runs the Q/K/V projection as one library GEMM, then the
- *                     q/k RMSNorm + RoPE kernel; 1: one fused kernel computes
- *                     the projection, the norms and RoPE (OlmoAttention.cpp:63-88;
- *                     same results within the mode's tolerance, slower on
- *                     MI355X at the OLMo-2 shapes).
+ *   DT_OPT_QKV_FUSED  how dt_attn_layer_fwd (and the model forward) computes
+ *                     the Q/K/V projection, the q/k RMSNorm and RoPE
+ *                     (OlmoAttention.cpp:63-88):
+ *                     DT_QKV_GEMM  one library GEMM, then a norm + RoPE kernel;
+ *                     DT_QKV_FUSED one fused kernel (same results within the
+ *                                  mode's tolerance);
+ *                     DT_QKV_AUTO  (default) the fused kernel when its 128-row x
+ *                                  one-head tiles fit one round on the GPU's
+ *                                  CUs (B*T <= 640 at 16 heads on MI355X),
+ *                                  where it measured faster; the GEMM path
+ *                                  above that.
  * Returns DT_ERR_INVALID_ARG for an unknown option or value.
  */
 #define DT_OPT_QKV_FUSED 1
+#define DT_QKV_GEMM 0
+#define DT_QKV_FUSED 1
+#define DT_QKV_AUTO 2
 int dt_ctx_set_option(dt_ctx* ctx, int option, int value);
 
 /*

@@ -183,3 +183,10 @@ def test_bench_refuses_multi_gpu():
     r = subprocess.run([sys.executable, os.path.join(ROOT, "bench.py"), "--gpus", "2"], capture_output=True,
                        text=True, timeout=120)
     assert r.returncode == 2 and "one GPU" in r.stderr
+
+
+def test_ctx_option_validation():
+    """dt_ctx_set_option rejects a NULL context before touching it (no GPU needed)."""
+    lib = C.lib()
+    assert lib.dt_ctx_set_option(None, C.DT_OPT_QKV_FUSED, C.DT_QKV_AUTO) == C.DT_ERR_INVALID_ARG
+    assert "ctx is NULL" in last_error()

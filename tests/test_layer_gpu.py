@@ -67,7 +67,7 @@ def fused_ctx(gpu):
     from dirktensor_amd import Context
 
     ctx = Context(0)
-    ctx.set_qkv_fused(True)
+    ctx.set_qkv_path("fused")
     return ctx
 
 
@@ -77,22 +77,33 @@ def fused_layer(gpu, weights, fused_ctx):
     return OlmoAttention.from_weights(w["wq"], w["wk"], w["wv"], w["wo"], w["q_norm"], w["k_norm"], ctx=fused_ctx)
 
 
+@pytest.fixture(scope="module")
+def gemm_layer(gpu, weights):
+    """The same weights on a context whose layer forwards run the library QKV GEMM + the norm/RoPE kernel."""
+    from dirktensor_amd import Context
+
+    ctx = Context(0)
+    ctx.set_qkv_path("gemm")
+    w = weights
+    return OlmoAttention.from_weights(w["wq"], w["wk"], w["wv"], w["wo"], w["q_norm"], w["k_norm"], ctx=ctx)
+
+
 @pytest.mark.parametrize("mode", ["fp32", "bf16"])
 @pytest.mark.parametrize("B,T", [(1, 512), (1, 130), (2, 2048)])
-def test_fused_qkv_projection(gpu, weights, layer, fused_layer, mode, B, T):
-    """The fused projection + q/k norm + RoPE kernel (OlmoAttention.cpp:63-88) against the two-launch path and,
+def test_fused_qkv_projection(gpu, weights, gemm_layer, fused_layer, mode, B, T):
+    """The fused projection + q/k norm + RoPE kernel (OlmoAttention.cpp:63-88) against the GEMM path and,
     at T<=512, the oracle; rows not a multiple of the 128-row tile (T=130) and several tile rounds (B*T=4096);
     repeated calls are bit-identical (the per-row sums are added in a fixed order)."""
     x = torch.from_numpy(synth.normal(2301 + T, (B, T, 2048))).to(gpu)
     a = fused_layer.forward(x, mode=mode)
     a2 = fused_layer.forward(x, mode=mode)
-    b = layer.forward(x, mode=mode)
+    b = gemm_layer.forward(x, mode=mode)
     torch.cuda.synchronize()
     assert torch.isfinite(a).all()
     assert torch.equal(a, a2)
     tol = TOL_FP32 if mode == "fp32" else TOL_BF16
     err = rel_err(to_np(a), to_np(b))
-    print(f"fused vs two-launch {mode} B={B} T={T}: rel err {err:.3e}")
+    print(f"fused vs GEMM path {mode} B={B} T={T}: rel err {err:.3e}")
     assert err <= tol
     if B == 1 and T <= 512:
         w = weights
