@@ -246,6 +246,8 @@ def main() -> int:
     ap.add_argument("--qkv", choices=["auto", "fused", "gemm"], default="auto",
                     help="layer/model forwards: fused QKV projection + q/k norm + RoPE kernel, the library GEMM "
                     "followed by the separate norm + RoPE kernel, or auto (fused where its tiles fit one round)")
+    ap.add_argument("--gemm-tune", type=int, choices=[0, 1], default=1,
+                    help="bf16 GEMMs: time hipBLASLt's heuristic candidates once per shape (1) or take its first choice (0)")
     ap.add_argument("--copy-mib", type=int, default=0,
                     help="instead of attention, time a plain copy kernel over this many MiB (counter calibration)")
     args = ap.parse_args()
@@ -267,6 +269,7 @@ def main() -> int:
     stream = torch.cuda.current_stream(dev)
     ctx = dt.default_context(0)
     ctx.set_qkv_path(args.qkv)
+    ctx.set_gemm_tune(bool(args.gemm_tune))
     wl = WORKLOADS[args.workload](args, dev, stream, ctx)
 
     settle = settle_clock(wl["step"], stream)
@@ -306,6 +309,7 @@ def main() -> int:
         "cpu_baseline": cpu,
     }
     if args.workload.startswith(("layer", "model")):
+        line["config"]["gemm_choice"] = "tuned hipBLASLt candidates" if args.gemm_tune else "first hipBLASLt heuristic"
         line["config"]["qkv_projection"] = {"fused": "fused kernel", "gemm": "library GEMM + norm/RoPE kernel",
                                             "auto": "auto (fused kernel when its tiles fit one round)"}[args.qkv]
     if args.workload == "flash_fwd":

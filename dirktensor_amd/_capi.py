@@ -29,6 +29,7 @@ DT_OPT_QKV_FUSED = 1
 DT_QKV_GEMM = 0
 DT_QKV_FUSED = 1
 DT_QKV_AUTO = 2
+DT_OPT_GEMM_TUNE = 2
 
 HEAD_DIM = 128
 MAX_SEQ_LEN = 8192

@@ -66,6 +66,11 @@ class Context:
             raise ValueError(f"unknown QKV path {path!r}: expected one of {sorted(values)}")
         C.call("dt_ctx_set_option", self.handle, C.DT_OPT_QKV_FUSED, values[path])
 
+    def set_gemm_tune(self, tune: bool) -> None:
+        """bf16 GEMMs of a new shape: time hipBLASLt's heuristic candidates once and keep the fastest reproducible
+        one (True, the default), or take its first heuristic choice (False)."""
+        C.call("dt_ctx_set_option", self.handle, C.DT_OPT_GEMM_TUNE, int(bool(tune)))
+
 
 _default_ctx: dict = {}
 

@@ -168,6 +168,7 @@ static int ensure_blas(dt_ctx* ctx) {
 // once per shape and kept in the context.
 namespace {
 constexpr size_t kLtWorkspace = size_t(128) << 20;
+constexpr int kLtCandidates = 16;  // heuristic candidates timed for a new shape
 struct LtPlan {
     hipblasLtMatmulDesc_t desc = nullptr;
     hipblasLtMatrixLayout_t la = nullptr, lb = nullptr, lc = nullptr;
@@ -177,6 +178,15 @@ struct LtCache {
     hipblasLtHandle_t h = nullptr;
     std::map<std::array<int, 10>, LtPlan> plans;
 };
+// an order-independent 64-bit fingerprint of n words: sum of w_i * (odd multiplier of i), modulo 2^64 (integer
+// additions commute, so the atomics leave the same value whatever order the blocks finish in)
+__global__ void words_fingerprint_kernel(const uint32_t* p, int64_t n, unsigned long long* out) {
+    unsigned long long acc = 0;
+    for (int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; i < n; i += (int64_t)gridDim.x * blockDim.x)
+        acc += (unsigned long long)p[i] * ((unsigned long long)i * 0x9E3779B97F4A7C15ull | 1ull);
+    atomicAdd(out, acc);
+}
+
 void lt_free(LtPlan& p) {
     if (p.la) hipblasLtMatrixLayoutDestroy(p.la);
     if (p.lb) hipblasLtMatrixLayoutDestroy(p.lb);
@@ -184,6 +194,72 @@ void lt_free(LtPlan& p) {
     if (p.desc) hipblasLtMatmulDescDestroy(p.desc);
 }
 }  // namespace
+
+// One-time choice among hipBLASLt's heuristic candidates for a shape: each candidate runs once into a scratch
+// output (beta 0, so an accumulating caller's C is not touched), then three times under events; a candidate whose
+// second run does not reproduce the first bit for bit (a split-K reduction by atomics) is dropped, and the
+// fastest remaining one replaces the first heuristic choice. Synchronises the stream once per new shape.
+static int lt_tune(dt_ctx* ctx, hipStream_t s, hipblasLtHandle_t h, LtPlan& p,
+                   const hipblasLtMatmulHeuristicResult_t* heur, int n, int M, int N, int K, const void* A,
+                   const void* B, int ldc, bool c_bf16) {
+    (void)N;
+    (void)K;
+    DT_TRY(ctx->lt_ws.ensure(kLtWorkspace));
+    const size_t words = (size_t)ldc * M * (c_bf16 ? 2 : 4) / 4;
+    void* scratch = nullptr;
+    unsigned long long* fp = nullptr;
+    hipEvent_t e0 = nullptr, e1 = nullptr;
+    if (hipMalloc(&scratch, words * 4) != hipSuccess || hipMalloc(&fp, 2 * sizeof(unsigned long long)) != hipSuccess ||
+        hipEventCreate(&e0) != hipSuccess || hipEventCreate(&e1) != hipSuccess) {
+        (void)hipGetLastError();  // no room to tune: keep the first heuristic choice
+        if (scratch) (void)hipFree(scratch);
+        if (fp) (void)hipFree(fp);
+        if (e0) (void)hipEventDestroy(e0);
+        if (e1) (void)hipEventDestroy(e1);
+        return DT_OK;
+    }
+    const float one = 1.0f, zero = 0.0f;
+    float best = -1.0f;
+    hipblasLtMatmulAlgo_t best_algo = heur[0].algo;
+    auto run = [&](const hipblasLtMatmulAlgo_t& algo) {
+        return hipblasLtMatmul(h, p.desc, &one, B, p.la, A, p.lb, &zero, scratch, p.lc, scratch, p.lc, &algo,
+                               ctx->lt_ws.ptr, kLtWorkspace, s) == HIPBLAS_STATUS_SUCCESS;
+    };
+    const int64_t nw = (int64_t)words;
+    const unsigned blocks = (unsigned)std::min<int64_t>((nw + 255) / 256, 4096);
+    for (int i = 0; i < n; ++i) {
+        if (hipMemsetAsync(fp, 0, 2 * sizeof(unsigned long long), s) != hipSuccess) break;
+        if (!run(heur[i].algo)) continue;
+        hipLaunchKernelGGL(words_fingerprint_kernel, dim3(blocks), dim3(256), 0, s, static_cast<const uint32_t*>(scratch),
+                           nw, fp);
+        bool ok = run(heur[i].algo);
+        hipLaunchKernelGGL(words_fingerprint_kernel, dim3(blocks), dim3(256), 0, s, static_cast<const uint32_t*>(scratch),
+                           nw, fp + 1);
+        ok = ok && hipEventRecord(e0, s) == hipSuccess;
+        for (int r = 0; r < 3 && ok; ++r) ok = run(heur[i].algo);
+        ok = ok && hipEventRecord(e1, s) == hipSuccess && hipEventSynchronize(e1) == hipSuccess;
+        unsigned long long f[2] = {0, 1};
+        ok = ok && hipMemcpy(f, fp, sizeof(f), hipMemcpyDeviceToHost) == hipSuccess;
+        float ms = 0.0f;
+        ok = ok && hipEventElapsedTime(&ms, e0, e1) == hipSuccess;
+        if (!ok) {
+            (void)hipGetLastError();
+            continue;
+        }
+        if (f[0] != f[1]) continue;  // not reproducible run to run
+        if (best < 0.0f || ms < best) {
+            best = ms;
+            best_algo = heur[i].algo;
+        }
+    }
+    (void)hipStreamSynchronize(s);
+    (void)hipFree(scratch);
+    (void)hipFree(fp);
+    (void)hipEventDestroy(e0);
+    (void)hipEventDestroy(e1);
+    p.algo = best_algo;
+    return DT_OK;
+}
 
 // Row-major C[M][N] = op(A) op(B) + beta C with bf16 A, B and fp32 C (bf16 C when c_bf16) through hipBLASLt
 // (the same column-major mapping as gemm_rm below). Returns 1 (no error set) when hipBLASLt offers no
@@ -215,22 +291,23 @@ static int gemm_lt(dt_ctx* ctx, hipStream_t s, bool ta, bool tb, int M, int N, i
                   hipblasLtMatrixLayoutCreate(&p.lc, c_bf16 ? HIP_R_16BF : HIP_R_32F, N, M, ldc) ==
                       HIPBLAS_STATUS_SUCCESS;
         int n = 0;
-        hipblasLtMatmulHeuristicResult_t heur{};
+        hipblasLtMatmulHeuristicResult_t heur[kLtCandidates]{};
         if (ok) {
             hipblasLtMatmulPreference_t pref = nullptr;
             size_t wsz = kLtWorkspace;
             ok = hipblasLtMatmulPreferenceCreate(&pref) == HIPBLAS_STATUS_SUCCESS &&
                  hipblasLtMatmulPreferenceSetAttribute(pref, HIPBLASLT_MATMUL_PREF_MAX_WORKSPACE_BYTES, &wsz,
                                                        sizeof(wsz)) == HIPBLAS_STATUS_SUCCESS &&
-                 hipblasLtMatmulAlgoGetHeuristic(lc->h, p.desc, p.la, p.lb, p.lc, p.lc, pref, 1, &heur, &n) ==
-                     HIPBLAS_STATUS_SUCCESS;
+                 hipblasLtMatmulAlgoGetHeuristic(lc->h, p.desc, p.la, p.lb, p.lc, p.lc, pref,
+                                                 ctx->gemm_tune ? kLtCandidates : 1, heur, &n) == HIPBLAS_STATUS_SUCCESS;
             if (pref) hipblasLtMatmulPreferenceDestroy(pref);
         }
         if (!ok || n < 1) {
             lt_free(p);
             return 1;
         }
-        p.algo = heur.algo;
+        p.algo = heur[0].algo;
+        if (n > 1) DT_TRY(lt_tune(ctx, s, lc->h, p, heur, n, M, N, K, A, B, ldc, c_bf16));
         it = lc->plans.emplace(key, p).first;
     }
     DT_TRY(ctx->lt_ws.ensure(kLtWorkspace));
@@ -386,6 +463,11 @@ int dt_ctx_set_option(dt_ctx* ctx, int option, int value) {
             return set_error(DT_ERR_INVALID_ARG, "DT_OPT_QKV_FUSED takes DT_QKV_GEMM, DT_QKV_FUSED or DT_QKV_AUTO, not %d",
                              value);
         ctx->qkv_fused = value;
+        return DT_OK;
+    }
+    if (option == DT_OPT_GEMM_TUNE) {
+        if (value != 0 && value != 1) return set_error(DT_ERR_INVALID_ARG, "DT_OPT_GEMM_TUNE takes 0 or 1, not %d", value);
+        ctx->gemm_tune = value;
         return DT_OK;
     }
     return set_error(DT_ERR_INVALID_ARG, "unknown context option %d", option);

@@ -201,6 +201,7 @@ struct dt_ctx {
     dt::DeviceBuffer qkv_ss;   // fused QKV projection: per-row, per-head sums of squares (zeroed when allocated)
     uint32_t qkv_epoch = 0;    // the tag of its last launch
     int qkv_fused = DT_QKV_AUTO;  // DT_OPT_QKV_FUSED
+    int gemm_tune = 1;            // DT_OPT_GEMM_TUNE
 };
 
 // OlmoAttention on the device (OlmoAttention.h:10-42): weights, forward state kept for backward, gradients.

@@ -94,9 +94,15 @@ int dt_ctx_destroy(dt_ctx* ctx);
  *                                  CUs (B*T <= 640 at 16 heads on MI355X),
  *                                  where it measured faster; the GEMM path
  *                                  above that.
+ *   DT_OPT_GEMM_TUNE  1 (default): the first bf16 GEMM of each new shape on
+ *                     this context times hipBLASLt's heuristic candidates
+ *                     (up to 16, into a scratch output; synchronises the
+ *                     stream once) and keeps the fastest whose repeated run
+ *                     is bit-identical; 0: the first heuristic choice.
  * Returns DT_ERR_INVALID_ARG for an unknown option or value.
  */
 #define DT_OPT_QKV_FUSED 1
+#define DT_OPT_GEMM_TUNE 2
 #define DT_QKV_GEMM 0
 #define DT_QKV_FUSED 1
 #define DT_QKV_AUTO 2

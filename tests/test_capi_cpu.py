@@ -190,3 +190,8 @@ def test_ctx_option_validation():
     lib = C.lib()
     assert lib.dt_ctx_set_option(None, C.DT_OPT_QKV_FUSED, C.DT_QKV_AUTO) == C.DT_ERR_INVALID_ARG
     assert "ctx is NULL" in last_error()
+
+
+def test_gemm_tune_option_validation():
+    lib = C.lib()
+    assert lib.dt_ctx_set_option(None, C.DT_OPT_GEMM_TUNE, 1) == C.DT_ERR_INVALID_ARG
