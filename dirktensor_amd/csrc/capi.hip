@@ -824,7 +824,9 @@ int dt_attn_layer_fwd(dt_attn_layer* L, const float* x, float* out, int B, int T
         od = static_cast<float*>(ctx->stage[1].ptr);
     }
     bool fused = ctx->qkv_fused == DT_QKV_FUSED && H % 4 == 0;  // (the fused kernel needs H % 4 == 0)
-    if (ctx->qkv_fused == DT_QKV_AUTO) DT_TRY(qkv_fused_one_round(rows, H, &fused));
+    // auto: the fused kernel in bf16 mode where its tiles fit one round (measured faster there); fp32 exact mode
+    // keeps rocBLAS sgemm + the norm kernel (T = 512: 226 against 235 us per layer)
+    if (ctx->qkv_fused == DT_QKV_AUTO && dtype == DT_BF16) DT_TRY(qkv_fused_one_round(rows, H, &fused));
     float* rms = save_for_backward ? static_cast<float*>(L->rms.ptr) : nullptr;
     float* st_m = save_for_backward ? static_cast<float*>(L->stats.ptr) : nullptr;
     float* st_l = save_for_backward ? st_m + (size_t)rows * H : nullptr;

@@ -89,11 +89,12 @@ int dt_ctx_destroy(dt_ctx* ctx);
  *                     DT_QKV_GEMM  one library GEMM, then a norm + RoPE kernel;
  *                     DT_QKV_FUSED one fused kernel (same results within the
  *                                  mode's tolerance);
- *                     DT_QKV_AUTO  (default) the fused kernel when its 128-row x
- *                                  one-head tiles fit one round on the GPU's
- *                                  CUs (B*T <= 640 at 16 heads on MI355X),
- *                                  where it measured faster; the GEMM path
- *                                  above that.
+ *                     DT_QKV_AUTO  (default) in DT_BF16 mode the fused kernel
+ *                                  when its 128-row x one-head tiles fit one
+ *                                  round on the GPU's CUs (B*T <= 640 at 16
+ *                                  heads on MI355X), where it measured faster;
+ *                                  the GEMM path above that and in
+ *                                  DT_FP32_EXACT mode.
  *   DT_OPT_GEMM_TUNE  1 (default): the first bf16 GEMM of each new shape on
  *                     this context times hipBLASLt's heuristic candidates
  *                     (up to 16, into a scratch output; synchronises the
