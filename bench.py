@@ -248,6 +248,9 @@ def main() -> int:
                     "followed by the separate norm + RoPE kernel, or auto (fused where its tiles fit one round)")
     ap.add_argument("--gemm-tune", type=int, choices=[0, 1], default=1,
                     help="bf16 GEMMs: time hipBLASLt's heuristic candidates once per shape (1) or take its first choice (0)")
+    ap.add_argument("--bwd-dq", choices=["auto", "from_ds", "recompute"], default="auto",
+                    help="bf16 attention backward: dQ from the dS the dK/dV pass stores, recomputed S and dP, or "
+                    "auto (the dS path with more than one 128-row block per CU and pass)")
     ap.add_argument("--copy-mib", type=int, default=0,
                     help="instead of attention, time a plain copy kernel over this many MiB (counter calibration)")
     args = ap.parse_args()
@@ -270,6 +273,7 @@ def main() -> int:
     ctx = dt.default_context(0)
     ctx.set_qkv_path(args.qkv)
     ctx.set_gemm_tune(bool(args.gemm_tune))
+    ctx.set_bwd_dq_path(args.bwd_dq)
     wl = WORKLOADS[args.workload](args, dev, stream, ctx)
 
     settle = settle_clock(wl["step"], stream)
@@ -484,7 +488,7 @@ def wl_flash_bwd(args, dev, stream, ctx):
                 metric=f"causal attn backward TFLOP/s, OLMo-2-1B shape T={T} (% of MFMA peak)",
                 data="synthetic (Q/K/V ~ N(0,1) seeds 1001-1003, dO ~ N(0,1) seed 1004)",
                 config={"workload": f"causal flash attention backward, B={B} T={T} H={H} D={D}, {args.mode}",
-                        "B": B, "T": T, "H": H, "D": D, "causal": True})
+                        "B": B, "T": T, "H": H, "D": D, "causal": True, "dq_path": args.bwd_dq})
 
 
 def wl_ragged_fwd(args, dev, stream, ctx):

@@ -30,6 +30,10 @@ DT_QKV_GEMM = 0
 DT_QKV_FUSED = 1
 DT_QKV_AUTO = 2
 DT_OPT_GEMM_TUNE = 2
+DT_OPT_BWD_DQ = 3
+DT_BWD_DQ_RECOMPUTE = 0
+DT_BWD_DQ_FROM_DS = 1
+DT_BWD_DQ_AUTO = 2
 
 HEAD_DIM = 128
 MAX_SEQ_LEN = 8192

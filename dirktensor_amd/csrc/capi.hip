@@ -470,6 +470,13 @@ int dt_ctx_set_option(dt_ctx* ctx, int option, int value) {
         ctx->gemm_tune = value;
         return DT_OK;
     }
+    if (option == DT_OPT_BWD_DQ) {
+        if (value != DT_BWD_DQ_RECOMPUTE && value != DT_BWD_DQ_FROM_DS && value != DT_BWD_DQ_AUTO)
+            return set_error(DT_ERR_INVALID_ARG,
+                             "DT_OPT_BWD_DQ takes DT_BWD_DQ_RECOMPUTE, DT_BWD_DQ_FROM_DS or DT_BWD_DQ_AUTO, not %d", value);
+        ctx->bwd_dq = value;
+        return DT_OK;
+    }
     return set_error(DT_ERR_INVALID_ARG, "unknown context option %d", option);
 }
 
@@ -481,6 +488,7 @@ int dt_ctx_destroy(dt_ctx* ctx) {
     if (ctx->rope_sin) (void)hipFree(ctx->rope_sin);
     for (auto& b : ctx->stage) b.release();
     ctx->bwd_stats.release();
+    ctx->bwd_ds.release();
     ctx->fwd_split.release();
     ctx->fwd_split_cnt.release();
     ctx->qkv_ss.release();
@@ -555,6 +563,30 @@ int dt_flash_attn_fwd(dt_ctx* ctx, const void* q, const void* k, const void* v, 
     return DT_OK;
 }
 
+// The dS workspace of a bf16 attention backward when DT_OPT_BWD_DQ selects the dS path, else NULL. The
+// automatic choice takes it where it measured faster (more than one 128-row block per CU and pass, e.g.
+// B*H = 16 at T = 4096) and falls back to the recompute path when the buffer cannot be allocated.
+static int bwd_ds_workspace(dt_ctx* ctx, int B, int H, int T, int causal, void** ws) {
+    *ws = nullptr;
+    if (ctx->bwd_dq == DT_BWD_DQ_RECOMPUTE) return DT_OK;
+    const size_t bytes = flash_bwd_ds_bytes(B, H, T, causal);
+    if (ctx->bwd_dq == DT_BWD_DQ_AUTO) {
+        int cus = 0;
+        DT_TRY(persistent_grid(0x7fffffff, &cus));
+        const int64_t blocks = (int64_t)((T + 127) / 128) * B * H;
+        if (blocks <= cus) return DT_OK;
+        if (ctx->bwd_ds.ensure(bytes) != DT_OK) {  // out of memory: the recompute path needs no buffer
+            (void)hipGetLastError();
+            clear_error();
+            return DT_OK;
+        }
+    } else {
+        DT_TRY(ctx->bwd_ds.ensure(bytes));
+    }
+    *ws = ctx->bwd_ds.ptr;
+    return DT_OK;
+}
+
 int dt_flash_attn_bwd(dt_ctx* ctx, const void* d_o, const void* o, const float* m, const float* l, const void* q,
                       const void* k, const void* v, void* d_q, void* d_k, void* d_v, int B, int T, int H, int D,
                       float scale, int causal, int dtype, int mem, void* stream) {
@@ -581,6 +613,7 @@ int dt_flash_attn_bwd(dt_ctx* ctx, const void* d_o, const void* o, const float* 
     DT_TRY(ctx->bwd_stats.ensure(2 * nst * sizeof(float)));
     float* stats = static_cast<float*>(ctx->bwd_stats.ptr);
     FlashBwdArgs ba{q, k, v, o, d_o, m, l, d_q, d_k, d_v, stats, stats + nst, B, T, H, ld, ld, ld, scale, causal};
+    if (dtype == DT_BF16) DT_TRY(bwd_ds_workspace(ctx, B, H, T, causal, &ba.ds_ws));
     auto run = [&](const FlashBwdArgs& x) {
         return dtype == DT_BF16 ? launch_flash_bwd_bf16(x, s) : launch_flash_bwd_f32(x, s);
     };
@@ -1031,6 +1064,7 @@ static int attn_layer_bwd(dt_attn_layer* L, const float* d_out, float* d_x, int 
     char* dq = static_cast<char*>(dqkv);
     FlashBwdArgs ba{att, att + dm * esz, att + 2 * dm * esz, attn, d_o, st_m, st_l, dq, dq + dm * esz,
                     dq + 2 * dm * esz, bstats, bstats + (size_t)rows * H, B, T, H, 3 * dm, dm, 3 * dm, scale, 1};
+    if (bf) DT_TRY(bwd_ds_workspace(ctx, B, H, T, 1, &ba.ds_ws));
     DT_TRY(bf ? launch_flash_bwd_bf16(ba, s) : launch_flash_bwd_f32(ba, s));
     // steps 3-4 (:234-244): RoPE backward and the q/k norms' backward, in place on dq | dk
     NormRopeBwdArgs nb{dq, dq + dm * esz, pre, pre + dm * esz, rms, rms + rows, L->q_norm, L->k_norm,

@@ -90,8 +90,12 @@ struct FlashBwdArgs {
     int ld_grad; // row stride of d_q, d_k and d_v
     float scale;
     int causal;
+    // bf16 mode: workspace for dS (flash_bwd_ds_bytes); when set, the dK/dV pass stores dS there and dQ is
+    // computed as dS K from it instead of recomputing S and dP. NULL: the recompute path.
+    void* ds_ws = nullptr;
 };
 int launch_flash_bwd_prep(const FlashBwdArgs& a, int bf16, hipStream_t stream);  // fills delta and lse2
+size_t flash_bwd_ds_bytes(int B, int H, int T, int causal);  // bf16 dS workspace of one backward call
 int launch_flash_bwd_bf16(const FlashBwdArgs& a, hipStream_t stream);
 int launch_flash_bwd_f32(const FlashBwdArgs& a, hipStream_t stream);
 
@@ -202,6 +206,8 @@ struct dt_ctx {
     uint32_t qkv_epoch = 0;    // the tag of its last launch
     int qkv_fused = DT_QKV_AUTO;  // DT_OPT_QKV_FUSED
     int gemm_tune = 1;            // DT_OPT_GEMM_TUNE
+    int bwd_dq = DT_BWD_DQ_AUTO;  // DT_OPT_BWD_DQ
+    dt::DeviceBuffer bwd_ds;      // bf16 attention backward: dS of one call (the dS path)
 };
 
 // OlmoAttention on the device (OlmoAttention.h:10-42): weights, forward state kept for backward, gradients.

@@ -61,6 +61,7 @@ typedef __bf16 bf16x2 __attribute__((ext_vector_type(2)));
 typedef float floatx2 __attribute__((ext_vector_type(2)));
 typedef short shortx4 __attribute__((ext_vector_type(4)));
 typedef short shortx8 __attribute__((ext_vector_type(8)));
+typedef unsigned int u32x4 __attribute__((ext_vector_type(4)));
 typedef __attribute__((address_space(3))) shortx4 lds_shortx4;
 
 constexpr int kD = 128;
@@ -71,6 +72,26 @@ constexpr int kBlk = 128;                      // rows owned by a workgroup: 4 w
 constexpr int kThreads = 256;
 constexpr float kLog2e = 1.4426950408889634f;
 constexpr int kBufferDword3 = 0x00020000;  // raw buffer, 32-bit data format (gfx9 family)
+
+// dS workspace (the path that stores dS in the dK/dV pass and computes dQ = dS K from it). Per (batch, head)
+// and 128-key block kb, one 16 KB block per 64-query tile the keys can see (tiles 2*kb .. under causality,
+// all otherwise), tiles of one key block consecutive. A block holds 128 key rows of 128 bytes; a row holds
+// the tile's 64 queries as 16-byte chunks, chunk c = 4*qb + 2*u + hh holding queries 32*qb + 16*u + 4*hh
+// + {0..3} and then + 8 + {0..3} (one dK/dV lane's bf16 B operand of dS, stored whole), at chunk position
+// c ^ (2 * (row & 3)) so that the dQ pass's transposing reads of four consecutive rows hit distinct banks.
+constexpr int kDsRowBytes = 128;
+constexpr int kDsBlockBytes = kBlk * kDsRowBytes;  // 16 KB
+constexpr int kDsHalfBytes = kTile * kDsRowBytes;  // the rows of one 64-key tile: 8 KB
+
+struct DsLayout {
+    int nqt, nkb, causal;
+    __host__ __device__ DsLayout(int T, int causal_) : nqt((T + kTile - 1) / kTile), nkb((T + kBlk - 1) / kBlk), causal(causal_) {}
+    __host__ __device__ int first_tile(int kb) const { return causal ? 2 * kb : 0; }
+    __host__ __device__ int64_t block_offset(int kb) const {  // blocks before key block kb's, in one (batch, head)
+        return (int64_t)kb * nqt - (causal ? (int64_t)kb * (kb - 1) : 0);
+    }
+    __host__ __device__ int64_t per_head() const { return block_offset(nkb); }
+};
 
 __device__ __forceinline__ uint32_t pack_bf16x2(float lo, float hi) {
     bf16x2 r = __builtin_convertvector((floatx2){lo, hi}, bf16x2);
@@ -222,7 +243,8 @@ struct DkdvStage {
     float delta[kTile];
 };
 
-// dK and dV of key block kb_own of (batch, head) bh
+// dK and dV of key block kb_own of (batch, head) bh; kEmitDs: also dS -> the dS workspace
+template <bool kEmitDs>
 __device__ __forceinline__ void dkdv_block(const FlashBwdArgs& a, int kb_own, int bh, DkdvStage& st0, DkdvStage& st1) {
     const int tid = threadIdx.x;
     const int lane = tid & 63;
@@ -266,6 +288,20 @@ __device__ __forceinline__ void dkdv_block(const FlashBwdArgs& a, int kb_own, in
         const int q_begin = a.causal ? kb * kBlk : 0;
         const int n_steps = (T - q_begin + kTile - 1) / kTile;
 
+        // dS stores: this key block's blocks of the workspace; lane row 32*wave + ln, chunk (4*qb + 2*u + hh) ^ xs
+        const __amdgpu_buffer_rsrc_t ds_rsrc = [&] {
+            if constexpr (kEmitDs) {
+                const DsLayout lay(T, a.causal);
+                const uint8_t* base = static_cast<const uint8_t*>(a.ds_ws) +
+                                      (uint64_t)(bh * lay.per_head() + lay.block_offset(kb)) * kDsBlockBytes;
+                return make_rsrc(base, (uint32_t)n_steps * kDsBlockBytes);
+            } else {
+                return make_rsrc(a.ds_ws, 0u);
+            }
+        }();
+        const uint32_t ds_row = (uint32_t)((32 * wave + ln) * kDsRowBytes);
+        const uint32_t ds_xs = (uint32_t)((hh ^ (2 * (ln & 3))) << 4);
+
         auto dma = [&](DkdvStage& s, int q0) {
             dma_tile(s.q, Qg, q0, T, a.ld_qkv, voff_q, wave);
             dma_tile(s.g, Gg, q0, T, a.ld_o, voff_g, wave);
@@ -275,7 +311,9 @@ __device__ __forceinline__ void dkdv_block(const FlashBwdArgs& a, int kb_own, in
         auto step = [&](const DkdvStage& s, DkdvStage& nxt, int q0, bool has_next) {
             if (has_next) dma(nxt, q0 + kTile);
             if (a.causal && q0 + kTile - 1 < kw) return;  // every query of the tile precedes the wave's keys
-            const bool need_mask = a.causal && q0 < kw + 31;
+            // (the dQ pass never reads the dS of such a tile and wave: all of it is masked)
+            // with dS stored, keys past T are masked too (their dS would otherwise be exp2(-lse2) (-delta))
+            const bool need_mask = (a.causal && q0 < kw + 31) || (kEmitDs && kw + 31 >= T);
             // One software-pipelined sequence of 64 bundles (one LDS fragment read three ahead + one MFMA
             // each), the P / dS arithmetic of one 32-query block riding on the MFMAs of the next phase so
             // that it issues while the matrix pipe works:
@@ -307,7 +345,8 @@ __device__ __forceinline__ void dkdv_block(const FlashBwdArgs& a, int kb_own, in
             auto elem = [&](int qb, int i) {  // P = exp2(S c - lse2), dS = P (dP - delta)
                 float pv = __builtin_amdgcn_exp2f(sc[qb][i] * c - Lr[qb][i]);
                 const int q = q0 + 32 * qb + 8 * (i >> 2) + 4 * hh + (i & 3);
-                pv = (need_mask && key > q) ? 0.0f : pv;
+                if constexpr (kEmitDs) pv = (need_mask && key > (a.causal ? min(q, T - 1) : T - 1)) ? 0.0f : pv;
+                else pv = (need_mask && key > q) ? 0.0f : pv;
                 p[qb][i] = pv;
                 ds[qb][i] = pv * (dp[qb][i] - Dr[qb][i]);
             };
@@ -341,6 +380,12 @@ __device__ __forceinline__ void dkdv_block(const FlashBwdArgs& a, int kb_own, in
                 if constexpr (b >= 32 && b < 48) elem(1, b - 32);
                 if constexpr (b == 23 || b == 31) pack(0, b == 31);
                 if constexpr (b == 39 || b == 47) pack(1, b == 47);
+                if constexpr (kEmitDs && (b == 24 || b == 32 || b == 40 || b == 48)) {
+                    constexpr int qb = (b - 24) >> 4, u = ((b - 24) >> 3) & 1;
+                    __builtin_amdgcn_raw_buffer_store_b128(__builtin_bit_cast(u32x4, dsb[qb][u]), ds_rsrc,
+                                                          ds_row + (((4 * qb + 2 * u) << 4) ^ ds_xs),
+                                                          (int)((q0 - q_begin) / kTile) * kDsBlockBytes, 0);
+                }
                 DT_BUNDLE_END;
             });
         };
@@ -481,6 +526,155 @@ __device__ __forceinline__ void dq_block(const FlashBwdArgs& a, int qb_own, int 
     }
 }
 
+// ------------------------------------------------------------------------------------------------ dQ from dS
+// Eight waves per workgroup share each 64-key tile: wave w takes the block's queries 32*(w & 3) .. +31 and
+// dims 64*(w >> 2) .. +63, so every dQ element has one owner and the tiles' products add in key order. The
+// tiles stream through a four-stage LDS ring, three tiles ahead of the one in use (the dS rows come from
+// HBM: one tile of lookahead left the kernel waiting on memory latency). One workgroup per CU, blocks in
+// decreasing causal cost.
+constexpr int kDqThreads = 512;
+constexpr int kDqStages = 4;
+
+// LDS stage: a 64-key tile of K and the dS rows of those keys for the block's two 64-query tiles
+struct DsqStage {
+    uint8_t k[kTileBytes];
+    uint8_t ds[2][kDsHalfBytes];
+};
+
+// the stage of tile s + 1 has landed (this wave's requests for the two tiles after it, eight instructions,
+// may still be in flight) and every wave is done with the stage of tile s
+__device__ __forceinline__ void ring_barrier() { asm volatile("s_waitcnt vmcnt(8) lgkmcnt(0)\n\ts_barrier" ::: "memory"); }
+
+// dQ of query block qb_own of (batch, head) bh from the dS the dK/dV pass stored: per 64-key tile a wave
+// accumulates its 64 dims of dQ^T += K^T dS^T for its 32 queries (8 MFMAs), K^T and dS^T by transposing reads.
+__device__ __forceinline__ void dq_ds_block(const FlashBwdArgs& a, int qb_own, int bh, DsqStage (&st)[kDqStages]) {
+    const int tid = threadIdx.x;
+    const int lane = tid & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+    const int wq = wave & 3, dsel = wave >> 2;
+    const int ln = lane & 31;
+    const int hh = lane >> 5;
+    const int T = a.T;
+    const int b = bh / a.H, h = bh % a.H;
+
+    // K^T reads of this wave's dim blocks 2*dsel and 2*dsel + 1
+    const LaneAddr LA = lane_addr(lane);
+    uint32_t taddr[2][2];
+#pragma unroll
+    for (int r = 0; r < 2; ++r)
+#pragma unroll
+        for (int d = 0; d < 2; ++d) taddr[r][d] = dsel ? LA.taddr[r][2 + d] : LA.taddr[r][d];
+    // K DMA: instruction i of wave w fills rows 32*i + 4*w + lane/16 at chunk position lane%16, fetching the
+    // global chunk the swizzle puts there (swz of those rows is 4*(lane/16) + (w & 3))
+    uint32_t voff[2];
+    {
+        const int rlo = lane >> 4;
+        const int chunk = (lane & 15) ^ (4 * rlo + (wave & 3));
+#pragma unroll
+        for (int i = 0; i < 2; ++i) voff[i] = (uint32_t)(((32 * i + 4 * wave + rlo) * a.ld_qkv + 8 * chunk) * 2);
+    }
+    const uint16_t* Kg = static_cast<const uint16_t*>(a.k) + (int64_t)b * T * a.ld_qkv + (int64_t)h * kD;
+    uint16_t* dQg = static_cast<uint16_t*>(a.d_q) + (int64_t)b * T * a.ld_grad + (int64_t)h * kD;
+    const DsLayout lay(T, a.causal);
+    const uint8_t* ds_head = static_cast<const uint8_t*>(a.ds_ws) + (uint64_t)(bh * lay.per_head()) * kDsBlockBytes;
+
+    const int qw = qb_own * kBlk + 32 * wq;  // the wave's first query
+    const int q = qw + ln;
+    const int qt = wq >> 1, qh = wq & 1;      // the wave's 64-query tile in the block, its 32-query half there
+    // dS^T fragment reads: lane i of 16-lane group G reads key row 4*hh + i/4 (+8 for the second read) of a
+    // 16-key chunk, queries 32*qh + 16*(G & 1) + 4*(i & 3) .. +3 (chunk 4*qh + 2*(G & 1) + (i & 1), half
+    // (i & 3) / 2, the chunk swizzled by the row); the transposing read hands lane i query 16*(G & 1) + i.
+    const int i16 = lane & 15, G = lane >> 4;
+    const uint32_t ds_addr = (uint32_t)(qt * kDsHalfBytes + (4 * hh + (i16 >> 2)) * kDsRowBytes +
+                                        (((4 * qh + 2 * (G & 1) + (i16 & 1)) ^ (2 * (i16 >> 2))) << 4) + 8 * ((i16 & 3) >> 1));
+    auto read_ds = [&](const uint8_t* ds, int c) {  // keys 16*c + {4*hh .. +3, 8 + 4*hh .. +3}: the B operand
+        const shortx4 lo = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_shortx4*)(ds + ds_addr + 16 * c * kDsRowBytes));
+        const shortx4 hi =
+            __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_shortx4*)(ds + ds_addr + (16 * c + 8) * kDsRowBytes));
+        return __builtin_bit_cast(bf16x8, (shortx8){lo[0], lo[1], lo[2], lo[3], hi[0], hi[1], hi[2], hi[3]});
+    };
+    auto read_kt = [&](const uint8_t* tile, int c, int d) {  // K^T chunk: keys of 16-key chunk c, dims 32*(2*dsel + d) ..
+        const int rows = (c >> 1) * 8192 + (c & 1) * 4096;
+        const shortx4 lo = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_shortx4*)(tile + taddr[0][d] + rows));
+        const shortx4 hi = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_shortx4*)(tile + taddr[1][d] + rows + 2048));
+        return __builtin_bit_cast(bf16x8, (shortx8){lo[0], lo[1], lo[2], lo[3], hi[0], hi[1], hi[2], hi[3]});
+    };
+
+    floatx16 dq[2] = {zero16(), zero16()};
+    const int k_end = a.causal ? min(qb_own * kBlk + kBlk, T) : T;
+    const int n_tiles = (k_end + kTile - 1) / kTile;
+    const int qt0 = 2 * qb_own;  // the block's first 64-query tile
+    const int n_qt = min(2, lay.nqt - qt0);
+
+    // tile kt -> stage kt % 4: four DMA instructions per wave, also for kt past the range (an empty buffer
+    // then: nothing is read, the stage is not used), so that the count of requests in flight is fixed
+    auto dma = [&](int kt) {
+        DsqStage& s = st[kt & (kDqStages - 1)];
+        const bool live = kt < n_tiles;
+        const int k0 = live ? kt * kTile : 0;
+        const __amdgpu_buffer_rsrc_t rk = make_rsrc(Kg + (int64_t)k0 * a.ld_qkv, live ? (uint32_t)(T - k0) * (uint32_t)a.ld_qkv * 2u : 0u);
+        const uint32_t lk = __builtin_amdgcn_readfirstlane(lds_addr(s.k + wave * 1024));
+        dma16(lk, voff[0], rk);
+        dma16(lk + 8192, voff[1], rk);
+        const int kb = k0 / kBlk;
+        const uint8_t* blk = ds_head + (uint64_t)(lay.block_offset(kb) + (qt0 - lay.first_tile(kb))) * kDsBlockBytes;
+        const __amdgpu_buffer_rsrc_t r = make_rsrc(blk, live ? (uint32_t)n_qt * kDsBlockBytes : 0u);
+        const uint32_t rows = (uint32_t)(kt & 1) * kDsHalfBytes;  // this tile's rows of the key block
+        const uint32_t chunk = (uint32_t)(wave * 64);              // 16-byte chunks of an 8 KB half
+#pragma unroll
+        for (int t = 0; t < 2; ++t)
+            dma16(__builtin_amdgcn_readfirstlane(lds_addr(s.ds[t] + chunk * 16)),
+                  (uint32_t)t * kDsBlockBytes + rows + (chunk + (uint32_t)lane) * 16u, r);
+    };
+    auto step = [&](int kt) {
+        const DsqStage& s = st[kt & (kDqStages - 1)];
+        const int k0 = kt * kTile;
+        if (qw >= T || (a.causal && k0 > qw + 31)) return;  // no query of the wave, or every key after them
+        // the second 32 keys are all after the wave's queries under causality: their dS was not stored
+        const bool second = !a.causal || k0 + 32 <= qw + 31;
+        bf16x8 dsf[4];
+#pragma unroll
+        for (int c = 0; c < 4; ++c) dsf[c] = read_ds(s.ds[0], c);
+        if (!second) {
+            dsf[2] = __builtin_bit_cast(bf16x8, make_uint4(0, 0, 0, 0));
+            dsf[3] = dsf[2];
+        }
+        bf16x8 ring[4];
+        ring[0] = read_kt(s.k, 0, 0);
+        ring[1] = read_kt(s.k, 0, 1);
+        ring[2] = read_kt(s.k, 1, 0);
+        static_for<8>([&](auto J) {
+            constexpr int j = decltype(J)::value;  // chunk j / 2, dim block 2*dsel + j % 2
+            if constexpr (j + 3 < 8) ring[(j + 3) & 3] = read_kt(s.k, (j + 3) >> 1, (j + 3) & 1);
+            dq[j & 1] = mfma(ring[j & 3], dsf[j >> 1], dq[j & 1]);
+            DT_BUNDLE_END;
+        });
+    };
+
+    dma(0);
+    dma(1);
+    dma(2);
+    ring_barrier();  // tile 0 has landed
+    for (int kt = 0; kt < n_tiles; ++kt) {
+        dma(kt + 3);  // into the stage of tile kt - 1, which every wave has finished
+        step(kt);
+        ring_barrier();
+    }
+    asm volatile("s_waitcnt vmcnt(0)" ::: "memory");  // the requests past the range, before the workgroup ends
+    if (q < T) {
+        uint16_t* p = dQg + (int64_t)q * a.ld_grad + 64 * dsel;
+#pragma unroll
+        for (int d = 0; d < 2; ++d)
+#pragma unroll
+            for (int g = 0; g < 4; ++g) {
+                uint2 w;
+                w.x = pack_bf16x2(dq[d][4 * g] * a.scale, dq[d][4 * g + 1] * a.scale);
+                w.y = pack_bf16x2(dq[d][4 * g + 2] * a.scale, dq[d][4 * g + 3] * a.scale);
+                *reinterpret_cast<uint2*>(p + 32 * d + 8 * g + 4 * hh) = w;
+            }
+    }
+}
+
 // One 128-row block per workgroup, listed in decreasing causal cost, so that the hardware, which hands
 // the next workgroup to the first CU that frees up, runs a longest-first schedule.
 // pass = 0 (dK/dV) or 1 (dQ): one pass per launch; workgroup BH*j + bh takes, for (batch, head) bh,
@@ -507,8 +701,22 @@ __global__ __launch_bounds__(kThreads, 1) void flash_bwd_bf16_kernel(FlashBwdArg
     const int j = (int)blockIdx.x / (pass == 2 ? 2 * BH : BH);
     const int kind = pass == 2 ? ((int)blockIdx.x / BH) & 1 : pass;
     const int bh = (int)blockIdx.x % BH;
-    if (kind == 0) dkdv_block(a, j, bh, lds.kv.s0, lds.kv.s1);
+    if (kind == 0) dkdv_block<false>(a, j, bh, lds.kv.s0, lds.kv.s1);
     else dq_block(a, n - 1 - j, bh, lds.q.s0, lds.q.s1);
+}
+
+// The dS path: the dK/dV pass (workgroup BH*j + bh: key block j) storing dS, then dQ = dS K (workgroup
+// BH*j + bh: query block n-1-j), both in decreasing causal cost.
+__global__ __launch_bounds__(kThreads, 1) void flash_bwd_dkdv_ds_bf16_kernel(FlashBwdArgs a) {
+    __shared__ __attribute__((aligned(1024))) DkdvStage s0, s1;
+    const int BH = a.B * a.H;
+    dkdv_block<true>(a, (int)blockIdx.x / BH, (int)blockIdx.x % BH, s0, s1);
+}
+__global__ __launch_bounds__(kDqThreads, 1) void flash_bwd_dq_ds_bf16_kernel(FlashBwdArgs a) {
+    __shared__ __attribute__((aligned(1024))) DsqStage st[kDqStages];
+    const int BH = a.B * a.H;
+    const int n = (a.T + kBlk - 1) / kBlk;
+    dq_ds_block(a, n - 1 - (int)blockIdx.x / BH, (int)blockIdx.x % BH, st);
 }
 
 }  // namespace
@@ -519,6 +727,13 @@ int launch_flash_bwd_bf16(const FlashBwdArgs& a, hipStream_t stream) {
     DT_TRY(launch_flash_bwd_prep(a, 1, stream));
     const int64_t blocks = (int64_t)((a.T + kBlk - 1) / kBlk) * a.B * a.H;  // per pass, one per workgroup
     if (2 * blocks > 0x7fffffff) return set_error(DT_ERR_UNSUPPORTED, "too many workgroups");
+    if (a.ds_ws) {  // dS stored by the dK/dV pass, dQ = dS K
+        hipLaunchKernelGGL(flash_bwd_dkdv_ds_bf16_kernel, dim3((unsigned)blocks), dim3(kThreads), 0, stream, a);
+        DT_HIP_TRY(hipGetLastError());
+        hipLaunchKernelGGL(flash_bwd_dq_ds_bf16_kernel, dim3((unsigned)blocks), dim3(kDqThreads), 0, stream, a);
+        DT_HIP_TRY(hipGetLastError());
+        return DT_OK;
+    }
     int cus = 0;
     DT_TRY(persistent_grid(0x7fffffff, &cus));
     if (blocks <= cus) {  // the passes share one launch (measured: T = 2048, B*H = 16: 148 -> 94 us; at
@@ -532,6 +747,10 @@ int launch_flash_bwd_bf16(const FlashBwdArgs& a, hipStream_t stream) {
         }
     }
     return DT_OK;
+}
+
+size_t flash_bwd_ds_bytes(int B, int H, int T, int causal) {
+    return (size_t)B * H * (size_t)DsLayout(T, causal).per_head() * kDsBlockBytes;
 }
 
 }  // namespace dt

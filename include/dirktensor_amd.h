@@ -100,13 +100,33 @@ int dt_ctx_destroy(dt_ctx* ctx);
  *                     (up to 16, into a scratch output; synchronises the
  *                     stream once) and keeps the fastest whose repeated run
  *                     is bit-identical; 0: the first heuristic choice.
+ *   DT_OPT_BWD_DQ     how the DT_BF16 attention backward (dt_flash_attn_bwd,
+ *                     dt_attn_layer_bwd, the model backward) forms dQ
+ *                     (FlashAttention.cpp:185-359):
+ *                     DT_BWD_DQ_RECOMPUTE  the dQ pass recomputes S and dP
+ *                                          (no workspace);
+ *                     DT_BWD_DQ_FROM_DS    the dK/dV pass stores dS (bf16,
+ *                                          B*H*T*(T+128)/2 * 2 bytes causal,
+ *                                          B*H*T*T*2 otherwise, a context
+ *                                          buffer) and dQ = dS K reads it;
+ *                     DT_BWD_DQ_AUTO       (default) the dS path where it
+ *                                          measured faster (more than one
+ *                                          128-row block per CU and pass),
+ *                                          the recompute path otherwise or
+ *                                          when the buffer cannot be had.
+ *                     Both give the same results within the mode's
+ *                     tolerance; each is deterministic.
  * Returns DT_ERR_INVALID_ARG for an unknown option or value.
  */
 #define DT_OPT_QKV_FUSED 1
 #define DT_OPT_GEMM_TUNE 2
+#define DT_OPT_BWD_DQ 3
 #define DT_QKV_GEMM 0
 #define DT_QKV_FUSED 1
 #define DT_QKV_AUTO 2
+#define DT_BWD_DQ_RECOMPUTE 0
+#define DT_BWD_DQ_FROM_DS 1
+#define DT_BWD_DQ_AUTO 2
 int dt_ctx_set_option(dt_ctx* ctx, int option, int value);
 
 /*

@@ -195,3 +195,9 @@ def test_ctx_option_validation():
 def test_gemm_tune_option_validation():
     lib = C.lib()
     assert lib.dt_ctx_set_option(None, C.DT_OPT_GEMM_TUNE, 1) == C.DT_ERR_INVALID_ARG
+
+
+def test_bwd_dq_option_validation():
+    lib = C.lib()
+    assert lib.dt_ctx_set_option(None, C.DT_OPT_BWD_DQ, C.DT_BWD_DQ_FROM_DS) == C.DT_ERR_INVALID_ARG
+    assert "ctx is NULL" in last_error()
