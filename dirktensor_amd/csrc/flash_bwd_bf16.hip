@@ -529,11 +529,11 @@ __device__ __forceinline__ void dq_block(const FlashBwdArgs& a, int qb_own, int 
 // ------------------------------------------------------------------------------------------------ dQ from dS
 // Eight waves per workgroup share each 64-key tile: wave w takes the block's queries 32*(w & 3) .. +31 and
 // dims 64*(w >> 2) .. +63, so every dQ element has one owner and the tiles' products add in key order. The
-// tiles stream through a four-stage LDS ring, three tiles ahead of the one in use (the dS rows come from
-// HBM: one tile of lookahead left the kernel waiting on memory latency). One workgroup per CU, blocks in
-// decreasing causal cost.
+// tiles stream through a five-stage LDS ring (all 160 KB), four tiles ahead of the one in use (the dS rows
+// come from HBM: one tile of lookahead left the kernel waiting on memory latency). One workgroup per CU,
+// blocks in decreasing causal cost.
 constexpr int kDqThreads = 512;
-constexpr int kDqStages = 4;
+constexpr int kDqStages = 5;
 
 // LDS stage: a 64-key tile of K and the dS rows of those keys for the block's two 64-query tiles
 struct DsqStage {
@@ -541,9 +541,9 @@ struct DsqStage {
     uint8_t ds[2][kDsHalfBytes];
 };
 
-// the stage of tile s + 1 has landed (this wave's requests for the two tiles after it, eight instructions,
-// may still be in flight) and every wave is done with the stage of tile s
-__device__ __forceinline__ void ring_barrier() { asm volatile("s_waitcnt vmcnt(8) lgkmcnt(0)\n\ts_barrier" ::: "memory"); }
+// the stage of tile s + 1 has landed (this wave's requests for the three tiles after it, twelve
+// instructions, may still be in flight) and every wave is done with the stage of tile s
+__device__ __forceinline__ void ring_barrier() { asm volatile("s_waitcnt vmcnt(12) lgkmcnt(0)\n\ts_barrier" ::: "memory"); }
 
 // dQ of query block qb_own of (batch, head) bh from the dS the dK/dV pass stored: per 64-key tile a wave
 // accumulates its 64 dims of dQ^T += K^T dS^T for its 32 queries (8 MFMAs), K^T and dS^T by transposing reads.
@@ -606,10 +606,10 @@ __device__ __forceinline__ void dq_ds_block(const FlashBwdArgs& a, int qb_own, i
     const int qt0 = 2 * qb_own;  // the block's first 64-query tile
     const int n_qt = min(2, lay.nqt - qt0);
 
-    // tile kt -> stage kt % 4: four DMA instructions per wave, also for kt past the range (an empty buffer
+    // tile kt -> stage kt % 5: four DMA instructions per wave, also for kt past the range (an empty buffer
     // then: nothing is read, the stage is not used), so that the count of requests in flight is fixed
     auto dma = [&](int kt) {
-        DsqStage& s = st[kt & (kDqStages - 1)];
+        DsqStage& s = st[kt % kDqStages];
         const bool live = kt < n_tiles;
         const int k0 = live ? kt * kTile : 0;
         const __amdgpu_buffer_rsrc_t rk = make_rsrc(Kg + (int64_t)k0 * a.ld_qkv, live ? (uint32_t)(T - k0) * (uint32_t)a.ld_qkv * 2u : 0u);
@@ -627,7 +627,7 @@ __device__ __forceinline__ void dq_ds_block(const FlashBwdArgs& a, int qb_own, i
                   (uint32_t)t * kDsBlockBytes + rows + (chunk + (uint32_t)lane) * 16u, r);
     };
     auto step = [&](int kt) {
-        const DsqStage& s = st[kt & (kDqStages - 1)];
+        const DsqStage& s = st[kt % kDqStages];
         const int k0 = kt * kTile;
         if (qw >= T || (a.causal && k0 > qw + 31)) return;  // no query of the wave, or every key after them
         // the second 32 keys are all after the wave's queries under causality: their dS was not stored
@@ -654,9 +654,10 @@ __device__ __forceinline__ void dq_ds_block(const FlashBwdArgs& a, int qb_own, i
     dma(0);
     dma(1);
     dma(2);
+    dma(3);
     ring_barrier();  // tile 0 has landed
     for (int kt = 0; kt < n_tiles; ++kt) {
-        dma(kt + 3);  // into the stage of tile kt - 1, which every wave has finished
+        dma(kt + 4);  // into the stage of tile kt - 1, which every wave has finished
         step(kt);
         ring_barrier();
     }
