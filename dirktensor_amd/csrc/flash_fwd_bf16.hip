@@ -104,8 +104,16 @@ __device__ __forceinline__ uint32_t pack_bf16x2(float lo, float hi) {
 // query). ds_bpermute via __shfl_xor; v_permlane32_swap would avoid the LDS
 // crossbar, but this compiler returns the same register for both of the
 // builtin's results, so its second half is unusable.
-__device__ __forceinline__ float max_halves(float x) { return fmaxf(x, __shfl_xor(x, 32, 64)); }
-__device__ __forceinline__ float sum_halves(float x) { return x + __shfl_xor(x, 32, 64); }
+// Over the two lane halves (lanes l and l ^ 32), through v_permlane32_swap with x as both operands: the
+// result pair holds, in every lane, the lower half's value and the upper half's (same order in both halves).
+__device__ __forceinline__ float max_halves(float x) {
+    const auto r = __builtin_amdgcn_permlane32_swap(__float_as_uint(x), __float_as_uint(x), false, false);
+    return fmaxf(__uint_as_float(r[0]), __uint_as_float(r[1]));
+}
+__device__ __forceinline__ float sum_halves(float x) {
+    const auto r = __builtin_amdgcn_permlane32_swap(__float_as_uint(x), __float_as_uint(x), false, false);
+    return __uint_as_float(r[0]) + __uint_as_float(r[1]);
+}
 
 __device__ __forceinline__ shortx4 lds_read_tr16(const uint8_t* p) {
     return __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_shortx4*)(p));
@@ -453,23 +461,35 @@ __global__ __launch_bounds__(kThreads, 1) void flash_fwd_bf16_kernel(FlashArgs a
             stage_barrier();
         }
 
-        // combine the lane halves' maxima and sums, then merge the two groups through LDS
-        // (no DMA is in flight now)
+        // combine the lane halves' maxima and sums, then merge the two groups through LDS: group g finalises
+        // dims 64g .. 64g+63 (dim blocks 2g, 2g+1) of its block's rows and hands the other half of its partial
+        // O to the other group (no DMA is in flight now)
         A.m_t = max_halves(A.m_t);
         A.l = sum_halves(A.l);
-        // group 1's O of block wq: float4 k = 4*db + I of lane `lane` at xo[k*64 + lane] (16 KB per wave)
-        float4* xo = reinterpret_cast<float4*>(&stage0[0][0][0]) + wq * (16 * 64);
-        float* xs = reinterpret_cast<float*>(&stage1[0][0][0]) + wq * (3 * 64);
-        uint8_t* obuf = &stage1[0][0][0] + 4096;  // the output tile on its way to HBM (128 x 272 bytes, after xs)
-        if (grp == 1) {
-#pragma unroll
-            for (int db = 0; db < 4; ++db)
+        // group g's handed-over half of block wq: float4 k = 4*(db - 2*(1-g)) + I of lane `lane` at
+        // xo(g)[k*64 + lane] (8 KB per wave and group, stage0); its (m_s, m_t, l) at xs(g) (stage1)
+        auto xo = [&](int g) { return reinterpret_cast<float4*>(&stage0[0][0][0]) + (g * 4 + wq) * (8 * 64); };
+        auto xs = [&](int g) { return reinterpret_cast<float*>(&stage1[0][0][0]) + (g * 4 + wq) * (3 * 64); };
+        uint8_t* obuf = &stage1[0][0][0] + 8192;  // the output tile on its way to HBM (128 x 272 bytes, after xs)
+        {
+            float4* out = xo(grp);
+            auto hand = [&](auto DB) {
+                constexpr int db = decltype(DB)::value;
 #pragma unroll
                 for (int I = 0; I < 4; ++I)
-                    xo[(4 * db + I) * 64 + lane] = make_float4(A.o[db][4 * I], A.o[db][4 * I + 1], A.o[db][4 * I + 2], A.o[db][4 * I + 3]);
-            xs[lane] = A.m_s;
-            xs[64 + lane] = A.m_t;
-            xs[128 + lane] = A.l;
+                    out[(4 * (db & 1) + I) * 64 + lane] = make_float4(A.o[db][4 * I], A.o[db][4 * I + 1], A.o[db][4 * I + 2], A.o[db][4 * I + 3]);
+            };
+            if (grp == 0) {
+                hand(std::integral_constant<int, 2>{});
+                hand(std::integral_constant<int, 3>{});
+            } else {
+                hand(std::integral_constant<int, 0>{});
+                hand(std::integral_constant<int, 1>{});
+            }
+            float* st = xs(grp);
+            st[lane] = A.m_s;
+            st[64 + lane] = A.m_t;
+            st[128 + lane] = A.l;
         }
         __syncthreads();
         // part p's partial result in the workspace (split items), and a float4's byte offset in it
@@ -477,62 +497,82 @@ __global__ __launch_bounds__(kThreads, 1) void flash_fwd_bf16_kernel(FlashArgs a
             return make_rsrc(a.split_ws + ((size_t)u.slot * kMaxParts + part) * kPartialFloats, (uint32_t)(kPartialFloats * 4));
         };
         auto pslot = [&](int k) { return (uint32_t)(((wq * 17 + k) * 64 + lane) * 16); };
-        if (grp == 0) {
-            const float m1s = xs[lane];
-            const float m1t = xs[64 + lane];
-            const float l1 = xs[128 + lane];
-            const float ms = fmaxf(A.m_s, m1s);
-            const float a0 = (A.m_s == kNegInf) ? 0.0f : exp2f(A.m_s - ms);
+        {
+            // both groups form the same statistics, group 0's terms first
+            const float* so = xs(1 - grp);
+            const float os = so[lane], ot = so[64 + lane], ol = so[128 + lane];
+            const float m0s = grp ? os : A.m_s, m1s = grp ? A.m_s : os;
+            const float m0t = grp ? ot : A.m_t, m1t = grp ? A.m_t : ot;
+            const float l0 = grp ? ol : A.l, l1 = grp ? A.l : ol;
+            const float ms = fmaxf(m0s, m1s);
+            const float a0 = (m0s == kNegInf) ? 0.0f : exp2f(m0s - ms);
             const float a1 = (m1s == kNegInf) ? 0.0f : exp2f(m1s - ms);
-            const float l = A.l * a0 + l1 * a1;
-            const float mt = fmaxf(A.m_t, m1t);
-            if (u.parts == 1) {
-                {
-                    // the output rows go to LDS (row-major, rows padded to 272 bytes so the 32 rows a write
-                    // instruction touches fall in different banks) and from there to HBM as whole rows, below
-                    const bool valid = qrow < L && l > 0.0f;
-                    const float inv = valid ? 1.0f / l : 0.0f;
-                    const float s0 = a0 * inv, s1 = a1 * inv;
-                    const int orow = 32 * wq + ln;
+            const float l = l0 * a0 + l1 * a1;
+            const float mt = fmaxf(m0t, m1t);
+            const float4* in = xo(1 - grp);
+            // v = O0 * c0 + O1 * c1 over dim block db (this group's): its own O and the other group's half
+            auto merged = [&](auto DB, int I, float c0, float c1, float (&v)[4]) {
+                constexpr int db = decltype(DB)::value;
+                const float4 x = in[(4 * (db & 1) + I) * 64 + lane];
+                const float xv[4] = {x.x, x.y, x.z, x.w};
 #pragma unroll
-                    for (int db = 0; db < 4; ++db)
-#pragma unroll
-                        for (int I = 0; I < 4; ++I) {
-                            const float4 x1 = xo[(4 * db + I) * 64 + lane];
-                            const float x1v[4] = {x1.x, x1.y, x1.z, x1.w};
-                            float v[4];
-#pragma unroll
-                            for (int r = 0; r < 4; ++r) v[r] = A.o[db][4 * I + r] * s0 + x1v[r] * s1;
-                            uint2 w;
-                            w.x = pack_bf16x2(v[0], v[1]);
-                            w.y = pack_bf16x2(v[2], v[3]);
-                            *reinterpret_cast<uint2*>(obuf + orow * kObufRow + 16 * (4 * db + I) + 8 * hh) = w;
-                        }
+                for (int r = 0; r < 4; ++r) {
+                    const float own = A.o[db][4 * I + r];
+                    v[r] = (db < 2) ? own * c0 + xv[r] * c1 : xv[r] * c0 + own * c1;
                 }
-                if (qrow < T) {
-                    const bool valid = qrow < L && l > 0.0f;
-                    if (hh == 0) {
+            };
+            if (u.parts == 1) {
+                // the output rows go to LDS (row-major, rows padded to 272 bytes so the 32 rows a write
+                // instruction touches fall in different banks) and from there to HBM as whole rows, below
+                const bool valid = qrow < L && l > 0.0f;
+                const float inv = valid ? 1.0f / l : 0.0f;
+                const float s0 = a0 * inv, s1 = a1 * inv;
+                const int orow = 32 * wq + ln;
+                auto fin = [&](auto DB) {
+                    constexpr int db = decltype(DB)::value;
+#pragma unroll
+                    for (int I = 0; I < 4; ++I) {
+                        float v[4];
+                        merged(DB, I, s0, s1, v);
+                        uint2 w;
+                        w.x = pack_bf16x2(v[0], v[1]);
+                        w.y = pack_bf16x2(v[2], v[3]);
+                        *reinterpret_cast<uint2*>(obuf + orow * kObufRow + 16 * (4 * db + I) + 8 * hh) = w;
+                    }
+                };
+                if (grp == 0) {
+                    fin(std::integral_constant<int, 0>{});
+                    fin(std::integral_constant<int, 1>{});
+                    if (qrow < T && hh == 0) {
                         if (a.m) a.m[stat_base + (int64_t)qrow * a.H] = valid ? mt * (1.0f / kLog2e) : kNegInf;
                         if (a.l) a.l[stat_base + (int64_t)qrow * a.H] = valid ? l * exp2f(ms - mt) : 0.0f;
                     }
+                } else {
+                    fin(std::integral_constant<int, 2>{});
+                    fin(std::integral_constant<int, 3>{});
                 }
             } else {
                 // this part's O relative to ms, both groups' keys, and (m_s, m_t, l) -> its workspace slot in
                 // register order: float4 k = 4*db + I of lane `lane` of wave wq at ((wq*17 + k)*64 + lane)*16
-                // bytes, k = 16 the statistics (1 KB contiguous per store instruction)
+                // bytes, k = 16 the statistics (1 KB contiguous per store instruction); each group its dims
                 const __amdgpu_buffer_rsrc_t rp = partial_rsrc(u.part);
-#pragma unroll
-                for (int db = 0; db < 4; ++db)
+                auto put = [&](auto DB) {
+                    constexpr int db = decltype(DB)::value;
 #pragma unroll
                     for (int I = 0; I < 4; ++I) {
-                        const float4 x1 = xo[(4 * db + I) * 64 + lane];
-                        const float x1v[4] = {x1.x, x1.y, x1.z, x1.w};
                         float v[4];
-#pragma unroll
-                        for (int r = 0; r < 4; ++r) v[r] = A.o[db][4 * I + r] * a0 + x1v[r] * a1;
+                        merged(DB, I, a0, a1, v);
                         store_coherent(make_float4(v[0], v[1], v[2], v[3]), rp, pslot(4 * db + I));
                     }
-                store_coherent(make_float4(ms, mt, l, 0.0f), rp, pslot(16));
+                };
+                if (grp == 0) {
+                    put(std::integral_constant<int, 0>{});
+                    put(std::integral_constant<int, 1>{});
+                    store_coherent(make_float4(ms, mt, l, 0.0f), rp, pslot(16));
+                } else {
+                    put(std::integral_constant<int, 2>{});
+                    put(std::integral_constant<int, 3>{});
+                }
             }
         }
         if (u.parts == 1) {  // the item's 128 output rows: 16 lanes per 256-byte row, 4 rows per store instruction
