@@ -249,7 +249,7 @@ def main() -> int:
     ap.add_argument("--gemm-tune", type=int, choices=[0, 1], default=1,
                     help="bf16 GEMMs: time hipBLASLt's heuristic candidates once per shape (1) or take its first choice (0)")
     ap.add_argument("--bwd-dq", choices=["auto", "from_ds", "recompute"], default="auto",
-                    help="bf16 attention backward: dQ from the dS the dK/dV pass stores, recomputed S and dP, or "
+                    help="attention backward: dQ from the dS the dK/dV pass stores, recomputed S and dP, or "
                     "auto (the dS path with more than one 128-row block per CU and pass)")
     ap.add_argument("--copy-mib", type=int, default=0,
                     help="instead of attention, time a plain copy kernel over this many MiB (counter calibration)")

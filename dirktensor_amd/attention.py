@@ -72,7 +72,7 @@ class Context:
         C.call("dt_ctx_set_option", self.handle, C.DT_OPT_GEMM_TUNE, int(bool(tune)))
 
     def set_bwd_dq_path(self, path: str) -> None:
-        """How bf16 attention backwards on this context form dQ: "recompute" (the dQ pass recomputes S and dP),
+        """How attention backwards on this context form dQ: "recompute" (the dQ pass recomputes S and dP),
         "from_ds" (the dK/dV pass stores dS in a context buffer and dQ = dS K reads it) or "auto" (the default:
         the dS path with more than one 128-row block per CU and pass)."""
         values = {"recompute": C.DT_BWD_DQ_RECOMPUTE, "from_ds": C.DT_BWD_DQ_FROM_DS, "auto": C.DT_BWD_DQ_AUTO}

@@ -563,13 +563,13 @@ int dt_flash_attn_fwd(dt_ctx* ctx, const void* q, const void* k, const void* v, 
     return DT_OK;
 }
 
-// The dS workspace of a bf16 attention backward when DT_OPT_BWD_DQ selects the dS path, else NULL. The
+// The dS workspace of an attention backward when DT_OPT_BWD_DQ selects the dS path, else NULL. The
 // automatic choice takes it where it measured faster (more than one 128-row block per CU and pass, e.g.
 // B*H = 16 at T = 4096) and falls back to the recompute path when the buffer cannot be allocated.
-static int bwd_ds_workspace(dt_ctx* ctx, int B, int H, int T, int causal, void** ws) {
+static int bwd_ds_workspace(dt_ctx* ctx, int B, int H, int T, int causal, int dtype, void** ws) {
     *ws = nullptr;
     if (ctx->bwd_dq == DT_BWD_DQ_RECOMPUTE) return DT_OK;
-    const size_t bytes = flash_bwd_ds_bytes(B, H, T, causal);
+    const size_t bytes = flash_bwd_ds_bytes(B, H, T, causal, dtype == DT_BF16 ? 2 : 4);
     if (ctx->bwd_dq == DT_BWD_DQ_AUTO) {
         int cus = 0;
         DT_TRY(persistent_grid(0x7fffffff, &cus));
@@ -613,7 +613,7 @@ int dt_flash_attn_bwd(dt_ctx* ctx, const void* d_o, const void* o, const float* 
     DT_TRY(ctx->bwd_stats.ensure(2 * nst * sizeof(float)));
     float* stats = static_cast<float*>(ctx->bwd_stats.ptr);
     FlashBwdArgs ba{q, k, v, o, d_o, m, l, d_q, d_k, d_v, stats, stats + nst, B, T, H, ld, ld, ld, scale, causal};
-    if (dtype == DT_BF16) DT_TRY(bwd_ds_workspace(ctx, B, H, T, causal, &ba.ds_ws));
+    DT_TRY(bwd_ds_workspace(ctx, B, H, T, causal, dtype, &ba.ds_ws));
     auto run = [&](const FlashBwdArgs& x) {
         return dtype == DT_BF16 ? launch_flash_bwd_bf16(x, s) : launch_flash_bwd_f32(x, s);
     };
@@ -1064,7 +1064,7 @@ static int attn_layer_bwd(dt_attn_layer* L, const float* d_out, float* d_x, int 
     char* dq = static_cast<char*>(dqkv);
     FlashBwdArgs ba{att, att + dm * esz, att + 2 * dm * esz, attn, d_o, st_m, st_l, dq, dq + dm * esz,
                     dq + 2 * dm * esz, bstats, bstats + (size_t)rows * H, B, T, H, 3 * dm, dm, 3 * dm, scale, 1};
-    if (bf) DT_TRY(bwd_ds_workspace(ctx, B, H, T, 1, &ba.ds_ws));
+    DT_TRY(bwd_ds_workspace(ctx, B, H, T, 1, bf ? DT_BF16 : DT_FP32_EXACT, &ba.ds_ws));
     DT_TRY(bf ? launch_flash_bwd_bf16(ba, s) : launch_flash_bwd_f32(ba, s));
     // steps 3-4 (:234-244): RoPE backward and the q/k norms' backward, in place on dq | dk
     NormRopeBwdArgs nb{dq, dq + dm * esz, pre, pre + dm * esz, rms, rms + rows, L->q_norm, L->k_norm,

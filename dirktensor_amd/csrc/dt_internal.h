@@ -90,12 +90,27 @@ struct FlashBwdArgs {
     int ld_grad; // row stride of d_q, d_k and d_v
     float scale;
     int causal;
-    // bf16 mode: workspace for dS (flash_bwd_ds_bytes); when set, the dK/dV pass stores dS there and dQ is
-    // computed as dS K from it instead of recomputing S and dP. NULL: the recompute path.
+    // workspace for dS (flash_bwd_ds_bytes); when set, the dK/dV pass stores dS there and dQ is computed as
+    // dS K from it instead of recomputing S and dP. NULL: the recompute path.
     void* ds_ws = nullptr;
 };
 int launch_flash_bwd_prep(const FlashBwdArgs& a, int bf16, hipStream_t stream);  // fills delta and lse2
-size_t flash_bwd_ds_bytes(int B, int H, int T, int causal);  // bf16 dS workspace of one backward call
+// dS workspace of the backward's dS path: per (batch, head) and 128-key block kb, one block per 64-query
+// tile the keys can see (tiles 2*kb .. under causality, all otherwise), the tiles of one key block
+// consecutive. A block holds 128 keys x 64 queries of dS (16 KB in bf16, 32 KB in fp32).
+struct BwdDsLayout {
+    int nqt, nkb, causal;
+    __host__ __device__ BwdDsLayout(int T, int causal_) : nqt((T + 63) / 64), nkb((T + 127) / 128), causal(causal_) {}
+    __host__ __device__ int first_tile(int kb) const { return causal ? 2 * kb : 0; }
+    __host__ __device__ int64_t block_offset(int kb) const {  // blocks before key block kb's, in one (batch, head)
+        return (int64_t)kb * nqt - (causal ? (int64_t)kb * (kb - 1) : 0);
+    }
+    __host__ __device__ int64_t per_head() const { return block_offset(nkb); }
+};
+// bytes of the dS workspace of one backward call; elem_bytes 2 (bf16 mode) or 4 (fp32 exact mode)
+inline size_t flash_bwd_ds_bytes(int B, int H, int T, int causal, int elem_bytes) {
+    return (size_t)B * H * (size_t)BwdDsLayout(T, causal).per_head() * (size_t)(128 * 64 * elem_bytes);
+}
 int launch_flash_bwd_bf16(const FlashBwdArgs& a, hipStream_t stream);
 int launch_flash_bwd_f32(const FlashBwdArgs& a, hipStream_t stream);
 

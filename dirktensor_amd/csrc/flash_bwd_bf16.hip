@@ -83,15 +83,6 @@ constexpr int kDsRowBytes = 128;
 constexpr int kDsBlockBytes = kBlk * kDsRowBytes;  // 16 KB
 constexpr int kDsHalfBytes = kTile * kDsRowBytes;  // the rows of one 64-key tile: 8 KB
 
-struct DsLayout {
-    int nqt, nkb, causal;
-    __host__ __device__ DsLayout(int T, int causal_) : nqt((T + kTile - 1) / kTile), nkb((T + kBlk - 1) / kBlk), causal(causal_) {}
-    __host__ __device__ int first_tile(int kb) const { return causal ? 2 * kb : 0; }
-    __host__ __device__ int64_t block_offset(int kb) const {  // blocks before key block kb's, in one (batch, head)
-        return (int64_t)kb * nqt - (causal ? (int64_t)kb * (kb - 1) : 0);
-    }
-    __host__ __device__ int64_t per_head() const { return block_offset(nkb); }
-};
 
 __device__ __forceinline__ uint32_t pack_bf16x2(float lo, float hi) {
     bf16x2 r = __builtin_convertvector((floatx2){lo, hi}, bf16x2);
@@ -291,7 +282,7 @@ __device__ __forceinline__ void dkdv_block(const FlashBwdArgs& a, int kb_own, in
         // dS stores: this key block's blocks of the workspace; lane row 32*wave + ln, chunk (4*qb + 2*u + hh) ^ xs
         const __amdgpu_buffer_rsrc_t ds_rsrc = [&] {
             if constexpr (kEmitDs) {
-                const DsLayout lay(T, a.causal);
+                const BwdDsLayout lay(T, a.causal);
                 const uint8_t* base = static_cast<const uint8_t*>(a.ds_ws) +
                                       (uint64_t)(bh * lay.per_head() + lay.block_offset(kb)) * kDsBlockBytes;
                 return make_rsrc(base, (uint32_t)n_steps * kDsBlockBytes);
@@ -575,7 +566,7 @@ __device__ __forceinline__ void dq_ds_block(const FlashBwdArgs& a, int qb_own, i
     }
     const uint16_t* Kg = static_cast<const uint16_t*>(a.k) + (int64_t)b * T * a.ld_qkv + (int64_t)h * kD;
     uint16_t* dQg = static_cast<uint16_t*>(a.d_q) + (int64_t)b * T * a.ld_grad + (int64_t)h * kD;
-    const DsLayout lay(T, a.causal);
+    const BwdDsLayout lay(T, a.causal);
     const uint8_t* ds_head = static_cast<const uint8_t*>(a.ds_ws) + (uint64_t)(bh * lay.per_head()) * kDsBlockBytes;
 
     const int qw = qb_own * kBlk + 32 * wq;  // the wave's first query
@@ -748,10 +739,6 @@ int launch_flash_bwd_bf16(const FlashBwdArgs& a, hipStream_t stream) {
         }
     }
     return DT_OK;
-}
-
-size_t flash_bwd_ds_bytes(int B, int H, int T, int causal) {
-    return (size_t)B * H * (size_t)DsLayout(T, causal).per_head() * kDsBlockBytes;
 }
 
 }  // namespace dt

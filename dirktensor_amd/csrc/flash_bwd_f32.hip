@@ -10,7 +10,9 @@
 // Each gradient row has a single owner, so no atomics; S and dP are computed
 // in both kernels. Each workgroup owns one block; the grid lists the blocks in
 // decreasing causal cost, so the hardware's first-free-CU dispatch runs the
-// longest blocks first.
+// longest blocks first. With more than one block per CU and pass the dS path
+// replaces the dQ kernel: the dK/dV kernel also stores dS (fp32) and
+// flash_bwd_dq_ds forms dQ = dS K from it (5 products per tile pair instead of 7).
 //
 // v_mfma_f32_32x32x2_f32 takes one A value per lane (row l%32, k = l/32) and
 // one B value (column l%32, k = l/32). For the products over the head
@@ -228,7 +230,16 @@ struct DkdvStage {
     float delta[kTile];
 };
 
-// dK and dV of key block kb_own of (batch, head) bh
+// dS workspace blocks (the dS path): 128 key rows of 256 bytes (the 64 queries of a query tile); 16-byte
+// chunk c of a row holds queries 4c .. 4c+3 (one dK/dV lane's four consecutive accumulator rows) and sits at
+// position c ^ (8 * ((row >> 2) & 1)), so the dQ pass's reads of rows r and r + 4 (its two lane halves)
+// fall in different banks.
+constexpr int kDsRowBytes = 256;
+constexpr int kDsBlockBytes = kBlk * kDsRowBytes;  // 32 KB
+constexpr int kDsHalfBytes = kTile * kDsRowBytes;  // the rows of one 64-key tile: 16 KB
+
+// dK and dV of key block kb_own of (batch, head) bh; kEmitDs: also dS -> the dS workspace
+template <bool kEmitDs>
 __device__ __forceinline__ void dkdv_block(const FlashBwdArgs& a, int kb_own, int bh, DkdvStage (&stg)[2]) {
     const int tid = threadIdx.x;
     const int lane = tid & 63;
@@ -266,6 +277,15 @@ __device__ __forceinline__ void dkdv_block(const FlashBwdArgs& a, int kb_own, in
         const int n_steps = (T - q_begin + kTile - 1) / kTile;
         fetch(stg[0], q_begin);  // both stages are free: the previous block ended with a barrier
 
+        // dS stores: this key block's blocks of the workspace; lane row 32*wave + ln
+        uint8_t* ds_base = nullptr;
+        if constexpr (kEmitDs) {
+            const BwdDsLayout lay(T, a.causal);
+            ds_base = static_cast<uint8_t*>(a.ds_ws) + (uint64_t)(bh * lay.per_head() + lay.block_offset(kb)) * kDsBlockBytes;
+        }
+        const int ds_row = (32 * wave + ln) * kDsRowBytes;
+        const int ds_xs = 8 * ((ln >> 2) & 1);
+
         float kf[64], vf[64];
         load_half_row(kf, Kg, key, T, a.ld_qkv, hh);
         load_half_row(vf, Vg, key, T, a.ld_qkv, hh);
@@ -281,7 +301,9 @@ __device__ __forceinline__ void dkdv_block(const FlashBwdArgs& a, int kb_own, in
             const DkdvStage& s = stg[it & 1];
             if (it + 1 < n_steps) fetch(stg[(it + 1) & 1], q0 + kTile);
             if (!(a.causal && q0 + kTile - 1 < kw)) {
-                const bool need_mask = a.causal && q0 < kw + 31;
+                // (the dQ pass never reads the dS of a skipped tile and wave: all of it is masked); with dS
+                // stored, keys past T are masked too (their dS would otherwise be exp2(-lse2) (-delta))
+                const bool need_mask = (a.causal && q0 < kw + 31) || (kEmitDs && kw + 31 >= T);
                 floatx16 sc[2], dp[2];
                 // S = Q K^T (raw), dP = dO V^T (two query blocks; explicit calls keep every index static)
                 dot_rows2(sc[0], dp[0], s.q, s.g, 0, ln, hh, kf, vf);
@@ -293,10 +315,23 @@ __device__ __forceinline__ void dkdv_block(const FlashBwdArgs& a, int kb_own, in
                     for (int i = 0; i < 16; ++i) {
                         const int qi = 32 * qb + 8 * (i / 4) + 4 * hh + (i % 4);
                         float pv = __builtin_amdgcn_exp2f(sc[qb][i] * c - s.lse2[qi]);
-                        if (need_mask && key > q0 + qi) pv = 0.0f;
+                        if constexpr (kEmitDs) {
+                            if (need_mask && key > (a.causal ? min(q0 + qi, T - 1) : T - 1)) pv = 0.0f;
+                        } else {
+                            if (need_mask && key > q0 + qi) pv = 0.0f;
+                        }
                         sc[qb][i] = pv;
                         dp[qb][i] = pv * (dp[qb][i] - s.delta[qi]);
                     }
+                if constexpr (kEmitDs) {  // dS: chunk 8*qb + 2*g + hh of the lane's key row
+                    uint8_t* blk = ds_base + (size_t)(it * kDsBlockBytes);
+#pragma unroll
+                    for (int qb = 0; qb < 2; ++qb)
+#pragma unroll
+                        for (int g = 0; g < 4; ++g)
+                            *reinterpret_cast<float4*>(blk + ds_row + (((8 * qb + 2 * g + hh) ^ ds_xs) << 4)) =
+                                make_float4(dp[qb][4 * g], dp[qb][4 * g + 1], dp[qb][4 * g + 2], dp[qb][4 * g + 3]);
+                }
                 acc_cols(dv, s.g, ln, hh, sc);  // dV^T += dO^T P
                 acc_cols(dk, s.q, ln, hh, dp);  // dK^T += Q^T dS
             }
@@ -387,6 +422,88 @@ __device__ __forceinline__ void dq_block(const FlashBwdArgs& a, int qb_own, int 
     }
 }
 
+// ------------------------------------------------------------------------------------------------ dQ from dS
+// LDS stage: a 64-key tile of K and the dS rows of those keys for the block's two 64-query tiles
+struct DsqStage {
+    uint8_t k[kTileBytes];
+    uint8_t ds[2][kDsHalfBytes];
+};
+
+// dQ of query block qb_own of (batch, head) bh from the dS the dK/dV pass stored: per 64-key tile
+// dQ^T += K^T dS^T, the A operand from the K tile as in acc_cols and the B operand (one key and query per
+// lane and step) read from the dS tile.
+__device__ __forceinline__ void dq_ds_block(const FlashBwdArgs& a, int qb_own, int bh, DsqStage (&stg)[2]) {
+    const int tid = threadIdx.x;
+    const int lane = tid & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+    const int ln = lane & 31;
+    const int hh = lane >> 5;
+    const int T = a.T;
+    const int b = bh / a.H, h = bh % a.H;
+    const float* Kg = static_cast<const float*>(a.k) + (int64_t)b * T * a.ld_qkv + (int64_t)h * kD;
+    float* dQg = static_cast<float*>(a.d_q) + (int64_t)b * T * a.ld_grad + (int64_t)h * kD;
+    const BwdDsLayout lay(T, a.causal);
+    const uint8_t* ds_head = static_cast<const uint8_t*>(a.ds_ws) + (uint64_t)(bh * lay.per_head()) * kDsBlockBytes;
+
+    const int qw = qb_own * kBlk + 32 * wave;  // the wave's first query
+    const int q = qw + ln;
+    const int qt0 = 2 * qb_own;                // the block's first 64-query tile
+    const int n_qt = min(2, lay.nqt - qt0);
+    const int k_end = a.causal ? min(qb_own * kBlk + kBlk, T) : T;
+    const int n_steps = (k_end + kTile - 1) / kTile;
+
+    // K rows k0 .. k0+63 and their dS rows of the block's query tiles -> stage s (the dS rows as stored:
+    // instruction n of wave w moves 1 KB of each 16 KB half)
+    auto fetch = [&](DsqStage& s, int k0) {
+        dma_tile(s.k, Kg, k0, T, a.ld_qkv, lane, wave);
+        const int kb = k0 / kBlk;
+        const uint8_t* blk = ds_head + (uint64_t)(lay.block_offset(kb) + (qt0 - lay.first_tile(kb))) * kDsBlockBytes;
+        const __amdgpu_buffer_rsrc_t r = make_rsrc(blk, (uint32_t)n_qt * kDsBlockBytes);
+        const uint32_t rows = (uint32_t)((k0 / kTile) & 1) * kDsHalfBytes;  // this tile's rows of the key block
+#pragma unroll
+        for (int t = 0; t < 2; ++t)
+#pragma unroll
+            for (int n = 0; n < 4; ++n) {
+                const uint32_t chunk = (uint32_t)((n * 4 + wave) * 64);  // 16-byte chunks of a 16 KB half
+                dma16(__builtin_amdgcn_readfirstlane(lds_addr(s.ds[t] + chunk * 16)),
+                      (uint32_t)t * kDsBlockBytes + rows + (chunk + (uint32_t)lane) * 16u, r);
+            }
+    };
+
+    // the B operand of step t (t = 16*blk + i): dS of key row 32*blk + 8*(i/4) + 4*hh + i%4 and this lane's
+    // query (column 32*(wave & 1) + ln of query tile wave / 2); that row's (row >> 2) & 1 is hh, so the
+    // chunk's position is a constant of the lane
+    const int qcol = 32 * (wave & 1) + ln;
+    const int ds_lane = (wave >> 1) * kDsHalfBytes + 4 * hh * kDsRowBytes + (((qcol >> 2) ^ (8 * hh)) << 4) + 4 * (qcol & 3);
+    floatx16 dq[4];
+#pragma unroll
+    for (int db = 0; db < 4; ++db) dq[db] = zero16();
+
+    fetch(stg[0], 0);
+    stage_barrier();
+    for (int it = 0; it < n_steps; ++it) {
+        const int k0 = it * kTile;
+        const DsqStage& s = stg[it & 1];
+        if (it + 1 < n_steps) fetch(stg[(it + 1) & 1], k0 + kTile);
+        if (q - ln < T && !(a.causal && k0 > qw + 31)) {
+            // the second 32 keys are all after the wave's queries under causality: their dS was not stored
+            const bool second = !a.causal || k0 + 32 <= qw + 31;
+            floatx16 w[2];
+#pragma unroll
+            for (int blk = 0; blk < 2; ++blk)
+#pragma unroll
+                for (int i = 0; i < 16; ++i) {
+                    const int r = 32 * blk + 8 * (i / 4) + (i % 4);  // the key row without the lane half
+                    const float x = *reinterpret_cast<const float*>(s.ds[0] + ds_lane + r * kDsRowBytes);
+                    w[blk][i] = (blk == 0 || second) ? x : 0.0f;
+                }
+            acc_cols(dq, s.k, ln, hh, w);  // dQ^T += K^T dS^T
+        }
+        stage_barrier();  // stage it&1 is free for the tile after next; tile it+1 has landed
+    }
+    if (q < T) store_rows(dQg, q, a.ld_grad, hh, dq, a.scale);
+}
+
 // One 128-row block per workgroup, listed in decreasing causal cost, so that the hardware, which hands
 // the next workgroup to the first CU that frees up, runs a longest-first schedule.
 // pass = 0 (dK/dV) or 1 (dQ): one pass per launch; workgroup BH*j + bh takes, for (batch, head) bh,
@@ -406,8 +523,22 @@ __global__ __launch_bounds__(kThreads, 1) void flash_bwd_f32_kernel(FlashBwdArgs
     const int j = (int)blockIdx.x / (pass == 2 ? 2 * BH : BH);
     const int kind = pass == 2 ? ((int)blockIdx.x / BH) & 1 : pass;
     const int bh = (int)blockIdx.x % BH;
-    if (kind == 0) dkdv_block(a, j, bh, lds.kv);
+    if (kind == 0) dkdv_block<false>(a, j, bh, lds.kv);
     else dq_block(a, n - 1 - j, bh, lds.q);
+}
+
+// The dS path: the dK/dV pass (workgroup BH*j + bh: key block j) storing dS, then dQ = dS K (workgroup
+// BH*j + bh: query block n-1-j), both in decreasing causal cost.
+__global__ __launch_bounds__(kThreads, 1) void flash_bwd_dkdv_ds_f32_kernel(FlashBwdArgs a) {
+    __shared__ __attribute__((aligned(1024))) DkdvStage st[2];
+    const int BH = a.B * a.H;
+    dkdv_block<true>(a, (int)blockIdx.x / BH, (int)blockIdx.x % BH, st);
+}
+__global__ __launch_bounds__(kThreads, 1) void flash_bwd_dq_ds_f32_kernel(FlashBwdArgs a) {
+    __shared__ __attribute__((aligned(1024))) DsqStage st[2];
+    const int BH = a.B * a.H;
+    const int n = (a.T + kBlk - 1) / kBlk;
+    dq_ds_block(a, n - 1 - (int)blockIdx.x / BH, (int)blockIdx.x % BH, st);
 }
 
 }  // namespace
@@ -419,6 +550,13 @@ int launch_flash_bwd_f32(const FlashBwdArgs& a, hipStream_t stream) {
     DT_TRY(launch_flash_bwd_prep(a, 0, stream));
     const int64_t blocks = (int64_t)((a.T + kBlk - 1) / kBlk) * a.B * a.H;  // per pass, one per workgroup
     if (2 * blocks > 0x7fffffff) return set_error(DT_ERR_UNSUPPORTED, "too many workgroups");
+    if (a.ds_ws) {  // dS stored by the dK/dV pass, dQ = dS K
+        hipLaunchKernelGGL(flash_bwd_dkdv_ds_f32_kernel, dim3((unsigned)blocks), dim3(kThreads), 0, stream, a);
+        DT_HIP_TRY(hipGetLastError());
+        hipLaunchKernelGGL(flash_bwd_dq_ds_f32_kernel, dim3((unsigned)blocks), dim3(kThreads), 0, stream, a);
+        DT_HIP_TRY(hipGetLastError());
+        return DT_OK;
+    }
     int cus = 0;
     DT_TRY(persistent_grid(0x7fffffff, &cus));
     if (blocks <= cus) {  // the passes share one launch (at most one block per CU and pass)

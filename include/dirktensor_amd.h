@@ -100,15 +100,16 @@ int dt_ctx_destroy(dt_ctx* ctx);
  *                     (up to 16, into a scratch output; synchronises the
  *                     stream once) and keeps the fastest whose repeated run
  *                     is bit-identical; 0: the first heuristic choice.
- *   DT_OPT_BWD_DQ     how the DT_BF16 attention backward (dt_flash_attn_bwd,
+ *   DT_OPT_BWD_DQ     how the attention backward (dt_flash_attn_bwd,
  *                     dt_attn_layer_bwd, the model backward) forms dQ
- *                     (FlashAttention.cpp:185-359):
+ *                     (FlashAttention.cpp:185-359), in both modes:
  *                     DT_BWD_DQ_RECOMPUTE  the dQ pass recomputes S and dP
  *                                          (no workspace);
- *                     DT_BWD_DQ_FROM_DS    the dK/dV pass stores dS (bf16,
- *                                          B*H*T*(T+128)/2 * 2 bytes causal,
- *                                          B*H*T*T*2 otherwise, a context
- *                                          buffer) and dQ = dS K reads it;
+ *                     DT_BWD_DQ_FROM_DS    the dK/dV pass stores dS in the
+ *                                          mode's dtype (B*H*T*(T+128)/2
+ *                                          values causal, B*H*T*T otherwise,
+ *                                          a context buffer) and dQ = dS K
+ *                                          reads it;
  *                     DT_BWD_DQ_AUTO       (default) the dS path where it
  *                                          measured faster (more than one
  *                                          128-row block per CU and pass),

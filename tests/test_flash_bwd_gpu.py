@@ -104,7 +104,7 @@ def test_bwd_deterministic(gpu):
     assert all(np.array_equal(x, y) for x, y in zip(a, b))
 
 
-# The dS path (DT_OPT_BWD_DQ = DT_BWD_DQ_FROM_DS): the dK/dV pass stores dS (bf16) in a context buffer and
+# The dS path (DT_OPT_BWD_DQ = DT_BWD_DQ_FROM_DS): the dK/dV pass stores dS in a context buffer and
 # dQ = dS K reads it, on a context that selects it for every shape.
 @pytest.fixture(scope="module")
 def ds_ctx(gpu):
@@ -124,44 +124,51 @@ def recompute_ctx(gpu):
     return ctx
 
 
-def gpu_bwd_ctx(inputs, dev, ctx, causal=True):
+def gpu_bwd_ctx(inputs, ctx, mode, causal=True):
     Q, K, V, G, O, m, l = inputs
-    q, k, v, g, o = (torch.from_numpy(x).to(dev).to(torch.bfloat16) for x in (Q, K, V, G, O))
-    mm, ll = (torch.from_numpy(x).to(dev) for x in (m, l))
+    tdt = torch.float32 if mode == "fp32" else torch.bfloat16
+    q, k, v, g, o = (torch.from_numpy(x).to("cuda").to(tdt) for x in (Q, K, V, G, O))
+    mm, ll = (torch.from_numpy(x).to("cuda") for x in (m, l))
     r = flash_attention_backward(g, o, mm, ll, q, k, v, SCALE, causal, ctx=ctx)
     torch.cuda.synchronize()
     return to_np(r.d_Q), to_np(r.d_K), to_np(r.d_V)
 
 
+@pytest.mark.parametrize("mode", ["fp32", "bf16"])
 @pytest.mark.parametrize("B,T,H", [(1, 1, 1), (1, 2, 3), (2, 33, 2), (1, 64, 16), (1, 100, 5), (1, 127, 1),
                                    (2, 128, 2), (1, 129, 3), (1, 255, 2), (1, 257, 4), (3, 500, 2), (1, 1000, 1)])
-def test_bwd_ds_path_shapes(ds_ctx, B, T, H):
-    inputs, ref = case(B, T, H, 300 + T, "bf16")
-    check(gpu_bwd_ctx(inputs, "cuda", ds_ctx), ref, TOL_BF16, f"dS path B={B} T={T} H={H}")
+def test_bwd_ds_path_shapes(ds_ctx, mode, B, T, H):
+    inputs, ref = case(B, T, H, 300 + T, mode)
+    check(gpu_bwd_ctx(inputs, ds_ctx, mode), ref, TOL_FP32 if mode == "fp32" else TOL_BF16,
+          f"dS path {mode} B={B} T={T} H={H}")
 
 
+@pytest.mark.parametrize("mode", ["fp32", "bf16"])
 @pytest.mark.parametrize("T", [1, 64, 129, 300])
-def test_bwd_ds_path_full_attention(ds_ctx, T):
-    inputs, ref = case(2, T, 3, 700 + T, "bf16", causal=False)
-    check(gpu_bwd_ctx(inputs, "cuda", ds_ctx, causal=False), ref, TOL_BF16, f"dS path full T={T}")
+def test_bwd_ds_path_full_attention(ds_ctx, mode, T):
+    inputs, ref = case(2, T, 3, 700 + T, mode, causal=False)
+    check(gpu_bwd_ctx(inputs, ds_ctx, mode, causal=False), ref, TOL_FP32 if mode == "fp32" else TOL_BF16,
+          f"dS path {mode} full T={T}")
 
 
+@pytest.mark.parametrize("mode", ["fp32", "bf16"])
 @pytest.mark.parametrize("T", [2048, 4096])
-def test_bwd_ds_path_long_context(ds_ctx, T):
-    inputs, ref = case(1, T, 16, 1001, "bf16")
-    check(gpu_bwd_ctx(inputs, "cuda", ds_ctx), ref, TOL_BF16, f"dS path T={T}")
+def test_bwd_ds_path_long_context(ds_ctx, mode, T):
+    inputs, ref = case(1, T, 16, 1001, mode)
+    check(gpu_bwd_ctx(inputs, ds_ctx, mode), ref, TOL_FP32 if mode == "fp32" else TOL_BF16, f"dS path {mode} T={T}")
 
 
+@pytest.mark.parametrize("mode", ["fp32", "bf16"])
 @pytest.mark.parametrize("B,T,H,causal", [(1, 1000, 4, True), (2, 300, 3, False), (1, 4096, 16, True)])
-def test_bwd_ds_path_against_recompute(ds_ctx, recompute_ctx, B, T, H, causal):
-    """dK and dV come from the same kernel code on both paths (bit-identical); dQ sums the same bf16 dS
-    values times K in another order; the dS path is deterministic like the other."""
-    inputs, _ = case(B, T, H, 1401 + T, "bf16", causal=causal)
-    a = gpu_bwd_ctx(inputs, "cuda", ds_ctx, causal)
-    b = gpu_bwd_ctx(inputs, "cuda", recompute_ctx, causal)
-    a2 = gpu_bwd_ctx(inputs, "cuda", ds_ctx, causal)
+def test_bwd_ds_path_against_recompute(ds_ctx, recompute_ctx, mode, B, T, H, causal):
+    """dK and dV come from the same kernel code on both paths (bit-identical); dQ sums the same dS values
+    times K (bf16: in another order); the dS path is deterministic like the other."""
+    inputs, _ = case(B, T, H, 1401 + T, mode, causal=causal)
+    a = gpu_bwd_ctx(inputs, ds_ctx, mode, causal)
+    b = gpu_bwd_ctx(inputs, recompute_ctx, mode, causal)
+    a2 = gpu_bwd_ctx(inputs, ds_ctx, mode, causal)
     assert all(np.array_equal(x, y) for x, y in zip(a, a2)), "dS path not deterministic"
     assert np.array_equal(a[1], b[1]) and np.array_equal(a[2], b[2]), "dK / dV differ between the paths"
     err = rel_err(a[0], b[0])
-    print(f"B={B} T={T} H={H} causal={causal}: dQ dS path vs recompute {err:.3e}")
-    assert err <= 4e-3
+    print(f"{mode} B={B} T={T} H={H} causal={causal}: dQ dS path vs recompute {err:.3e}")
+    assert err <= (1e-5 if mode == "fp32" else 4e-3)
