@@ -75,6 +75,7 @@ typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
 typedef __bf16 bf16x2 __attribute__((ext_vector_type(2)));
 typedef float floatx2 __attribute__((ext_vector_type(2)));
 typedef short shortx4 __attribute__((ext_vector_type(4)));
+typedef unsigned int u32x4 __attribute__((ext_vector_type(4)));
 typedef short shortx8 __attribute__((ext_vector_type(8)));
 typedef __attribute__((address_space(3))) shortx4 lds_shortx4;
 typedef __attribute__((address_space(3))) void lds_void;
@@ -583,7 +584,10 @@ __global__ __launch_bounds__(kThreads, 1) void flash_fwd_bf16_kernel(FlashArgs a
                 const int ch = j * kThreads + tid;  // 16-byte chunk ch % 16 of row ch / 16
                 const int r = ch >> 4, c = ch & 15;
                 const uint4 w = *reinterpret_cast<const uint4*>(obuf + r * kObufRow + 16 * c);
-                if (r < nrows) *reinterpret_cast<uint4*>(&Og[(int64_t)(q0 + r) * a.ldo + 8 * c]) = w;
+                // streaming (non-temporal) stores: whole 256-byte rows this kernel never reads back
+                if (r < nrows)
+                    __builtin_nontemporal_store((u32x4){w.x, w.y, w.z, w.w},
+                                                reinterpret_cast<u32x4*>(&Og[(int64_t)(q0 + r) * a.ldo + 8 * c]));
             }
         }
         if (u.parts > 1) {  // the same for every wave of the workgroup
