@@ -13,17 +13,20 @@
 //     one per CU) takes tile w, w+G, ... With G a multiple of 8 and 3H a multiple of 8, workgroup w
 //     runs on XCD w mod 8 and every tile of a column block runs on one XCD, so each block of W passes
 //     through one L2.
-//   * 8 waves in two groups of 4; the groups split the k-tiles (group g takes k-tiles g, g+2, ...) and
-//     their partial sums are added at the end. Wave (wr, wc) of a group computes rows 64wr..+64 and
-//     columns 64wc..+64 of the tile as 2 x 2 blocks of v_mfma_f32_32x32x16_bf16 (fp32 exact mode:
-//     v_mfma_f32_32x32x2f32), A = rows of x, B = rows of W, both read along K.
-//   * The k-tiles (128 bytes of K per row: 64 bf16 or 32 fp32) move from HBM into LDS with
-//     buffer_load ... lds, double-buffered per group; a wave's 8 DMA instructions for the next k-tile are
-//     spread over the current step's MFMAs; the descriptors of x end at the last valid row,
-//     so rows past it arrive as zeros. LDS rows are 128 bytes, the 16-byte chunk c of row r stored at
-//     position c ^ ((r >> 1) & 7), so the 16 rows a fragment read touches per cycle hit distinct banks.
+//   * 8 waves share every k-tile: wave (wr, wc) = (w / 2, w % 2) computes rows 32wr..+32 and columns
+//     64wc..+64 of the tile as 1 x 2 blocks of v_mfma_f32_32x32x16_bf16 (fp32 exact mode:
+//     v_mfma_f32_32x32x2f32), A = rows of x, B = rows of W, both read along K; every output element
+//     has one owner.
+//   * The k-tiles (128 bytes of K per row: 64 bf16 or 32 fp32; 32 KB per k-tile for x and W) move from
+//     HBM into LDS with buffer_load ... lds through a five-stage ring (all 160 KB), four k-tiles ahead of
+//     the one in use: with one k-tile of lookahead a workgroup waited on memory latency. A wave's 4 DMA
+//     instructions per k-tile are spread over the current step's MFMAs; past the last k-tile they go out
+//     with empty descriptors (nothing is read), so the count of requests in flight is fixed. The
+//     descriptors of x end at the last valid row, so rows past it arrive as zeros. LDS rows are 128
+//     bytes, the 16-byte chunk c of row r stored at position c ^ ((r >> 1) & 7), so the 16 rows a
+//     fragment read touches per cycle hit distinct banks.
 //
-// Epilogue of a tile: both groups' fp32 partial tiles go to LDS; each thread then owns 16 columns and
+// Epilogue of a tile: the fp32 tile goes to LDS; each thread then owns 16 columns and
 // their rotate-half partners (d, d+64) of one row. A q or k tile computes its rows' sums of squares
 // over the head's 128 columns and publishes them; the H tiles of the same row block and tensor run in
 // the same round on different workgroups (the grid is at most one workgroup per CU, so every workgroup is
@@ -55,9 +58,11 @@ constexpr int kTile = 128;               // rows and columns of a work tile
 constexpr int kThreads = 512;            // 8 waves
 constexpr int kRowB = 128;               // bytes of K per LDS row of a k-tile
 constexpr int kOpBytes = kTile * kRowB;  // 16 KB: one operand's k-tile
-constexpr int kRStride = 132;            // floats per row of an fp32 tile in the epilogue
-constexpr int kLdsBytes = 2 * kTile * kRStride * 4;  // two fp32 tiles; holds 2 stages x 2 groups x 2 operands
-static_assert(kLdsBytes >= 8 * kOpBytes, "the epilogue tiles must cover the stages");
+constexpr int kStages = 5;               // LDS ring of k-tiles (x and W), four ahead of the one in use
+constexpr int kStageBytes = 2 * kOpBytes;
+constexpr int kRStride = 132;            // floats per row of the fp32 tile in the epilogue
+constexpr int kLdsBytes = kStages * kStageBytes;  // 160 KB
+static_assert(kLdsBytes >= kTile * kRStride * 4, "the stages must hold the epilogue tile");
 constexpr int kBufferDword3 = 0x00020000;  // raw buffer, 32-bit data format (gfx9 family)
 constexpr int kCoherent = 16;              // cache policy sc1: device-scope coherent access
 constexpr int kSpinLimit = 1 << 20;        // polls (coherent loads and s_sleep 1, ~1 s in all) before a wait gives up
@@ -81,9 +86,11 @@ __device__ __forceinline__ void static_for(F&& f) {
 }
 #define DT_BUNDLE_END __builtin_amdgcn_sched_barrier(0)
 
-// Barrier for the double-buffered loop: this wave's LDS DMA and LDS reads are complete before any wave
-// passes it.
+// This wave's LDS DMA and LDS reads are complete before any wave passes it.
 __device__ __forceinline__ void stage_barrier() { asm volatile("s_waitcnt vmcnt(0) lgkmcnt(0)\n\ts_barrier" ::: "memory"); }
+// The ring's barrier: the k-tile after the one just used has landed (this wave's requests for the three after
+// it, twelve instructions, may still be in flight) and every wave is done reading the stage just used.
+__device__ __forceinline__ void ring_barrier() { asm volatile("s_waitcnt vmcnt(12) lgkmcnt(0)\n\ts_barrier" ::: "memory"); }
 
 __device__ __forceinline__ uint4 lds_read16(const uint8_t* p) { return *reinterpret_cast<const uint4*>(p); }
 
@@ -100,41 +107,45 @@ __device__ __forceinline__ void dma16(uint32_t lds, uint32_t voff, __amdgpu_buff
     asm volatile("s_nop 4\n\tbuffer_load_dwordx4 %0, %1, 0 offen lds" ::"v"(voff), "s"(r), "{m0}"(lds) : "memory");
 }
 
-// One k-tile (128 bytes of K) for one wave: acc[i][j] += A_i B_j^T over the tile, A_i = rows 32i + ln of the
-// wave's x band, B_j = rows 32j + ln of its W band. The 16-byte chunk kk of a row pair (2kk + hh) feeds
-// one bf16 MFMA (k 16) or four fp32 MFMAs (k 2 each; lanes hh = 0 and 1 hold k 8kk + e and 8kk + 4 + e).
-// Fragments go through a three-deep ring of chunks: bundle (kk, m) reads fragment m of chunk kk + 2, so
-// every fragment is requested at least five bundles before its MFMA. hook(slot) runs at the start of each
-// of the 16 bundles (the caller's memory requests, spread over the step).
+// One k-tile (128 bytes of K) for one wave: acc[j] += A B_j^T over the tile, A = rows ln of the wave's 32-row
+// x band, B_j = rows 32j + ln of its 64-row W band. The 16-byte chunk kk of a row pair (2kk + hh) feeds one
+// bf16 MFMA (k 16) or four fp32 MFMAs (k 2 each; lanes hh = 0 and 1 hold k 8kk + e and 8kk + 4 + e).
+// Fragments go through a three-deep ring of chunks: bundle (kk, j) reads fragment(s) of chunk kk + 2, so every
+// fragment is requested at least three bundles before its MFMA. hook(slot) runs at the start of each of the 8
+// bundles (the caller's memory requests, spread over the step).
 template <bool kF32, typename Hook>
-__device__ __forceinline__ void tile_step(floatx16 (&acc)[2][2], const uint8_t* As, const uint8_t* Bs,
+__device__ __forceinline__ void tile_step(floatx16 (&acc)[2], const uint8_t* As, const uint8_t* Bs,
                                           const uint32_t (&coff)[4], Hook&& hook) {
-    uint4 fr[3][4];  // [chunk % 3][a0, a1, b0, b1]
-    auto rd = [&](int c, int m) {
-        return m < 2 ? lds_read16(As + 4096 * m + coff[c]) : lds_read16(Bs + 4096 * (m - 2) + coff[c]);
-    };
+    uint4 fr[3][3];  // [chunk % 3][a, b0, b1]
+    auto rd = [&](int c, int m) { return m == 0 ? lds_read16(As + coff[c]) : lds_read16(Bs + 4096 * (m - 1) + coff[c]); };
 #pragma unroll
-    for (int m = 0; m < 4; ++m) fr[0][m] = rd(0, m);
+    for (int m = 0; m < 3; ++m) fr[0][m] = rd(0, m);
 #pragma unroll
-    for (int m = 0; m < 4; ++m) fr[1][m] = rd(1, m);
+    for (int m = 0; m < 3; ++m) fr[1][m] = rd(1, m);
     static_for<4>([&](auto KK) {
         constexpr int kk = decltype(KK)::value;
-        static_for<4>([&](auto M) {
-            constexpr int m = decltype(M)::value;  // MFMA block (i, j) = (m >> 1, m & 1)
-            constexpr int i = m >> 1, j = m & 1;
-            hook(std::integral_constant<int, 4 * kk + m>{});
-            if constexpr (kk + 2 < 4) fr[(kk + 2) % 3][m] = rd(kk + 2, m);
-            const uint4 fa = fr[kk % 3][i], fb = fr[kk % 3][2 + j];
+        static_for<2>([&](auto J) {
+            constexpr int j = decltype(J)::value;
+            hook(std::integral_constant<int, 2 * kk + j>{});
+            if constexpr (kk + 2 < 4) {
+                if constexpr (j == 0) {
+                    fr[(kk + 2) % 3][0] = rd(kk + 2, 0);
+                    fr[(kk + 2) % 3][1] = rd(kk + 2, 1);
+                } else {
+                    fr[(kk + 2) % 3][2] = rd(kk + 2, 2);
+                }
+            }
+            const uint4 fa = fr[kk % 3][0], fb = fr[kk % 3][1 + j];
             if constexpr (kF32) {
-                const floatx4 a = __builtin_bit_cast(floatx4, fa);
-                const floatx4 b = __builtin_bit_cast(floatx4, fb);
+                const floatx4 av = __builtin_bit_cast(floatx4, fa);
+                const floatx4 bv = __builtin_bit_cast(floatx4, fb);
                 static_for<4>([&](auto E) {
                     constexpr int e = decltype(E)::value;
-                    acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x2f32(a[e], b[e], acc[i][j], 0, 0, 0);
+                    acc[j] = __builtin_amdgcn_mfma_f32_32x32x2f32(av[e], bv[e], acc[j], 0, 0, 0);
                 });
             } else {
-                acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(__builtin_bit_cast(bf16x8, fa),
-                                                                   __builtin_bit_cast(bf16x8, fb), acc[i][j], 0, 0, 0);
+                acc[j] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(__builtin_bit_cast(bf16x8, fa),
+                                                               __builtin_bit_cast(bf16x8, fb), acc[j], 0, 0, 0);
             }
             DT_BUNDLE_END;
         });
@@ -158,23 +169,21 @@ __global__ __launch_bounds__(kThreads, 1) void qkv_norm_rope_kernel(QkvArgs a) {
     const int tid = threadIdx.x;
     const int lane = tid & 63;
     const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
-    const int grp = wave >> 2;  // k-tile group
-    const int wv = wave & 3;
-    const int wr = wv >> 1, wc = wv & 1;  // the wave's 64-row band of x and 64-row band of W
+    const int wr = wave >> 1, wc = wave & 1;  // the wave's 32-row band of x and 64-row band of W
     const int ln = lane & 31, hh = lane >> 5;
     const int H = a.H, dm = H * 128, ncb = 3 * H;
-    const int nsteps = dm * es / kRowB / 2;  // k-tiles per group
+    const int nk = dm * es / kRowB;  // k-tiles
     const int n_tiles = (a.rows + kTile - 1) / kTile * ncb;
 
-    // DMA: instruction i of wave wv fills LDS rows 8*(4i + wv) .. +8 of an operand's k-tile (1 KB); lane -> row
-    // 8*(4i + wv) + lane/8 at chunk position lane%8, holding the global chunk (lane%8) ^ ((row >> 1) & 7), where
-    // (row >> 1) & 7 = (4*(wv & 1) + lane/16) & 7 does not depend on i
-    uint32_t offx[4], offw[4];
+    // DMA: instruction i of wave w fills LDS rows 8*(8i + w) .. +8 of an operand's k-tile (1 KB); lane -> row
+    // 8*(8i + w) + lane/8 at chunk position lane%8, holding the global chunk (lane%8) ^ ((row >> 1) & 7), where
+    // (row >> 1) & 7 = (4*(w & 1) + lane/16) & 7 does not depend on i
+    uint32_t offx[2], offw[2];
     {
-        const int gc = (lane & 7) ^ ((4 * (wv & 1) + (lane >> 4)) & 7);
+        const int gc = (lane & 7) ^ ((4 * (wave & 1) + (lane >> 4)) & 7);
 #pragma unroll
-        for (int i = 0; i < 4; ++i) {
-            const int r = 8 * (4 * i + wv) + (lane >> 3);
+        for (int i = 0; i < 2; ++i) {
+            const int r = 8 * (8 * i + wave) + (lane >> 3);
             offx[i] = (uint32_t)(r * a.ldx * es + 16 * gc);
             offw[i] = (uint32_t)(r * dm * es + 16 * gc);
         }
@@ -186,12 +195,11 @@ __global__ __launch_bounds__(kThreads, 1) void qkv_norm_rope_kernel(QkvArgs a) {
 #pragma unroll
         for (int kk = 0; kk < 4; ++kk) coff[kk] = (uint32_t)((((2 * kk + hh) ^ f)) * 16);
     }
-    const uint32_t arow = (uint32_t)((64 * wr + ln) * kRowB);
+    const uint32_t arow = (uint32_t)((32 * wr + ln) * kRowB);
     const uint32_t brow = (uint32_t)((64 * wc + ln) * kRowB);
 
     const __amdgpu_buffer_rsrc_t rss = make_rsrc(a.ss, (uint32_t)a.ss_bytes);
     float* const R0 = reinterpret_cast<float*>(lds);
-    float* const R1 = R0 + kTile * kRStride;
 
     for (int tile = blockIdx.x; tile < n_tiles; tile += gridDim.x) {
         const int rb = tile / ncb, cb = tile - rb * ncb;
@@ -203,67 +211,52 @@ __global__ __launch_bounds__(kThreads, 1) void qkv_norm_rope_kernel(QkvArgs a) {
         const uint32_t xbytes = (uint32_t)(nrows * a.ldx * es);
         const uint32_t wbytes = (uint32_t)(kTile * dm * es);
 
-        // k-tile kt of this group's x and W bands -> stage st (rows of x past the last arrive as zeros): DMA
-        // instruction q (0-3 x, 4-7 W) of this wave
-        auto dma_one = [&](int st, int kt, auto Q) {
+        // k-tile kt of x and W -> stage kt % kStages (rows of x past the last arrive as zeros): DMA instruction
+        // q (0-1 x, 2-3 W) of this wave; a k-tile past the last gets empty descriptors
+        auto dma_one = [&](int kt, auto Q) {
             constexpr int q = decltype(Q)::value;
-            const uint32_t koff = (uint32_t)(kt * kRowB);
-            const uint32_t l0 = lds_addr(lds + (st * 2 + grp) * 2 * kOpBytes);
-            if constexpr (q < 4) dma16(l0 + (4 * q + wv) * 1024, offx[q], make_rsrc(xg + koff, xbytes - koff));
-            else dma16(l0 + kOpBytes + (4 * (q - 4) + wv) * 1024, offw[q - 4], make_rsrc(wg + koff, wbytes - koff));
+            const bool live = kt < nk;
+            const uint32_t koff = live ? (uint32_t)(kt * kRowB) : 0u;
+            const uint32_t l0 = lds_addr(lds + (kt % kStages) * kStageBytes);
+            if constexpr (q < 2)
+                dma16(l0 + (8 * q + wave) * 1024, offx[q], make_rsrc(xg + koff, live ? xbytes - koff : 0u));
+            else
+                dma16(l0 + kOpBytes + (8 * (q - 2) + wave) * 1024, offw[q - 2], make_rsrc(wg + koff, live ? wbytes - koff : 0u));
         };
-        auto dma = [&](int st, int kt) { static_for<8>([&](auto Q) { dma_one(st, kt, Q); }); };
+        auto dma = [&](int kt) { static_for<4>([&](auto Q) { dma_one(kt, Q); }); };
 
-        floatx16 acc[2][2];
+        floatx16 acc[2];
 #pragma unroll
-        for (int i = 0; i < 2; ++i)
+        for (int j = 0; j < 2; ++j)
 #pragma unroll
-            for (int j = 0; j < 2; ++j)
-#pragma unroll
-                for (int e = 0; e < 16; ++e) acc[i][j][e] = 0.0f;
+            for (int e = 0; e < 16; ++e) acc[j][e] = 0.0f;
 
-        dma(0, grp);
-        // steps 0 .. nsteps-2: compute from stage s & 1 while the next k-tile's 8 DMA instructions go out, one
-        // before every other bundle
-        for (int s = 0; s + 1 < nsteps; ++s) {
-            stage_barrier();  // this step's k-tiles have landed; every wave is done with the other stage
-            const int kn = 2 * (s + 1) + grp, sn = (s + 1) & 1;
-            const uint8_t* As = lds + ((s & 1) * 2 + grp) * 2 * kOpBytes;
+        static_for<kStages - 1>([&](auto K) { dma(decltype(K)::value); });
+        ring_barrier();  // k-tile 0 has landed
+        // step kt: compute from stage kt % 5 while k-tile kt + 4 goes out into the stage of k-tile kt - 1 (every
+        // wave finished it before the last barrier), one DMA instruction before every other bundle
+        for (int kt = 0; kt < nk; ++kt) {
+            const uint8_t* As = lds + (kt % kStages) * kStageBytes;
             tile_step<kF32>(acc, As + arow, As + kOpBytes + brow, coff, [&](auto SLOT) {
                 constexpr int slot = decltype(SLOT)::value;
-                if constexpr ((slot & 1) == 0) dma_one(sn, kn, std::integral_constant<int, slot / 2>{});
+                if constexpr ((slot & 1) == 0) dma_one(kt + kStages - 1, std::integral_constant<int, slot / 2>{});
             });
+            ring_barrier();
         }
-        {
-            stage_barrier();
-            const uint8_t* As = lds + (((nsteps - 1) & 1) * 2 + grp) * 2 * kOpBytes;
-            tile_step<kF32>(acc, As + arow, As + kOpBytes + brow, coff, [](auto) {});
-        }
-        stage_barrier();  // no load in flight and no wave reads a stage any more
+        stage_barrier();  // no load in flight (the empty ones included) and no wave reads a stage any more
 
-        // both groups' partial tiles, row-major fp32: element (i, j, e) is row 64wr + 32i + 8(e/4) + 4hh + e%4,
-        // column 64wc + 32j + ln
-        {
-            float* R = grp ? R1 : R0;
+        // the fp32 tile, row-major: element (j, e) is row 32wr + 8(e/4) + 4hh + e%4, column 64wc + 32j + ln
 #pragma unroll
-            for (int i = 0; i < 2; ++i)
+        for (int j = 0; j < 2; ++j)
 #pragma unroll
-                for (int j = 0; j < 2; ++j)
-#pragma unroll
-                    for (int e = 0; e < 16; ++e)
-                        R[(64 * wr + 32 * i + 8 * (e >> 2) + 4 * hh + (e & 3)) * kRStride + 64 * wc + 32 * j + ln] =
-                            acc[i][j][e];
-        }
+            for (int e = 0; e < 16; ++e)
+                R0[(32 * wr + 8 * (e >> 2) + 4 * hh + (e & 3)) * kRStride + 64 * wc + 32 * j + ln] = acc[j][e];
         __syncthreads();
 
         // thread -> row er of the tile, columns 16qd .. +16 and their rotate-half partners 64 + 16qd .. +16, read
-        // from the two partial tiles (summed) 4 columns at a time
+        // from the tile 4 columns at a time
         const int er = tid >> 2, qd = tid & 3;
-        auto cols4 = [&](int c) {  // columns c .. c+3 of row er, both groups' partial sums added
-            const float4 p0 = *reinterpret_cast<const float4*>(&R0[er * kRStride + c]);
-            const float4 p1 = *reinterpret_cast<const float4*>(&R1[er * kRStride + c]);
-            return make_float4(p0.x + p1.x, p0.y + p1.y, p0.z + p1.z, p0.w + p1.w);
-        };
+        auto cols4 = [&](int c) { return *reinterpret_cast<const float4*>(&R0[er * kRStride + c]); };
         const bool valid = er < nrows;
         const int64_t grow = (int64_t)row0 + er;
         const int64_t ocol = (int64_t)cb * kTile + 16 * qd;  // = which*dm + head*128 + 16qd
