@@ -159,6 +159,16 @@ def test_bwd_ds_path_long_context(ds_ctx, mode, T):
 
 
 @pytest.mark.parametrize("mode", ["fp32", "bf16"])
+@pytest.mark.parametrize("B,T,H,causal", [(1, 8192, 2, True), (2, 2000, 3, False)])
+def test_bwd_ds_path_max_context(ds_ctx, mode, B, T, H, causal):
+    """The longest sequence the API takes (key block 0 sees 128 query tiles, the workspace's largest
+    per-head extent) and a long non-causal batch (every key block sees every query tile)."""
+    inputs, ref = case(B, T, H, 1701 + T, mode, causal=causal)
+    check(gpu_bwd_ctx(inputs, ds_ctx, mode, causal=causal), ref, TOL_FP32 if mode == "fp32" else TOL_BF16,
+          f"dS path {mode} B={B} T={T} H={H} causal={causal}")
+
+
+@pytest.mark.parametrize("mode", ["fp32", "bf16"])
 @pytest.mark.parametrize("B,T,H,causal", [(1, 1000, 4, True), (2, 300, 3, False), (1, 4096, 16, True)])
 def test_bwd_ds_path_against_recompute(ds_ctx, recompute_ctx, mode, B, T, H, causal):
     """dK and dV come from the same kernel code on both paths (bit-identical); dQ sums the same dS values

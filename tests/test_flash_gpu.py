@@ -115,7 +115,7 @@ def test_config4_ragged(gpu, mode):
 
 
 @pytest.mark.parametrize("B,T,H,lens", [(1, 4096, 2, None), (1, 2048, 4, None), (3, 4096, 2, [4096, 2500, 129]),
-                                        (2, 3000, 3, [3000, 2900])])
+                                        (2, 3000, 3, [3000, 2900]), (1, 8192, 2, None)])
 def test_split_items(gpu, B, T, H, lens):
     """Shapes whose bf16 schedule splits the longest query tiles' keys across workgroups (up to three parts,
     merged by the last part to finish): against the oracle, and bit-identical on a second call (the merge
