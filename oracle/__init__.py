@@ -2,8 +2,8 @@
 
 ctypes wrapper of oracle/liboracle.so (built from oracle/dt_oracle.cpp by
 oracle/Makefile). Only tests/, __graft_entry__.smoke() and bench.py's
-cpu_baseline leg use it, as the checker or as the timed CPU baseline; the
-product path (dirktensor_amd) never imports it.
+cpu_baseline leg use it, to verify the GPU results or as the timed CPU
+baseline; the product path (dirktensor_amd) never imports it.
 
 Each function names the reference code it restates; see dt_oracle.cpp.
 """

@@ -2,7 +2,7 @@
 //
 // This file restates, on the CPU, the reference algorithms that the HIP kernels
 // replace. It is linked only by the test suite, by __graft_entry__.smoke() and
-// by bench.py's cpu_baseline leg, always as the checker (or as the timed CPU
+// by bench.py's cpu_baseline leg, always to verify results (or as the timed CPU
 // baseline), never as part of the product path.
 //
 // Functions and the reference code each one follows:
