@@ -31,6 +31,7 @@ DT_QKV_FUSED = 1
 DT_QKV_AUTO = 2
 DT_OPT_GEMM_TUNE = 2
 DT_OPT_BWD_DQ = 3
+DT_OPT_QKV_SPIN_LIMIT = 4
 DT_BWD_DQ_RECOMPUTE = 0
 DT_BWD_DQ_FROM_DS = 1
 DT_BWD_DQ_AUTO = 2
@@ -52,6 +53,7 @@ SIGNATURES = {
     "dt_ctx_create": (_c_int, [_c_int, ctypes.POINTER(_vp)]),
     "dt_ctx_destroy": (_c_int, [_vp]),
     "dt_ctx_set_option": (_c_int, [_vp, _c_int, _c_int]),
+    "dt_ctx_check": (_c_int, [_vp]),
     "dt_rope_table_init": (_c_int, [_vp, ctypes.c_float, _c_int]),
     "dt_flash_attn_fwd": (_c_int, [_vp, _vp, _vp, _vp, _vp, _vp, _vp, _c_int, _c_int, _c_int, _c_int,
                                    ctypes.c_float, _c_int, _vp, _c_int, _c_int, _vp]),

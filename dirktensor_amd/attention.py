@@ -80,6 +80,17 @@ class Context:
             raise ValueError(f"unknown backward dQ path {path!r}: expected one of {sorted(values)}")
         C.call("dt_ctx_set_option", self.handle, C.DT_OPT_BWD_DQ, values[path])
 
+    def set_qkv_spin_limit(self, polls: int) -> None:
+        """Polls a workgroup of the fused QKV kernel waits for the other heads' row sums before it gives up
+        (default 2^20, about a second; 0 makes every wait give up, which writes NaN rows and sets the status
+        that check() reports)."""
+        C.call("dt_ctx_set_option", self.handle, C.DT_OPT_QKV_SPIN_LIMIT, int(polls))
+
+    def check(self) -> None:
+        """Waits for the device, then raises DTError (DT_ERR_HIP) when a fused QKV wait gave up since the last
+        check."""
+        C.call("dt_ctx_check", self.handle)
+
 
 _default_ctx: dict = {}
 

@@ -15,6 +15,7 @@
 #include <algorithm>
 #include <array>
 #include <map>
+#include <mutex>
 
 #include <cmath>
 #include <cstdarg>
@@ -140,11 +141,29 @@ static int run_qkv_fused(dt_ctx* ctx, QkvArgs qa, int f32, hipStream_t s) {
         DT_TRY(ctx->qkv_ss.ensure(ss_bytes));
         DT_HIP_TRY(hipMemsetAsync(ctx->qkv_ss.ptr, 0, ctx->qkv_ss.bytes, s));
     }
+    if (!ctx->qkv_status.ptr) {
+        DT_TRY(ctx->qkv_status.ensure(256));
+        DT_HIP_TRY(hipMemsetAsync(ctx->qkv_status.ptr, 0, ctx->qkv_status.bytes, s));
+    }
     if (++ctx->qkv_epoch == 0) ctx->qkv_epoch = 1;
     qa.ss = static_cast<uint64_t*>(ctx->qkv_ss.ptr);
     qa.ss_bytes = (int64_t)ctx->qkv_ss.bytes;
+    qa.status = static_cast<uint32_t*>(ctx->qkv_status.ptr);
     qa.epoch = ctx->qkv_epoch;
+    qa.spin_limit = ctx->qkv_spin;
     return launch_qkv_norm_rope(qa, f32, s);
+}
+
+int qkv_status_check(dt_ctx* ctx) {
+    if (!ctx->qkv_status.ptr) return DT_OK;
+    uint32_t word = 0;
+    DT_HIP_TRY(hipMemcpy(&word, ctx->qkv_status.ptr, sizeof(word), hipMemcpyDeviceToHost));
+    if (word == 0) return DT_OK;
+    DT_HIP_TRY(hipMemset(ctx->qkv_status.ptr, 0, sizeof(word)));
+    return set_error(DT_ERR_HIP,
+                     "fused QKV projection: a workgroup's wait for the other heads' row sums gave up (a workgroup "
+                     "was kept off its CU); the q/k rows it normalises were written as NaN and the outputs built on them "
+                     "are wrong");
 }
 
 // ---------------- rocBLAS helpers ----------------
@@ -195,22 +214,28 @@ void lt_free(LtPlan& p) {
 }
 }  // namespace
 
-// One-time choice among hipBLASLt's heuristic candidates for a shape: each candidate runs once into a scratch
-// output (beta 0, so an accumulating caller's C is not touched), then three times under events; a candidate whose
-// second run does not reproduce the first bit for bit (a split-K reduction by atomics) is dropped, and the
-// fastest remaining one replaces the first heuristic choice. Synchronises the stream once per new shape.
+// One-time choice among hipBLASLt's heuristic candidates for a shape, returned as the candidate's rank in the
+// heuristic list (0: its first choice). Each candidate runs once into a zeroed scratch output (beta 0, so an
+// accumulating caller's C is not touched), again, then five times under events; a candidate whose second run does
+// not reproduce the first bit for bit (a split-K reduction by atomics) is dropped. The first choice is kept unless
+// another candidate is at least kTuneMargin faster; otherwise the lowest-ranked candidate within kTuneTie of the
+// fastest wins, so that two timings of the same candidates rarely choose differently. Synchronises the stream.
+constexpr float kTuneMargin = 0.05f;
+constexpr float kTuneTie = 0.03f;
 static int lt_tune(dt_ctx* ctx, hipStream_t s, hipblasLtHandle_t h, LtPlan& p,
-                   const hipblasLtMatmulHeuristicResult_t* heur, int n, int M, int N, int K, const void* A,
-                   const void* B, int ldc, bool c_bf16) {
-    (void)N;
-    (void)K;
+                   const hipblasLtMatmulHeuristicResult_t* heur, int n, int M, int ldc, bool c_bf16, const void* A,
+                   const void* B, int* rank) {
+    *rank = 0;
     DT_TRY(ctx->lt_ws.ensure(kLtWorkspace));
-    const size_t words = (size_t)ldc * M * (c_bf16 ? 2 : 4) / 4;
+    // whole 32-bit words covering the ldc * M output elements, the tail padded with zeros
+    const size_t out_bytes = (size_t)ldc * M * (c_bf16 ? 2 : 4);
+    const size_t words = (out_bytes + 3) / 4;
     void* scratch = nullptr;
     unsigned long long* fp = nullptr;
     hipEvent_t e0 = nullptr, e1 = nullptr;
     if (hipMalloc(&scratch, words * 4) != hipSuccess || hipMalloc(&fp, 2 * sizeof(unsigned long long)) != hipSuccess ||
-        hipEventCreate(&e0) != hipSuccess || hipEventCreate(&e1) != hipSuccess) {
+        hipEventCreate(&e0) != hipSuccess || hipEventCreate(&e1) != hipSuccess ||
+        hipMemsetAsync(scratch, 0, words * 4, s) != hipSuccess) {
         (void)hipGetLastError();  // no room to tune: keep the first heuristic choice
         if (scratch) (void)hipFree(scratch);
         if (fp) (void)hipFree(fp);
@@ -219,14 +244,13 @@ static int lt_tune(dt_ctx* ctx, hipStream_t s, hipblasLtHandle_t h, LtPlan& p,
         return DT_OK;
     }
     const float one = 1.0f, zero = 0.0f;
-    float best = -1.0f;
-    hipblasLtMatmulAlgo_t best_algo = heur[0].algo;
     auto run = [&](const hipblasLtMatmulAlgo_t& algo) {
         return hipblasLtMatmul(h, p.desc, &one, B, p.la, A, p.lb, &zero, scratch, p.lc, scratch, p.lc, &algo,
                                ctx->lt_ws.ptr, kLtWorkspace, s) == HIPBLAS_STATUS_SUCCESS;
     };
     const int64_t nw = (int64_t)words;
     const unsigned blocks = (unsigned)std::min<int64_t>((nw + 255) / 256, 4096);
+    std::vector<float> ms_of(n, -1.0f);  // -1: failed or not reproducible
     for (int i = 0; i < n; ++i) {
         if (hipMemsetAsync(fp, 0, 2 * sizeof(unsigned long long), s) != hipSuccess) break;
         if (!run(heur[i].algo)) continue;
@@ -236,7 +260,7 @@ static int lt_tune(dt_ctx* ctx, hipStream_t s, hipblasLtHandle_t h, LtPlan& p,
         hipLaunchKernelGGL(words_fingerprint_kernel, dim3(blocks), dim3(256), 0, s, static_cast<const uint32_t*>(scratch),
                            nw, fp + 1);
         ok = ok && hipEventRecord(e0, s) == hipSuccess;
-        for (int r = 0; r < 3 && ok; ++r) ok = run(heur[i].algo);
+        for (int r = 0; r < 5 && ok; ++r) ok = run(heur[i].algo);
         ok = ok && hipEventRecord(e1, s) == hipSuccess && hipEventSynchronize(e1) == hipSuccess;
         unsigned long long f[2] = {0, 1};
         ok = ok && hipMemcpy(f, fp, sizeof(f), hipMemcpyDeviceToHost) == hipSuccess;
@@ -246,20 +270,30 @@ static int lt_tune(dt_ctx* ctx, hipStream_t s, hipblasLtHandle_t h, LtPlan& p,
             (void)hipGetLastError();
             continue;
         }
-        if (f[0] != f[1]) continue;  // not reproducible run to run
-        if (best < 0.0f || ms < best) {
-            best = ms;
-            best_algo = heur[i].algo;
-        }
+        if (f[0] == f[1]) ms_of[i] = ms;  // else not reproducible run to run
     }
     (void)hipStreamSynchronize(s);
     (void)hipFree(scratch);
     (void)hipFree(fp);
     (void)hipEventDestroy(e0);
     (void)hipEventDestroy(e1);
-    p.algo = best_algo;
+    float best = -1.0f;
+    for (int i = 0; i < n; ++i)
+        if (ms_of[i] >= 0.0f && (best < 0.0f || ms_of[i] < best)) best = ms_of[i];
+    if (best < 0.0f || (ms_of[0] >= 0.0f && best >= (1.0f - kTuneMargin) * ms_of[0])) return DT_OK;
+    for (int i = 0; i < n; ++i)
+        if (ms_of[i] >= 0.0f && ms_of[i] <= (1.0f + kTuneTie) * best) {
+            *rank = i;
+            break;
+        }
+    p.algo = heur[*rank].algo;
     return DT_OK;
 }
+
+// The rank chosen for a shape on a device, shared by every context of the process, so that all of them run the
+// same algorithm for it and give the same bits (another process may time the candidates differently).
+static std::mutex g_tune_mu;
+static std::map<std::array<int, 11>, int> g_tune_rank;
 
 // Row-major C[M][N] = op(A) op(B) + beta C with bf16 A, B and fp32 C (bf16 C when c_bf16) through hipBLASLt
 // (the same column-major mapping as gemm_rm below). Returns 1 (no error set) when hipBLASLt offers no
@@ -307,7 +341,24 @@ static int gemm_lt(dt_ctx* ctx, hipStream_t s, bool ta, bool tb, int M, int N, i
             return 1;
         }
         p.algo = heur[0].algo;
-        if (n > 1) DT_TRY(lt_tune(ctx, s, lc->h, p, heur, n, M, N, K, A, B, ldc, c_bf16));
+        if (n > 1) {
+            const std::array<int, 11> gkey{ctx->device, ta, tb, M, N, K, lda, ldb, ldc, beta == 0.0f, c_bf16};
+            std::lock_guard<std::mutex> lock(g_tune_mu);
+            auto g = g_tune_rank.find(gkey);
+            if (g != g_tune_rank.end()) {
+                if (g->second < n) p.algo = heur[g->second].algo;
+            } else {
+                // a capturing stream cannot take the tuning's allocations and synchronisations: keep the first
+                // choice for this context and leave the shape to be tuned by a later uncaptured call
+                hipStreamCaptureStatus cs = hipStreamCaptureStatusNone;
+                if (hipStreamIsCapturing(s, &cs) != hipSuccess) (void)hipGetLastError();
+                if (cs == hipStreamCaptureStatusNone) {
+                    int rank = 0;
+                    DT_TRY(lt_tune(ctx, s, lc->h, p, heur, n, M, ldc, c_bf16, A, B, &rank));
+                    g_tune_rank.emplace(gkey, rank);
+                }
+            }
+        }
         it = lc->plans.emplace(key, p).first;
     }
     DT_TRY(ctx->lt_ws.ensure(kLtWorkspace));
@@ -374,32 +425,39 @@ static int gemm_xwt(dt_ctx* ctx, hipStream_t s, int M, int N, int K, const void*
 }
 
 // ---------------- .npy reader (v1/v2/v3, little-endian fp32, C order) ----------------
-int read_npy_f32(const std::string& path, std::vector<float>& out, std::vector<size_t>& shape) {
+// Parses a .npy header (v1-v3): little-endian float32 in C order, the shape, and where the data starts; checks
+// that the file holds all of the data. The file is left open at the data when f_out is given, else closed.
+static int npy_header(const std::string& path, std::vector<size_t>& shape, FILE** f_out) {
     FILE* f = std::fopen(path.c_str(), "rb");
     if (!f) return set_error(DT_ERR_IO, "cannot open %s", path.c_str());
-    unsigned char magic[8];
-    if (std::fread(magic, 1, 8, f) != 8 || std::memcmp(magic, "\x93NUMPY", 6) != 0) {
+    auto fail = [&](int rc) {
         std::fclose(f);
-        return set_error(DT_ERR_IO, "%s is not a .npy file (a Git-LFS pointer?)", path.c_str());
-    }
+        return rc;
+    };
+    unsigned char magic[8];
+    if (std::fread(magic, 1, 8, f) != 8 || std::memcmp(magic, "\x93NUMPY", 6) != 0)
+        return fail(set_error(DT_ERR_IO, "%s is not a .npy file (a Git-LFS pointer?)", path.c_str()));
     uint32_t hlen = 0;
+    long data_at = 0;
     if (magic[6] == 1) {
         unsigned char b[2];
-        if (std::fread(b, 1, 2, f) != 2) { std::fclose(f); return set_error(DT_ERR_IO, "%s: truncated", path.c_str()); }
+        if (std::fread(b, 1, 2, f) != 2) return fail(set_error(DT_ERR_IO, "%s: truncated", path.c_str()));
         hlen = b[0] | (b[1] << 8);
+        data_at = 10 + (long)hlen;
     } else {
         unsigned char b[4];
-        if (std::fread(b, 1, 4, f) != 4) { std::fclose(f); return set_error(DT_ERR_IO, "%s: truncated", path.c_str()); }
+        if (std::fread(b, 1, 4, f) != 4) return fail(set_error(DT_ERR_IO, "%s: truncated", path.c_str()));
         hlen = b[0] | (b[1] << 8) | (b[2] << 16) | ((uint32_t)b[3] << 24);
+        data_at = 12 + (long)hlen;
     }
+    if (hlen > (1u << 20)) return fail(set_error(DT_ERR_IO, "%s: header of %u bytes", path.c_str(), hlen));
     std::string hdr(hlen, '\0');
-    if (std::fread(&hdr[0], 1, hlen, f) != hlen) { std::fclose(f); return set_error(DT_ERR_IO, "%s: truncated", path.c_str()); }
-    if (hdr.find("'<f4'") == std::string::npos || hdr.find("'fortran_order': False") == std::string::npos) {
-        std::fclose(f);
-        return set_error(DT_ERR_IO, "%s: need little-endian float32 in C order, header %s", path.c_str(), hdr.c_str());
-    }
+    if (std::fread(&hdr[0], 1, hlen, f) != hlen) return fail(set_error(DT_ERR_IO, "%s: truncated", path.c_str()));
+    if (hdr.find("'<f4'") == std::string::npos || hdr.find("'fortran_order': False") == std::string::npos)
+        return fail(set_error(DT_ERR_IO, "%s: need little-endian float32 in C order, header %s", path.c_str(),
+                              hdr.c_str()));
     size_t p = hdr.find("'shape': (");
-    if (p == std::string::npos) { std::fclose(f); return set_error(DT_ERR_IO, "%s: no shape", path.c_str()); }
+    if (p == std::string::npos) return fail(set_error(DT_ERR_IO, "%s: no shape", path.c_str()));
     p += 10;
     shape.clear();
     size_t n = 1;
@@ -408,17 +466,39 @@ int read_npy_f32(const std::string& path, std::vector<float>& out, std::vector<s
         if (p < hdr.size() && hdr[p] == ')') break;
         size_t v = 0;
         bool any = false;
-        while (p < hdr.size() && hdr[p] >= '0' && hdr[p] <= '9') { v = v * 10 + (hdr[p] - '0'); ++p; any = true; }
-        if (!any) { std::fclose(f); return set_error(DT_ERR_IO, "%s: bad shape", path.c_str()); }
+        while (p < hdr.size() && hdr[p] >= '0' && hdr[p] <= '9') {
+            v = v * 10 + (hdr[p] - '0');
+            ++p;
+            any = true;
+        }
+        if (!any) return fail(set_error(DT_ERR_IO, "%s: bad shape", path.c_str()));
         shape.push_back(v);
         n *= v;
     }
-    out.resize(n);
-    if (std::fread(out.data(), sizeof(float), n, f) != n) {
+    if (std::fseek(f, 0, SEEK_END) != 0) return fail(set_error(DT_ERR_IO, "%s: cannot seek", path.c_str()));
+    const long size = std::ftell(f);
+    if (size < 0 || (size_t)(size - data_at) < n * sizeof(float) || size < data_at)
+        return fail(set_error(DT_ERR_IO, "%s: truncated data", path.c_str()));
+    if (!f_out) {
         std::fclose(f);
-        return set_error(DT_ERR_IO, "%s: truncated data", path.c_str());
+        return DT_OK;
     }
+    if (std::fseek(f, data_at, SEEK_SET) != 0) return fail(set_error(DT_ERR_IO, "%s: cannot seek", path.c_str()));
+    *f_out = f;
+    return DT_OK;
+}
+
+int read_npy_shape(const std::string& path, std::vector<size_t>& shape) { return npy_header(path, shape, nullptr); }
+
+int read_npy_f32(const std::string& path, std::vector<float>& out, std::vector<size_t>& shape) {
+    FILE* f = nullptr;
+    DT_TRY(npy_header(path, shape, &f));
+    size_t n = 1;
+    for (size_t v : shape) n *= v;
+    out.resize(n);
+    const size_t got = std::fread(out.data(), sizeof(float), n, f);
     std::fclose(f);
+    if (got != n) return set_error(DT_ERR_IO, "%s: truncated data", path.c_str());
     return DT_OK;
 }
 
@@ -470,6 +550,11 @@ int dt_ctx_set_option(dt_ctx* ctx, int option, int value) {
         ctx->gemm_tune = value;
         return DT_OK;
     }
+    if (option == DT_OPT_QKV_SPIN_LIMIT) {
+        if (value < 0) return set_error(DT_ERR_INVALID_ARG, "DT_OPT_QKV_SPIN_LIMIT must be >= 0, not %d", value);
+        ctx->qkv_spin = value;
+        return DT_OK;
+    }
     if (option == DT_OPT_BWD_DQ) {
         if (value != DT_BWD_DQ_RECOMPUTE && value != DT_BWD_DQ_FROM_DS && value != DT_BWD_DQ_AUTO)
             return set_error(DT_ERR_INVALID_ARG,
@@ -492,6 +577,7 @@ int dt_ctx_destroy(dt_ctx* ctx) {
     ctx->fwd_split.release();
     ctx->fwd_split_cnt.release();
     ctx->qkv_ss.release();
+    ctx->qkv_status.release();
     if (ctx->blas) rocblas_destroy_handle(static_cast<rocblas_handle>(ctx->blas));
     if (ctx->lt) {
         LtCache* lc = static_cast<LtCache*>(ctx->lt);
@@ -502,6 +588,14 @@ int dt_ctx_destroy(dt_ctx* ctx) {
     ctx->lt_ws.release();
     delete ctx;
     return DT_OK;
+}
+
+int dt_ctx_check(dt_ctx* ctx) {
+    clear_error();
+    if (!ctx) return set_error(DT_ERR_INVALID_ARG, "ctx is NULL");
+    DT_TRY(check_device_binding(ctx));
+    DT_HIP_TRY(hipDeviceSynchronize());
+    return qkv_status_check(ctx);
 }
 
 int dt_rope_table_init(dt_ctx* ctx, float theta, int max_seq_len) {
@@ -565,7 +659,10 @@ int dt_flash_attn_fwd(dt_ctx* ctx, const void* q, const void* k, const void* v, 
 
 // The dS workspace of an attention backward when DT_OPT_BWD_DQ selects the dS path, else NULL. The
 // automatic choice takes it where it measured faster (more than one 128-row block per CU and pass, e.g.
-// B*H = 16 at T = 4096) and falls back to the recompute path when the buffer cannot be allocated.
+// B*H = 16 at T = 4096), with a buffer of at most kDsAutoCap bytes and a quarter of the device's free memory
+// (the buffer is kept by the context; an unbounded one could starve the caller's own allocator), and takes the
+// recompute path above that or when the buffer cannot be allocated.
+constexpr size_t kDsAutoCap = size_t(2) << 30;
 static int bwd_ds_workspace(dt_ctx* ctx, int B, int H, int T, int causal, int dtype, void** ws) {
     *ws = nullptr;
     if (ctx->bwd_dq == DT_BWD_DQ_RECOMPUTE) return DT_OK;
@@ -575,6 +672,13 @@ static int bwd_ds_workspace(dt_ctx* ctx, int B, int H, int T, int causal, int dt
         DT_TRY(persistent_grid(0x7fffffff, &cus));
         const int64_t blocks = (int64_t)((T + 127) / 128) * B * H;
         if (blocks <= cus) return DT_OK;
+        if (ctx->bwd_ds.bytes < bytes) {
+            size_t free_b = 0, total_b = 0;
+            if (bytes > kDsAutoCap || hipMemGetInfo(&free_b, &total_b) != hipSuccess || bytes > free_b / 4) {
+                (void)hipGetLastError();
+                return DT_OK;
+            }
+        }
         if (ctx->bwd_ds.ensure(bytes) != DT_OK) {  // out of memory: the recompute path needs no buffer
             (void)hipGetLastError();
             clear_error();
@@ -938,6 +1042,7 @@ int dt_attn_layer_fwd(dt_attn_layer* L, const float* x, float* out, int B, int T
     if (mem == DT_MEM_HOST) {
         DT_HIP_TRY(hipMemcpyAsync(out, od, act * 4, hipMemcpyDeviceToHost, s));
         DT_HIP_TRY(hipStreamSynchronize(s));
+        DT_TRY(qkv_status_check(ctx));
     }
     if (save_for_backward) {
         L->saved_B = B;

@@ -151,7 +151,12 @@ struct QkvArgs {
     int rows, T, H;
     int ldx, ld_out, ld_pre;  // elements
     float eps;
+    uint32_t* status = nullptr;  // set to kQkvWaitGaveUp when a wait for the other heads' sums gives up
+    int spin_limit = 0;          // polls before such a wait gives up (0: every wait gives up at once)
 };
+// polls (coherent loads and s_sleep 1, about a second in all) before a wait of the fused kernel gives up
+constexpr int kQkvSpinLimit = 1 << 20;
+constexpr uint32_t kQkvWaitGaveUp = 1;
 int qkv_norm_rope_workspace(int rows, int H, size_t* ss_bytes);
 int launch_qkv_norm_rope(const QkvArgs& a, int f32, hipStream_t stream);
 // the fused kernel's tiles for rows x (3 H heads) fit one round on this device's CUs
@@ -195,11 +200,15 @@ int gemm_rm_bf16(dt_ctx* ctx, hipStream_t s, bool ta, bool tb, int M, int N, int
                  const void* B, int ldb, void* C, int ldc);
 // .npy reader (v1-v3 headers, little-endian fp32, C order)
 int read_npy_f32(const std::string& path, std::vector<float>& out, std::vector<size_t>& shape);
+// the same checks (format, dtype, order, the data all present) and the shape, without reading the data
+int read_npy_shape(const std::string& path, std::vector<size_t>& shape);
 bool aligned16(const void* p);
 // once per device, with it current (dt_ctx_create): looks up that device's address of the scratch array of
 // dt_flash_attn_bwd_noalloc (noalloc.hip)
 int noalloc_setup(int device);
 int check_device_binding(dt_ctx* ctx);
+// after the stream has been synchronised: DT_ERR_HIP (and clears the word) when a fused QKV wait gave up
+int qkv_status_check(dt_ctx* ctx);
 
 }  // namespace dt
 
@@ -219,6 +228,8 @@ struct dt_ctx {
     dt::DeviceBuffer fwd_split_cnt;  // and their counters (zeroed when allocated; each launch leaves them zero)
     dt::DeviceBuffer qkv_ss;   // fused QKV projection: per-row, per-head sums of squares (zeroed when allocated)
     uint32_t qkv_epoch = 0;    // the tag of its last launch
+    dt::DeviceBuffer qkv_status;  // its status word: nonzero once a wait gave up (zeroed when allocated and read)
+    int qkv_spin = dt::kQkvSpinLimit;  // DT_OPT_QKV_SPIN_LIMIT
     int qkv_fused = DT_QKV_AUTO;  // DT_OPT_QKV_FUSED
     int gemm_tune = 1;            // DT_OPT_GEMM_TUNE
     int bwd_dq = DT_BWD_DQ_AUTO;  // DT_OPT_BWD_DQ

@@ -18,8 +18,14 @@
 //     and dO fragments in registers and streams 64-key tiles of K and V.
 //     Per tile a wave forms S^T = K Q^T and dP^T = V dO^T, the same P and dS,
 //     and accumulates dQ^T += K^T dS^T.
-//   S and dP are recomputed in both kernels (7 MFMA products per tile pair
-//   instead of the reference's 5) in exchange for no atomics.
+//   On this recompute path S and dP are formed in both kernels (7 MFMA
+//   products per tile pair instead of the reference's 5) in exchange for no
+//   atomics.
+//   * The dS path (flash_bwd_dkdv_ds + flash_bwd_dq_ds, the default where each
+//     pass has more than one block per CU, e.g. B*H = 16 at T = 4096): the
+//     dK/dV kernel also stores the bf16 dS it forms for its dK product to a
+//     workspace, and the dQ kernel computes dQ = dS K from it, so a tile pair
+//     takes 5 products, still with one owner per gradient row and no atomics.
 // Causality (FlashAttention.cpp:247, 265-268) limits the dK/dV kernel to query
 // tiles at or after its keys and the dQ kernel to key tiles at or before its
 // queries. Each workgroup owns one 128-row block; the grid lists the blocks in

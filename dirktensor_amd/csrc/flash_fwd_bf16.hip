@@ -101,12 +101,9 @@ __device__ __forceinline__ uint32_t pack_bf16x2(float lo, float hi) {
     return __builtin_bit_cast(uint32_t, r);
 }
 
-// Row reductions across the two lane halves (lane l and lane l ^ 32 hold the same
-// query). ds_bpermute via __shfl_xor; v_permlane32_swap would avoid the LDS
-// crossbar, but this compiler returns the same register for both of the
-// builtin's results, so its second half is unusable.
-// Over the two lane halves (lanes l and l ^ 32), through v_permlane32_swap with x as both operands: the
-// result pair holds, in every lane, the lower half's value and the upper half's (same order in both halves).
+// Row reductions over the two lane halves (lane l and lane l ^ 32 hold the same query), through
+// v_permlane32_swap (VALU, no LDS crossbar) with x as both operands: the result pair holds, in every lane, the
+// lower half's value and the upper half's (same order in both halves).
 __device__ __forceinline__ float max_halves(float x) {
     const auto r = __builtin_amdgcn_permlane32_swap(__float_as_uint(x), __float_as_uint(x), false, false);
     return fmaxf(__uint_as_float(r[0]), __uint_as_float(r[1]));

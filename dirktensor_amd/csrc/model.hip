@@ -365,22 +365,43 @@ int dt_model_load(dt_ctx* ctx, const char* folder, int n_layers, dt_model** out)
     *out = nullptr;
     if (!folder) return set_error(DT_ERR_INVALID_ARG, "folder is NULL");
     if (n_layers < 1 || n_layers > 256) return set_error(DT_ERR_INVALID_ARG, "n_layers=%d outside [1, 256]", n_layers);
-    if (!ctx) return set_error(DT_ERR_INVALID_ARG, "ctx is NULL");
     const std::string dir(folder);
     // shapes from the embedding and the first MLP (OlmoModel.cpp:12-18, OlmoMlp.cpp:9-19)
-    std::vector<float> buf;
-    std::vector<size_t> shape;
-    DT_TRY(read_npy_f32(dir + "/model.embed_tokens.weight.npy", buf, shape));
-    if (shape.size() != 2) return set_error(DT_ERR_IO, "model.embed_tokens.weight: expected 2 dimensions");
+    std::vector<size_t> shape, up_shape;
+    DT_TRY(read_npy_shape(dir + "/model.embed_tokens.weight.npy", shape));
+    if (shape.size() != 2 || shape[0] < 1 || shape[1] < 1 || shape[0] > 0x7fffffff || shape[1] > 0x7fffffff)
+        return set_error(DT_ERR_IO, "model.embed_tokens.weight: expected a non-empty matrix");
     const int V = (int)shape[0], dm = (int)shape[1];
-    std::vector<float> up;
-    std::vector<size_t> up_shape;
-    DT_TRY(read_npy_f32(dir + "/model.layers.0.mlp.up_proj.weight.npy", up, up_shape));
-    if (up_shape.size() != 2 || (int)up_shape[1] != dm) return set_error(DT_ERR_IO, "mlp.up_proj: unexpected shape");
+    DT_TRY(read_npy_shape(dir + "/model.layers.0.mlp.up_proj.weight.npy", up_shape));
+    if (up_shape.size() != 2 || (int)up_shape[1] != dm || up_shape[0] < 1 || up_shape[0] > 0x7fffffff)
+        return set_error(DT_ERR_IO, "model.layers.0.mlp.up_proj.weight: unexpected shape");
     if (dm % DT_HEAD_DIM) return set_error(DT_ERR_UNSUPPORTED, "d_model=%d is not a multiple of %d", dm, DT_HEAD_DIM);
+    const size_t hid = up_shape[0];
+    // every file's header and shape are checked before the device is touched (a Git-LFS pointer, a wrong dtype
+    // or a truncated file fails here, not after gigabytes have been uploaded)
+    const std::vector<std::string> names = param_names(n_layers);
+    for (const std::string& name : names) {
+        std::vector<size_t> sh;
+        DT_TRY(read_npy_shape(dir + "/" + name + ".npy", sh));
+        std::vector<size_t> want;
+        const bool vec = name.find("norm") != std::string::npos;  // q_norm, k_norm, the post-norms, model.norm
+        if (name == "model.embed_tokens.weight" || name == "lm_head.weight") want = {(size_t)V, (size_t)dm};
+        else if (vec) want = {(size_t)dm};
+        else if (name.find("gate_proj") != std::string::npos || name.find("up_proj") != std::string::npos)
+            want = {hid, (size_t)dm};
+        else if (name.find("down_proj") != std::string::npos) want = {(size_t)dm, hid};
+        else want = {(size_t)dm, (size_t)dm};  // the attention projections
+        if (sh != want) {
+            std::string got, exp;
+            for (size_t v : sh) got += std::to_string(v) + ",";
+            for (size_t v : want) exp += std::to_string(v) + ",";
+            return set_error(DT_ERR_IO, "%s: shape (%s) where (%s) was expected", name.c_str(), got.c_str(), exp.c_str());
+        }
+    }
+    if (!ctx) return set_error(DT_ERR_INVALID_ARG, "ctx is NULL");
     dt_model* M = nullptr;
-    DT_TRY(dt_model_create(ctx, n_layers, dm, dm / DT_HEAD_DIM, (int)up_shape[0], V, &M));
-    for (const std::string& name : param_names(n_layers)) {
+    DT_TRY(dt_model_create(ctx, n_layers, dm, dm / DT_HEAD_DIM, (int)hid, V, &M));
+    for (const std::string& name : names) {
         std::vector<float> w;
         std::vector<size_t> sh;
         int rc = read_npy_f32(dir + "/" + name + ".npy", w, sh);
@@ -488,6 +509,7 @@ int dt_model_fwd(dt_model* M, const int32_t* tokens, int B, int T, float* logits
     if (mem == DT_MEM_HOST) {
         DT_HIP_TRY(hipMemcpyAsync(logits, lo, (size_t)rows * V * 4, hipMemcpyDeviceToHost, s));
         DT_HIP_TRY(hipStreamSynchronize(s));
+        DT_TRY(qkv_status_check(ctx));
     }
     if (save_for_backward) {
         // the final residual stream x is in M->x or M->x2; keep it addressable as M->x

@@ -65,7 +65,6 @@ constexpr int kLdsBytes = kStages * kStageBytes;  // 160 KB
 static_assert(kLdsBytes >= kTile * kRStride * 4, "the stages must hold the epilogue tile");
 constexpr int kBufferDword3 = 0x00020000;  // raw buffer, 32-bit data format (gfx9 family)
 constexpr int kCoherent = 16;              // cache policy sc1: device-scope coherent access
-constexpr int kSpinLimit = 1 << 20;        // polls (coherent loads and s_sleep 1, ~1 s in all) before a wait gives up
 
 __device__ __forceinline__ uint32_t pack_bf16x2(float lo, float hi) {
     bf16x2 r = __builtin_convertvector((floatx2){lo, hi}, bf16x2);
@@ -199,6 +198,7 @@ __global__ __launch_bounds__(kThreads, 1) void qkv_norm_rope_kernel(QkvArgs a) {
     const uint32_t brow = (uint32_t)((64 * wc + ln) * kRowB);
 
     const __amdgpu_buffer_rsrc_t rss = make_rsrc(a.ss, (uint32_t)a.ss_bytes);
+    const __amdgpu_buffer_rsrc_t rstat = make_rsrc(a.status, 4u);
     float* const R0 = reinterpret_cast<float*>(lds);
 
     for (int tile = blockIdx.x; tile < n_tiles; tile += gridDim.x) {
@@ -294,7 +294,7 @@ __global__ __launch_bounds__(kThreads, 1) void qkv_norm_rope_kernel(QkvArgs a) {
                 // thread qd polls heads 4qd .. 4qd+3 of its row until all four carry this launch's epoch
                 float part = 0.0f;
                 bool ok = false;
-                for (int spins = 0; spins < kSpinLimit; ++spins) {
+                for (int spins = 0; spins < a.spin_limit; ++spins) {
                     bool all = true;
                     float sum = 0.0f;
                     for (int h = 4 * qd; h < H; h += 16) {  // heads 4qd + 16j .. +3: each head once (H % 4 == 0)
@@ -324,6 +324,8 @@ __global__ __launch_bounds__(kThreads, 1) void qkv_norm_rope_kernel(QkvArgs a) {
                     __shfl_xor((int)ok, 1, 64) & __shfl_xor((int)ok, 2, 64) & __shfl_xor((int)ok, 3, 64) & (int)ok;
                 const float tot = part;
                 const float rms = all_ok ? sqrtf(tot / (float)dm + a.eps) : __builtin_nanf("");
+                if (!all_ok && qd == 0)  // the host reports it (dt_ctx_check, synchronous host-memory calls)
+                    __builtin_amdgcn_raw_buffer_store_b32(kQkvWaitGaveUp, rstat, 0, 0, 0);
                 if (a.rms && qd == 0) a.rms[(int64_t)which * a.rows + grow] = rms;
                 const int t = (int)(grow % a.T);
                 const float* cs = a.rope_cos + (int64_t)t * 64 + 16 * qd;
@@ -382,6 +384,7 @@ int launch_qkv_norm_rope(const QkvArgs& a, int f32, hipStream_t stream) {
     if ((int64_t)kTile * a.ldx * es >= ((int64_t)1 << 31) || (int64_t)kTile * dm * es >= ((int64_t)1 << 31))
         return set_error(DT_ERR_UNSUPPORTED, "fused QKV: a 128-row band exceeds 2 GiB");
     if (a.epoch == 0) return set_error(DT_ERR_INVALID_ARG, "fused QKV: epoch 0 is reserved");
+    if (!a.status || a.spin_limit < 0) return set_error(DT_ERR_INVALID_ARG, "fused QKV: no status word or a negative spin limit");
     size_t ssb = 0;
     DT_TRY(qkv_norm_rope_workspace(a.rows, a.H, &ssb));
     if (ssb >= ((size_t)1 << 31) || a.ss_bytes < (int64_t)ssb)

@@ -95,11 +95,19 @@ int dt_ctx_destroy(dt_ctx* ctx);
  *                                  heads on MI355X), where it measured faster;
  *                                  the GEMM path above that and in
  *                                  DT_FP32_EXACT mode.
- *   DT_OPT_GEMM_TUNE  1 (default): the first bf16 GEMM of each new shape on
- *                     this context times hipBLASLt's heuristic candidates
+ *   DT_OPT_GEMM_TUNE  1 (default): the first bf16 GEMM of each new shape in
+ *                     the process times hipBLASLt's heuristic candidates
  *                     (up to 16, into a scratch output; synchronises the
- *                     stream once) and keeps the fastest whose repeated run
- *                     is bit-identical; 0: the first heuristic choice.
+ *                     stream once; skipped while the stream is capturing a
+ *                     graph) and keeps the first heuristic choice unless a
+ *                     candidate whose repeated run is bit-identical is at
+ *                     least 5 % faster (then the best-ranked candidate within
+ *                     3 % of the fastest). The choice is shared by every
+ *                     context of the process, so their bf16 GEMM results are
+ *                     bit-identical; another process may time the candidates
+ *                     differently and choose another algorithm, whose results
+ *                     can differ in the last bits. 0: the first heuristic
+ *                     choice, the same in every process.
  *   DT_OPT_BWD_DQ     how the attention backward (dt_flash_attn_bwd,
  *                     dt_attn_layer_bwd, the model backward) forms dQ
  *                     (FlashAttention.cpp:185-359), in both modes:
@@ -112,16 +120,34 @@ int dt_ctx_destroy(dt_ctx* ctx);
  *                                          reads it;
  *                     DT_BWD_DQ_AUTO       (default) the dS path where it
  *                                          measured faster (more than one
- *                                          128-row block per CU and pass),
- *                                          the recompute path otherwise or
- *                                          when the buffer cannot be had.
+ *                                          128-row block per CU and pass)
+ *                                          and its buffer needs at most
+ *                                          2 GiB and a quarter of the free
+ *                                          device memory; the recompute
+ *                                          path otherwise or when the
+ *                                          buffer cannot be had. The buffer
+ *                                          is kept until dt_ctx_destroy.
  *                     Both give the same results within the mode's
  *                     tolerance; each is deterministic.
+ *   DT_OPT_QKV_SPIN_LIMIT  polls (default 1048576, about a second) that a
+ *                     workgroup of the fused QKV kernel spends waiting for the
+ *                     other heads' row sums of squares before it gives up.
+ *                     The kernel runs its H tiles of a row block in one round
+ *                     (one workgroup per CU); a workgroup kept off its CU that
+ *                     long (by another kernel holding CUs) makes the wait give
+ *                     up: the q/k rows it normalises are then written as NaN
+ *                     (the attention core turns such rows into its empty
+ *                     rows, so the layer output is wrong) and the context's
+ *                     status word is set, which dt_ctx_check
+ *                     (and any synchronous DT_MEM_HOST layer or model forward)
+ *                     reports as DT_ERR_HIP. 0 makes every wait give up at
+ *                     once (for testing that report).
  * Returns DT_ERR_INVALID_ARG for an unknown option or value.
  */
 #define DT_OPT_QKV_FUSED 1
 #define DT_OPT_GEMM_TUNE 2
 #define DT_OPT_BWD_DQ 3
+#define DT_OPT_QKV_SPIN_LIMIT 4
 #define DT_QKV_GEMM 0
 #define DT_QKV_FUSED 1
 #define DT_QKV_AUTO 2
@@ -129,6 +155,14 @@ int dt_ctx_destroy(dt_ctx* ctx);
 #define DT_BWD_DQ_FROM_DS 1
 #define DT_BWD_DQ_AUTO 2
 int dt_ctx_set_option(dt_ctx* ctx, int option, int value);
+
+/*
+ * Waits for the context's device to finish its work, then reports a fused
+ * QKV wait that gave up since the last check (DT_OPT_QKV_SPIN_LIMIT) as
+ * DT_ERR_HIP and clears it; DT_OK otherwise. No reference counterpart (the
+ * reference's CPU path has no such wait).
+ */
+int dt_ctx_check(dt_ctx* ctx);
 
 /*
  * Builds the RoPE sin/cos tables on the host in fp64, casts them to fp32 and
@@ -176,9 +210,13 @@ int dt_flash_attn_bwd(dt_ctx* ctx, const void* d_o, const void* o, const float* 
  * dt_flash_attn_bwd without any allocation. No counterpart in the reference:
  * it is for callers that cannot allocate device memory during the call (code
  * under HIP graph capture, serving loops, harnesses that forbid hipMalloc).
- * Same arguments and results as dt_flash_attn_bwd with mem = DT_MEM_DEVICE
- * (device pointers only, stream-ordered), the same kernels, bit-identical
- * output. The backward's row statistics go to a fixed device array of 8 MiB
+ * Same arguments as dt_flash_attn_bwd with mem = DT_MEM_DEVICE (device
+ * pointers only, stream-ordered). It always takes the recompute path, so its
+ * output is bit-identical to dt_flash_attn_bwd's on a context with
+ * DT_OPT_BWD_DQ = DT_BWD_DQ_RECOMPUTE. With the default DT_BWD_DQ_AUTO,
+ * dt_flash_attn_bwd takes the dS path above one 128-row block per CU and pass
+ * (e.g. B*H = 16, T = 4096): dK and dV are then still bit-identical, and dQ
+ * agrees within the mode's tolerance (a different summation order). The backward's row statistics go to a fixed device array of 8 MiB
  * per GPU, set up by dt_ctx_create and held until the process ends, so
  * B*T*H must be at most 1048576 (DT_ERR_UNSUPPORTED above that). Every call
  * on one GPU shares that array: calls that overlap in time on one GPU (on
@@ -277,7 +315,11 @@ int dt_attn_layer_get_grads(dt_attn_layer* layer, float* d_wq, float* d_wk, floa
  * (or, with grad = 1, its accumulated gradient) in or out. dt_model_load is
  * the OlmoModel(folder) constructor (OlmoModel.cpp:12-23): it reads every
  * "{folder}/{name}.npy" for n_layers blocks (the reference's n_layers = 16,
- * model_config.h:7).
+ * model_config.h:7). The sizes come from the embedding ([vocab][d_model]) and
+ * the first up_proj ([hidden][d_model]); every file's header (float32, C
+ * order, complete data) and shape is checked before ctx is used or anything is
+ * allocated, so a Git-LFS pointer, a wrong dtype or shape or a truncated file
+ * is reported (DT_ERR_IO) without touching the device.
  */
 typedef struct dt_model dt_model;
 int dt_model_create(dt_ctx* ctx, int n_layers, int d_model, int n_heads, int hidden, int vocab, dt_model** out);

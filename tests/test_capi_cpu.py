@@ -201,3 +201,50 @@ def test_bwd_dq_option_validation():
     lib = C.lib()
     assert lib.dt_ctx_set_option(None, C.DT_OPT_BWD_DQ, C.DT_BWD_DQ_FROM_DS) == C.DT_ERR_INVALID_ARG
     assert "ctx is NULL" in last_error()
+
+
+def _save_model(folder, n_layers=2, vocab=300, hidden=256, d_model=256):
+    from dirktensor_amd import synth
+
+    params = synth.model_params(n_layers, vocab, hidden, d_model, seed_base=7700)
+    for name, arr in params.items():
+        np.save(os.path.join(folder, name + ".npy"), arr.astype(np.float32))
+    return params
+
+
+def test_model_loader_validates_every_file(tmp_path):
+    """dt_model_load (the OlmoModel(folder) constructor, OlmoModel.cpp:12-23) checks every file's header and shape
+    before it needs a device: a complete folder stops only at the missing context; a Git-LFS pointer, a float64
+    file, a wrong shape, a truncated file or a missing block are each reported as DT_ERR_IO."""
+    lib = C.lib()
+    h = ctypes.c_void_p()
+    d = str(tmp_path)
+    _save_model(d)
+    assert lib.dt_model_load(None, d.encode(), 2, ctypes.byref(h)) == C.DT_ERR_INVALID_ARG
+    assert "ctx is NULL" in last_error()
+    assert lib.dt_model_load(None, d.encode(), 3, ctypes.byref(h)) == C.DT_ERR_IO  # no block 2
+    assert "model.layers.2." in last_error() and "cannot open" in last_error()
+    assert lib.dt_model_load(None, d.encode(), 0, ctypes.byref(h)) == C.DT_ERR_INVALID_ARG
+
+    def broken(name, how):
+        sub = tmp_path / f"broken_{how}"
+        sub.mkdir()
+        _save_model(str(sub))
+        p = sub / f"{name}.npy"
+        if how == "lfs":
+            p.write_text("version https://git-lfs.github.com/spec/v1\noid sha256:0\nsize 16777344\n")
+        elif how == "f64":
+            np.save(p, np.load(p).astype(np.float64))
+        elif how == "shape":
+            np.save(p, np.load(p)[:, :-1].copy())
+        elif how == "trunc":
+            p.write_bytes(p.read_bytes()[:-4])
+        return str(sub).encode()
+
+    cases = [("model.layers.1.mlp.down_proj.weight", "lfs", "not a .npy"),
+             ("model.layers.0.self_attn.q_proj.weight", "f64", "float32"),
+             ("model.layers.1.self_attn.o_proj.weight", "shape", "where (256,256,) was expected"),
+             ("lm_head.weight", "trunc", "truncated data")]
+    for name, how, msg in cases:
+        assert lib.dt_model_load(None, broken(name, how), 2, ctypes.byref(h)) == C.DT_ERR_IO, (name, how)
+        assert msg in last_error() and name in last_error(), last_error()

@@ -247,3 +247,26 @@ def test_backward_long_k_products(gpu):
     print("long-K backward: worst " + ", ".join(f"{k} {v:.2e}" for k, v in worst))
     assert max(errs.values()) <= TOL_BF16, worst
     assert all(np.array_equal(runs[0][k], runs[1][k]) for k in p)
+
+
+@pytest.mark.parametrize("mode", ["fp32", "bf16"])
+def test_model_load_from_npy_folder(gpu, params, model, mode, tmp_path_factory):
+    """OlmoModel(folder) (dt_model_load, OlmoModel.cpp:12-23) reads the reference's .npy files: its logits are
+    bit-identical to those of the same parameters set one by one through dt_model_set_param, and every parameter
+    reads back exactly."""
+    folder = tmp_path_factory.mktemp("olmo_npy")
+    for name, arr in params.items():
+        np.save(folder / f"{name}.npy", arr)
+    loaded = OlmoModel(str(folder), N_LAYERS)
+    assert (loaded.n_layers, loaded.d_model, loaded.hidden, loaded.vocab) == (N_LAYERS, 2048, HIDDEN, VOCAB)
+    tok = synth.model_tokens(2, 96, VOCAB, seed=6060)
+    a = torch.empty((2, 96, VOCAB), dtype=torch.float32, device=gpu)
+    b = torch.empty_like(a)
+    loaded.forward(tok, mode=mode, save_for_backward=False, out=a)
+    model.forward(tok, mode=mode, save_for_backward=False, out=b)
+    torch.cuda.synchronize()
+    assert torch.isfinite(a).all()
+    assert torch.equal(a, b)
+    for name in ("model.embed_tokens.weight", "model.layers.1.self_attn.q_norm.weight", "lm_head.weight"):
+        assert np.array_equal(loaded.param(name), params[name]), name
+    loaded.close()
