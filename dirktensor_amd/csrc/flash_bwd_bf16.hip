@@ -55,6 +55,7 @@
 
 #include "dt_internal.h"
 
+#include <climits>
 #include <type_traits>
 #include <utility>
 
@@ -311,6 +312,16 @@ __device__ __forceinline__ void dkdv_block(const FlashBwdArgs& a, int kb_own, in
             // (the dQ pass never reads the dS of such a tile and wave: all of it is masked)
             // with dS stored, keys past T are masked too (their dS would otherwise be exp2(-lse2) (-delta))
             const bool need_mask = (a.causal && q0 < kw + 31) || (kEmitDs && kw + 31 >= T);
+            // masking without branches: element i of query block qb (query q0 + 32*qb + 4*hh + off_i, off_i =
+            // 8*(i/4) + i%4 a constant) is masked when dmask[qb] > off_i, i.e. when key > query (causal) or,
+            // with dS stored, key >= T; dmask is INT_MIN when nothing in the tile is masked
+            int dmask[2];
+#pragma unroll
+            for (int qb = 0; qb < 2; ++qb)
+                dmask[qb] = !need_mask                  ? INT_MIN
+                            : (kEmitDs && key >= T)     ? INT_MAX
+                            : a.causal                  ? key - (q0 + 32 * qb + 4 * hh)
+                                                        : INT_MIN;
             // One software-pipelined sequence of 64 bundles (one LDS fragment read three ahead + one MFMA
             // each), the P / dS arithmetic of one 32-query block riding on the MFMAs of the next phase so
             // that it issues while the matrix pipe works:
@@ -341,9 +352,7 @@ __device__ __forceinline__ void dkdv_block(const FlashBwdArgs& a, int kb_own, in
             };
             auto elem = [&](int qb, int i) {  // P = exp2(S c - lse2), dS = P (dP - delta)
                 float pv = __builtin_amdgcn_exp2f(sc[qb][i] * c - Lr[qb][i]);
-                const int q = q0 + 32 * qb + 8 * (i >> 2) + 4 * hh + (i & 3);
-                if constexpr (kEmitDs) pv = (need_mask && key > (a.causal ? min(q, T - 1) : T - 1)) ? 0.0f : pv;
-                else pv = (need_mask && key > q) ? 0.0f : pv;
+                pv = dmask[qb] > 8 * (i >> 2) + (i & 3) ? 0.0f : pv;
                 p[qb][i] = pv;
                 ds[qb][i] = pv * (dp[qb][i] - Dr[qb][i]);
             };
@@ -458,6 +467,11 @@ __device__ __forceinline__ void dq_block(const FlashBwdArgs& a, int qb_own, int 
             if (has_next) dma(nxt, k0 + kTile);
             if (a.causal && k0 > qw + 31) return;  // every key of the tile follows the wave's queries
             const bool need_mask = (a.causal && k0 + kTile - 1 > qw) || k0 + kTile > T;
+            // masking without branches: element i of key block kb (key k0 + 32*kb + 4*hh + off_i, off_i =
+            // 8*(i/4) + i%4 a constant) is masked when off_i > emask[kb], i.e. when key > lim
+            int emask[2];
+#pragma unroll
+            for (int kb = 0; kb < 2; ++kb) emask[kb] = need_mask ? lim - (k0 + 32 * kb + 4 * hh) : INT_MAX;
             // One software-pipelined sequence of 48 bundles (one LDS fragment read three ahead + one MFMA):
             //   bundles  0..15  S^T and dP^T of keys 0..31   (fragment f = b: K / V rows)
             //   bundles 16..31  S^T and dP^T of keys 32..63; dS of keys 0..31, one element per bundle
@@ -473,8 +487,7 @@ __device__ __forceinline__ void dq_block(const FlashBwdArgs& a, int qb_own, int 
             };
             auto elem = [&](int kb, int i) {  // dS^T = P^T (dP^T - delta), P^T = exp2(S^T c - lse2)
                 float pv = __builtin_amdgcn_exp2f(sc[kb][i] * c - lse2);
-                const int key = k0 + 32 * kb + 8 * (i >> 2) + 4 * hh + (i & 3);
-                pv = (need_mask && key > lim) ? 0.0f : pv;
+                pv = 8 * (i >> 2) + (i & 3) > emask[kb] ? 0.0f : pv;
                 ds[kb][i] = pv * (dp[kb][i] - delta);
             };
             auto pack = [&](int kb, int u) {

@@ -35,6 +35,8 @@
 
 #include "dt_internal.h"
 
+#include <climits>
+
 #include <type_traits>
 #include <utility>
 
@@ -304,6 +306,16 @@ __device__ __forceinline__ void dkdv_block(const FlashBwdArgs& a, int kb_own, in
                 // (the dQ pass never reads the dS of a skipped tile and wave: all of it is masked); with dS
                 // stored, keys past T are masked too (their dS would otherwise be exp2(-lse2) (-delta))
                 const bool need_mask = (a.causal && q0 < kw + 31) || (kEmitDs && kw + 31 >= T);
+                // masking without branches: element i of query block qb (query q0 + 32*qb + 4*hh + off_i,
+                // off_i = 8*(i/4) + i%4) is masked when dmask[qb] > off_i, i.e. when key > query (causal) or,
+                // with dS stored, key >= T; INT_MIN when nothing in the tile is masked
+                int dmask[2];
+#pragma unroll
+                for (int qb = 0; qb < 2; ++qb)
+                    dmask[qb] = !need_mask              ? INT_MIN
+                                : (kEmitDs && key >= T) ? INT_MAX
+                                : a.causal              ? key - (q0 + 32 * qb + 4 * hh)
+                                                        : INT_MIN;
                 floatx16 sc[2], dp[2];
                 // S = Q K^T (raw), dP = dO V^T (two query blocks; explicit calls keep every index static)
                 dot_rows2(sc[0], dp[0], s.q, s.g, 0, ln, hh, kf, vf);
@@ -315,11 +327,7 @@ __device__ __forceinline__ void dkdv_block(const FlashBwdArgs& a, int kb_own, in
                     for (int i = 0; i < 16; ++i) {
                         const int qi = 32 * qb + 8 * (i / 4) + 4 * hh + (i % 4);
                         float pv = __builtin_amdgcn_exp2f(sc[qb][i] * c - s.lse2[qi]);
-                        if constexpr (kEmitDs) {
-                            if (need_mask && key > (a.causal ? min(q0 + qi, T - 1) : T - 1)) pv = 0.0f;
-                        } else {
-                            if (need_mask && key > q0 + qi) pv = 0.0f;
-                        }
+                        pv = dmask[qb] > 8 * (i / 4) + (i % 4) ? 0.0f : pv;
                         sc[qb][i] = pv;
                         dp[qb][i] = pv * (dp[qb][i] - s.delta[qi]);
                     }
@@ -401,6 +409,11 @@ __device__ __forceinline__ void dq_block(const FlashBwdArgs& a, int qb_own, int 
             if (it + 1 < n_steps) fetch(stg[(it + 1) & 1], k0 + kTile);
             if (!(a.causal && k0 > qw + 31)) {
                 const bool need_mask = (a.causal && k0 + kTile - 1 > qw) || k0 + kTile > T;
+                // masking without branches: element i of key block kb (key k0 + 32*kb + 4*hh + off_i, off_i =
+                // 8*(i/4) + i%4) is masked when off_i > emask[kb], i.e. when key > lim
+                int emask[2];
+#pragma unroll
+                for (int kb = 0; kb < 2; ++kb) emask[kb] = need_mask ? lim - (k0 + 32 * kb + 4 * hh) : INT_MAX;
                 floatx16 sc[2], dp[2];
                 // S^T = K Q^T (raw), dP^T = V dO^T (two key blocks; explicit calls keep every index static)
                 dot_rows2(sc[0], dp[0], s.k, s.v, 0, ln, hh, qf, gf);
@@ -411,7 +424,7 @@ __device__ __forceinline__ void dq_block(const FlashBwdArgs& a, int qb_own, int 
 #pragma unroll
                     for (int i = 0; i < 16; ++i) {
                         float pv = __builtin_amdgcn_exp2f(sc[kb][i] * c - lse2);
-                        if (need_mask && k0 + 32 * kb + 8 * (i / 4) + 4 * hh + (i % 4) > lim) pv = 0.0f;
+                        pv = 8 * (i / 4) + (i % 4) > emask[kb] ? 0.0f : pv;
                         ds[kb][i] = pv * (dp[kb][i] - delta);
                     }
                 acc_cols(dq, s.k, ln, hh, ds);  // dQ^T += K^T dS^T
