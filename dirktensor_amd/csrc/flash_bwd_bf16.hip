@@ -332,9 +332,9 @@ __device__ __forceinline__ void dkdv_block(const FlashBwdArgs& a, int kb_own, in
             // Row fragment f < 32: 16*qb + 2*cc + w (w = 0: Q for S, 1: dO for dP); transposed fragment
             // f >= 32: 2*ci + w with ci = 8*qb + 4*u + db (w = 0: dO^T for dV, 1: Q^T for dK).
             // Element i of block qb is query q0 + 32*qb + 8*(i/4) + 4*hh + i%4.
+            // the rows' lse2 and delta of query block qb, read from LDS a few bundles before block qb's P and dS
             float Lr[2][16], Dr[2][16];
-#pragma unroll
-            for (int qb = 0; qb < 2; ++qb)
+            auto load_stats = [&](int qb) {
 #pragma unroll
                 for (int g = 0; g < 4; ++g) {
                     const int qi = 32 * qb + 8 * g + 4 * hh;
@@ -343,6 +343,7 @@ __device__ __forceinline__ void dkdv_block(const FlashBwdArgs& a, int kb_own, in
                     Lr[qb][4 * g] = L4.x, Lr[qb][4 * g + 1] = L4.y, Lr[qb][4 * g + 2] = L4.z, Lr[qb][4 * g + 3] = L4.w;
                     Dr[qb][4 * g] = D4.x, Dr[qb][4 * g + 1] = D4.y, Dr[qb][4 * g + 2] = D4.z, Dr[qb][4 * g + 3] = D4.w;
                 }
+            };
             floatx16 sc[2], dp[2];
             float p[2][16], ds[2][16];
             bf16x8 pb[2][2], dsb[2][2];
@@ -372,6 +373,7 @@ __device__ __forceinline__ void dkdv_block(const FlashBwdArgs& a, int kb_own, in
             ring[2] = rd(2);
             static_for<64>([&](auto B) {
                 constexpr int b = decltype(B)::value;
+                if constexpr (b == 12 || b == 28) load_stats(b >= 16);  // (all at the start: 1-2 % slower)
                 if constexpr (b + 3 < 64) ring[(b + 3) & 3] = rd(b + 3);
                 if constexpr (b < 32) {
                     constexpr int qb = b >> 4, cc = (b >> 1) & 7;
