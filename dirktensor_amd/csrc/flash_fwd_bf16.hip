@@ -12,6 +12,9 @@
 //     (few heads, e.g. a tensor-parallel shard), items are split into parts of
 //     consecutive key tiles on different workgroups; each part writes its
 //     partial (m, l, O) to a workspace and the last one to finish merges them.
+//   * A launch that fits one round folds its units (flash_items.h): a unit is then
+//     the 64-query tiles p and n-1-p of one (batch, head), as one 128-query item
+//     whose rows 0-63 are tile p, so every workgroup gets the same work.
 //   * A workgroup has 8 waves in two groups of 4. Both groups hold the same 128
 //     queries (32 per wave) and split the key tiles: group g takes 64-key tiles
 //     g, g+2, g+4, ... At the end group 1 hands its partial (max, sum, O) to
@@ -82,7 +85,6 @@ typedef __attribute__((address_space(3))) void lds_void;
 typedef unsigned v4u32 __attribute__((ext_vector_type(4)));
 
 constexpr int kD = 128;
-constexpr int kBM = kItemRows;  // queries per item
 constexpr int kBN = 64;        // keys per tile
 constexpr int kThreads = 512;  // 8 waves
 constexpr int kRowBytes = 256;               // one K or V row (128 bf16), unpadded
@@ -286,7 +288,10 @@ __global__ __launch_bounds__(kThreads, 1) void flash_fwd_bf16_kernel(FlashArgs a
     const int lane = tid & 63;
     const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);  // wave-uniform, held in an SGPR
     const int grp = wave >> 2;  // key-tile group
-    const int wq = wave & 3;    // 32-query block within the item (also this wave's share of a DMA tile)
+    // 32-query block within the item (also this wave's share of a DMA tile). In a folded launch group 1's
+    // waves take the blocks in the other half, so each SIMD (waves w and w + 4) holds one wave of each
+    // 64-query tile and keeps one wave busy after the lower tile's keys run out.
+    const int wq = (wave & 3) ^ (sc.fold ? 2 * grp : 0);
     const int ln = lane & 31;
     const int hh = lane >> 5;
 
@@ -300,13 +305,14 @@ __global__ __launch_bounds__(kThreads, 1) void flash_fwd_bf16_kernel(FlashArgs a
         for (int i = 0; i < 4; ++i) voff[i] = (uint32_t)(((16 * i + 4 * wq + rlo) * a.ldk + 8 * chunk) * 2);
     }
     // Q DMA of an item's 128 rows: instruction i of wave w fills rows 32*i + 4*w + lane/16, in the same
-    // swizzled layout (swz(32*i + 4*w + lane/16) = 4*(lane/16) + (w & 3) does not depend on i)
-    uint32_t qoff[4];
+    // swizzled layout (swz(32*i + 4*w + lane/16) = 4*(lane/16) + (w & 3) does not depend on i); instructions
+    // 0-1 read the item's first 64 rows and 2-3 its second 64, each from its own base
+    uint32_t qoff[2];
     {
         const int rlo = lane >> 4;
         const int chunk = (lane & 15) ^ (4 * rlo + (wave & 3));
 #pragma unroll
-        for (int i = 0; i < 4; ++i) qoff[i] = (uint32_t)(((32 * i + 4 * wave + rlo) * a.ldq + 8 * chunk) * 2);
+        for (int i = 0; i < 2; ++i) qoff[i] = (uint32_t)(((32 * i + 4 * wave + rlo) * a.ldq + 8 * chunk) * 2);
     }
     // K fragment reads: row 32*kb + ln, chunk 2*cc + hh
     uint32_t kaddr[8];
@@ -350,8 +356,8 @@ __global__ __launch_bounds__(kThreads, 1) void flash_fwd_bf16_kernel(FlashArgs a
         const int k_next = snake_item(round + 1, G, (int)blockIdx.x);
         const int b = u.b, h = u.h;
         const int L = u.L;
-        const int q0 = u.qt * kBM;
-        const int qw0 = q0 + wq * 32;
+        const int q0 = u.qa;
+        const int qw0 = (wq < 2 ? u.qa : u.qb - 64) + wq * 32;  // this wave's first query
         const int qrow = qw0 + ln;
 
         const uint16_t* Qg = static_cast<const uint16_t*>(a.q) + (int64_t)b * T * a.ldq + (int64_t)h * kD;
@@ -375,7 +381,7 @@ __global__ __launch_bounds__(kThreads, 1) void flash_fwd_bf16_kernel(FlashArgs a
             continue;  // no LDS was touched: no barrier needed
         }
 
-        const int k_end = a.causal ? min(q0 + kBM, L) : L;
+        const int k_end = a.causal ? min(u.qb + 64, L) : L;
         // this unit's key tiles t0 .. t1-1: the whole item, or part u.part of S tiles (the last one the rest)
         const int n_item_tiles = (k_end + kBN - 1) / kBN;
         const int t0 = u.parts > 1 ? u.part * sc.S : 0;
@@ -400,11 +406,13 @@ __global__ __launch_bounds__(kThreads, 1) void flash_fwd_bf16_kernel(FlashArgs a
         }
         uint8_t* Qs = &stage1[0][0][0];  // 128 rows x 256 bytes (group 0's K and V areas of stage1)
         {
-            const __amdgpu_buffer_rsrc_t rq = make_rsrc(Qg + (int64_t)q0 * a.ldq, (uint32_t)(T - q0) * (uint32_t)a.ldq * 2u);
-#pragma unroll
-            for (int i = 0; i < 4; ++i)
-                __builtin_amdgcn_raw_ptr_buffer_load_lds(rq, (lds_void*)(Qs + i * 8192 + wave * 1024), 16, qoff[i], 0, 0,
-                                                         0);
+            const __amdgpu_buffer_rsrc_t rqa = make_rsrc(Qg + (int64_t)u.qa * a.ldq, (uint32_t)(T - u.qa) * (uint32_t)a.ldq * 2u);
+            const __amdgpu_buffer_rsrc_t rqb =
+                make_rsrc(Qg + (int64_t)u.qb * a.ldq, (uint32_t)max(T - u.qb, 0) * (uint32_t)a.ldq * 2u);
+            __builtin_amdgcn_raw_ptr_buffer_load_lds(rqa, (lds_void*)(Qs + wave * 1024), 16, qoff[0], 0, 0, 0);
+            __builtin_amdgcn_raw_ptr_buffer_load_lds(rqa, (lds_void*)(Qs + 8192 + wave * 1024), 16, qoff[1], 0, 0, 0);
+            __builtin_amdgcn_raw_ptr_buffer_load_lds(rqb, (lds_void*)(Qs + 16384 + wave * 1024), 16, qoff[0], 0, 0, 0);
+            __builtin_amdgcn_raw_ptr_buffer_load_lds(rqb, (lds_void*)(Qs + 24576 + wave * 1024), 16, qoff[1], 0, 0, 0);
         }
         if (k_next < sc.n_units) u_next = decode_unit(k_next, sc, a.H, cum_lds);
 
@@ -578,16 +586,16 @@ __global__ __launch_bounds__(kThreads, 1) void flash_fwd_bf16_kernel(FlashArgs a
         }
         if (u.parts == 1) {  // the item's 128 output rows: 16 lanes per 256-byte row, 4 rows per store instruction
             lds_barrier();
-            const int nrows = min(kBM, T - q0);
 #pragma unroll
             for (int j = 0; j < 4; ++j) {
                 const int ch = j * kThreads + tid;  // 16-byte chunk ch % 16 of row ch / 16
                 const int r = ch >> 4, c = ch & 15;
+                const int qr = (j < 2 ? u.qa : u.qb - 64) + r;  // rows 0-63 in j = 0, 1; rows 64-127 in j = 2, 3
                 const uint4 w = *reinterpret_cast<const uint4*>(obuf + r * kObufRow + 16 * c);
                 // streaming (non-temporal) stores: whole 256-byte rows this kernel never reads back
-                if (r < nrows)
+                if (qr < T)
                     __builtin_nontemporal_store((u32x4){w.x, w.y, w.z, w.w},
-                                                reinterpret_cast<u32x4*>(&Og[(int64_t)(q0 + r) * a.ldo + 8 * c]));
+                                                reinterpret_cast<u32x4*>(&Og[(int64_t)qr * a.ldo + 8 * c]));
             }
         }
         if (u.parts > 1) {  // the same for every wave of the workgroup
@@ -696,7 +704,7 @@ static int plan(const FlashArgs& a, const SeqLens* lens, int* grid, Schedule* sc
     // the schedule is planned for one workgroup per CU; the grid is then at most one per unit
     int cus = 0;
     DT_TRY(persistent_grid(0x7fffffff, &cus));
-    build_schedule(a, sl, cus, true, sc);
+    build_schedule(a, sl, cus, true, sc, true);
     *grid = sc->n_units < cus ? sc->n_units : cus;
     return DT_OK;
 }
@@ -720,7 +728,7 @@ int launch_flash_fwd_bf16(const FlashArgs& a, const SeqLens* lens, hipStream_t s
         SeqLens sl;
         if (a.ragged) sl = *lens;
         else sl.len[0] = a.T;
-        build_schedule(a, sl, grid, false, &sc);
+        build_schedule(a, sl, grid, false, &sc, true);
         grid = sc.n_units < grid ? sc.n_units : grid;
     }
     hipLaunchKernelGGL(flash_fwd_bf16_kernel, dim3(grid), dim3(kThreads), 0, stream, a, sc);

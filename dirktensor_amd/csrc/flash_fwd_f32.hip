@@ -4,7 +4,9 @@
 // runs 256x256 tiles with two cblas_sgemm calls per tile and a scalar softmax;
 // here a persistent workgroup walks 128-query items (flash_items.h: snake order
 // over items sorted by causal cost, so a long query tile is paired with a short
-// one) and streams 32-key tiles of K and V through LDS.
+// one) and streams 32-key tiles of K and V through LDS. A launch that fits one
+// round folds its units instead (flash_items.h): an item is then the 64-query
+// tiles p and n-1-p of one (batch, head), rows 0-63 and 64-127.
 //
 // Work split: 8 waves in two groups of 4. Both groups hold the same 128 queries
 // (32 per wave) and split the key tiles: group g takes tiles g, g+2, g+4, ... At
@@ -105,7 +107,9 @@ __global__ __launch_bounds__(kThreads, 1) void flash_fwd_f32_kernel(FlashArgs a,
     const int lane = tid & 63;
     const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
     const int grp = wave >> 2;  // key-tile group
-    const int wq = wave & 3;    // 32-query block within the item (also this wave's share of a DMA tile)
+    // 32-query block within the item (also this wave's share of a DMA tile); in a folded launch group 1's
+    // waves take the blocks in the other half, so each SIMD holds one wave of each 64-query tile
+    const int wq = (wave & 3) ^ (sc.fold ? 2 * grp : 0);
     const int ln = lane & 31;   // query within the wave's 32 (MFMA n index)
     const int hh = lane >> 5;   // lane half (MFMA k index)
 
@@ -130,8 +134,8 @@ __global__ __launch_bounds__(kThreads, 1) void flash_fwd_f32_kernel(FlashArgs a,
         const Unit u = decode_unit(k_unit, sc, a.H, sc.cum);  // a whole item: this kernel's schedules split nothing
         const int b = u.b, h = u.h;
         const int L = u.L;  // valid keys / rows of this sequence
-        const int q0 = u.qt * kBM;
-        const int qw0 = q0 + wq * 32;  // first query of this wave
+        const int q0 = u.qa;
+        const int qw0 = (wq < 2 ? u.qa : u.qb - 64) + wq * 32;  // first query of this wave
         const int qrow = qw0 + ln;
 
         const float* Qg = static_cast<const float*>(a.q) + (int64_t)b * T * a.ldq + (int64_t)h * kD;
@@ -152,7 +156,7 @@ __global__ __launch_bounds__(kThreads, 1) void flash_fwd_f32_kernel(FlashArgs a,
             continue;  // no LDS was touched: no barrier needed
         }
 
-        const int k_end = a.causal ? min(q0 + kBM, L) : L;
+        const int k_end = a.causal ? min(u.qb + 64, L) : L;
         const int n_tiles = (k_end + kBN - 1) / kBN;
         const int n_steps = (n_tiles + 1) / 2;
 
@@ -368,7 +372,7 @@ int launch_flash_fwd_f32(const FlashArgs& a, const SeqLens* lens, hipStream_t st
     int grid = 0;
     DT_TRY(persistent_grid((int64_t)((a.T + kBM - 1) / kBM) * a.B * a.H, &grid));
     Schedule sc;
-    build_schedule(a, sl, grid, false, &sc);
+    build_schedule(a, sl, grid, false, &sc, true);
     hipLaunchKernelGGL(flash_fwd_f32_kernel, dim3(grid), dim3(kThreads), 0, stream, a, sc);
     DT_HIP_TRY(hipGetLastError());
     return DT_OK;

@@ -12,6 +12,13 @@
 // part) pair, and its units are that tile's items, one per (sequence, head) whose sequence reaches the
 // tile (every sequence when the batch is not ragged), sequences by decreasing length, heads fastest.
 // Padding tiles (past a sequence's end, which only write the empty rows) come last.
+//
+// Folded units. A causal launch that fits one round (at most one unit per workgroup, no split, full
+// sequences, T a multiple of 128) has nothing for the snake to pair, so its longest query tile sets the
+// launch time while the average costs half as much. Such a launch folds instead: a unit is the 64-query
+// tiles p and n-1-p (n = T / 64) of one (batch, head), which together cost n + 1 64-query key steps for
+// every p. The kernel runs a folded unit as a 128-query item whose rows 0-63 are tile p and rows 64-127
+// tile n-1-p, over the key tiles of the upper one; the waves of tile p skip the key tiles past it.
 #pragma once
 
 #include "dt_internal.h"
@@ -31,6 +38,7 @@ struct Schedule {
     int n_kinds;
     int n_units;
     int dense;    // 1: no padding and nothing split, so kind j is query tile n_qt-1-j with B*H units
+    int fold;     // 1 (dense only): unit kind j is the folded pair of 64-query tiles j and 2*n_qt-1-j
     int n_qt;
     int S;        // 64-key tiles per part of a split item (0: nothing is split)
     int n_slots;  // split items: one counter and kMaxParts partial results each
@@ -43,6 +51,7 @@ struct Schedule {
 
 struct Unit {
     int b, h, qt, L;    // sequence, head, query tile, the sequence's length
+    int qa, qb;         // first query of the item's rows 0-63 and of its rows 64-127 (qa + 64 unless folded)
     int part, parts;    // parts == 1: a whole item
     int slot;           // split items: workspace slot
     bool pad;           // a padding tile
@@ -65,7 +74,15 @@ __host__ __device__ inline Unit decode_unit(int k, const Schedule& sc, int H, co
         const int BH = sc.cum[1];
         const int r = k % BH;
         Unit u;
-        u.qt = sc.n_qt - 1 - k / BH;
+        if (sc.fold) {
+            u.qt = k / BH;
+            u.qa = 64 * u.qt;
+            u.qb = 64 * (2 * sc.n_qt - 1 - u.qt);
+        } else {
+            u.qt = sc.n_qt - 1 - k / BH;
+            u.qa = u.qt * kItemRows;
+            u.qb = u.qa + 64;
+        }
         u.part = 0;
         u.parts = 1;
         u.pad = false;
@@ -85,6 +102,8 @@ __host__ __device__ inline Unit decode_unit(int k, const Schedule& sc, int H, co
     const int r = k - cum[lo];
     Unit u;
     u.qt = info & 0xff;
+    u.qa = u.qt * kItemRows;
+    u.qb = u.qa + 64;
     u.part = (info >> 8) & 0xf;
     u.parts = (info >> 12) & 0xf;
     u.pad = (info >> 16) & 1;
@@ -104,8 +123,9 @@ inline int tile_cost(int qt, int L, int causal) {
     return (k_end + 63) / 64;
 }
 
-// Builds the schedule of one launch on G workgroups; split = 0 keeps every item whole.
-inline void build_schedule(const FlashArgs& a, const SeqLens& sl, int G, bool split, Schedule* sc) {
+// Builds the schedule of one launch on G workgroups; split = 0 keeps every item whole; fold = 0 never
+// folds (a kernel that cannot run folded units).
+inline void build_schedule(const FlashArgs& a, const SeqLens& sl, int G, bool split, Schedule* sc, bool fold = false) {
     *sc = Schedule{};
     const int n_qt = (a.T + kItemRows - 1) / kItemRows;
     int idx[kMaxRaggedBatch];
@@ -139,6 +159,22 @@ inline void build_schedule(const FlashArgs& a, const SeqLens& sl, int G, bool sp
         if (S >= cmax) S = 0;
     }
     sc->S = S;
+    // a launch that splits nothing and fits one round folds (see the top of this file)
+    if (fold && S == 0 && a.causal && !a.ragged && a.T % kItemRows == 0 && n_qt >= 2 && G > 0 &&
+        (int64_t)a.B * a.H * n_qt <= G) {
+        // kind j: the pair (j, 2*n_qt-1-j) of 64-query tiles; every pair costs 2*n_qt+1 tile steps of 64 queries
+        for (int j = 0; j < n_qt; ++j) {
+            sc->kind[j] = j;
+            sc->cum[j + 1] = sc->cum[j] + a.B * a.H;
+            sc->nb[j] = a.B;
+        }
+        sc->n_kinds = n_qt;
+        sc->n_units = sc->cum[n_qt];
+        sc->n_qt = n_qt;
+        sc->dense = 1;
+        sc->fold = 1;
+        return;
+    }
     struct K {
         int cost, qt, part, parts, pad, count;
     };

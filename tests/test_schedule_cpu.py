@@ -30,3 +30,8 @@ def test_schedule_covers_every_tile_once(tmp_path):
     lines = {l.split(":")[0]: l for l in r.stdout.splitlines()}
     assert "split items 0," not in lines["B=1 T=4096 H=2 causal=1 dense cus=256"]
     assert "split items 0," in lines["B=1 T=4096 H=16 causal=1 dense cus=256"]
+    # a launch of one round folds its units; more than one round, a split launch or a ragged batch does not
+    assert "fold 1," in lines["B=1 T=2048 H=16 causal=1 dense cus=256"]
+    assert "fold 0," in lines["B=1 T=4096 H=16 causal=1 dense cus=256"]
+    assert "fold 0," in lines["B=1 T=4096 H=2 causal=1 dense cus=256"]
+    assert "fold 0," in lines["B=8 T=2048 H=16 causal=1 ragged cus=256"]
