@@ -138,6 +138,37 @@ def test_split_items(gpu, B, T, H, lens):
 
 
 @pytest.mark.parametrize("mode", ["fp32", "bf16"])
+@pytest.mark.parametrize("B,T,H", [(1, 1024, 16), (2, 2048, 8), (1, 256, 3), (1, 2048, 16)])
+def test_folded_launches(gpu, mode, B, T, H):
+    """Causal launches of at most one 128-query unit per CU fold their units (64-query tiles p and n-1-p of
+    one head per workgroup): against the oracle; causality bit-exact for a row of a lower tile and one of an
+    upper tile; and bit-identical to the unfolded schedule, which the same heads take when the launch holds
+    copies of its heads beyond one round of a 256-CU part."""
+    Q, K, V = synth.qkv(B, T, H, seeds=(41 + T, 42 + T, 43 + T))
+    O_ref, m_ref, l_ref = oracle.flash_attention_forward(Q, K, V, SCALE)
+    O, m, l = gpu_flash(Q, K, V, gpu, mode)
+    tol = TOL_FP32 if mode == "fp32" else TOL_BF16
+    err = rel_err(O, O_ref)
+    print(f"folded B={B} T={T} H={H} {mode}: rel err {err:.3e}", flush=True)
+    assert err <= tol
+    check_stats(m, l, m_ref, l_ref, tol)
+    for t in (T // 8 + 5, T - T // 16 - 3):
+        K2, V2 = K.copy(), V.copy()
+        K2[:, t + 1:] = synth.normal(79, K2[:, t + 1:].shape)
+        V2[:, t + 1:] = synth.normal(80, V2[:, t + 1:].shape)
+        O2, m2, l2 = gpu_flash(Q, K2, V2, gpu, mode)
+        assert np.array_equal(O2[:, :t + 1], O[:, :t + 1])
+        assert np.array_equal(m2[:, :t + 1], m[:, :t + 1]) and np.array_equal(l2[:, :t + 1], l[:, :t + 1])
+    rep = 300 // (B * H * (T // 128)) + 1  # more than 300 units: more than one round on up to 300 CUs
+    dup = [np.concatenate([x] * rep, axis=2) for x in (Q, K, V)]
+    O3, m3, l3 = gpu_flash(*dup, gpu, mode)
+    for r in range(rep):
+        part = slice(r * H, (r + 1) * H)
+        assert np.array_equal(O3[:, :, part], O) and np.array_equal(m3[:, :, part], m)
+        assert np.array_equal(l3[:, :, part], l)
+
+
+@pytest.mark.parametrize("mode", ["fp32", "bf16"])
 def test_properties_full_size(gpu, mode):
     """Size-independent checks at T=4096, H=16: row 0 returns V[0] exactly (one key, p=1, l=1);
     changing K/V after position t leaves rows <= t bit-identical (causality); heads are independent."""
