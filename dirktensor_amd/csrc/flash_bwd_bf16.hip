@@ -297,8 +297,10 @@ __device__ __forceinline__ void dkdv_block(const FlashBwdArgs& a, int kb_own, in
                 return make_rsrc(a.ds_ws, 0u);
             }
         }();
-        const uint32_t ds_row = (uint32_t)((32 * wave + ln) * kDsRowBytes);
-        const uint32_t ds_xs = (uint32_t)((hh ^ (2 * (ln & 3))) << 4);
+        // unit (key row r = 32*wave + ln, store k = 2*qb + u, half hh) of a block at
+        // ((((r/32)*8 + (r%32)/4)*4 + k)*4 + r%4)*2 + hh, times 16 bytes: every store instruction writes
+        // eight whole 128-byte runs (four keys' two halves), and so does every read of the dQ pass's DMA
+        const uint32_t ds_lane = (uint32_t)(((wave * 8 + (ln >> 2)) * 32 + (ln & 3) * 2 + hh) * 16);
 
         auto dma = [&](DkdvStage& s, int q0) {
             dma_tile(s.q, Qg, q0, T, a.ld_qkv, voff_q, wave);
@@ -391,7 +393,7 @@ __device__ __forceinline__ void dkdv_block(const FlashBwdArgs& a, int kb_own, in
                 if constexpr (kEmitDs && (b == 24 || b == 32 || b == 40 || b == 48)) {
                     constexpr int qb = (b - 24) >> 4, u = ((b - 24) >> 3) & 1;
                     __builtin_amdgcn_raw_buffer_store_b128(__builtin_bit_cast(u32x4, dsb[qb][u]), ds_rsrc,
-                                                          ds_row + (((4 * qb + 2 * u) << 4) ^ ds_xs),
+                                                          ds_lane + (uint32_t)((2 * qb + u) * 128),
                                                           (int)((q0 - q_begin) / kTile) * kDsBlockBytes, 0);
                 }
                 DT_BUNDLE_END;
@@ -620,6 +622,14 @@ __device__ __forceinline__ void dq_ds_block(const FlashBwdArgs& a, int qb_own, i
 
     // tile kt -> stage kt % 5: four DMA instructions per wave, also for kt past the range (an empty buffer
     // then: nothing is read, the stage is not used), so that the count of requests in flight is fixed
+    // the global unit that LDS chunk wave*64 + lane of a tile's half holds: row 8*wave + lane/8 of the tile
+    // (rows of the workspace block: 64*(kt & 1) + that), position lane%8, unit (position) ^ 2*(row & 3)
+    uint32_t ds_src;
+    {
+        const int rl = lane >> 3;
+        const int k8 = (lane & 7) ^ (2 * (rl & 3));
+        ds_src = (uint32_t)(((((wave >> 2) * 8 + 2 * (wave & 3) + (rl >> 2)) * 32 + (k8 >> 1) * 8 + (rl & 3) * 2 + (k8 & 1)) * 16));
+    }
     auto dma = [&](int kt) {
         DsqStage& s = st[kt % kDqStages];
         const bool live = kt < n_tiles;
@@ -635,8 +645,7 @@ __device__ __forceinline__ void dq_ds_block(const FlashBwdArgs& a, int qb_own, i
         const uint32_t chunk = (uint32_t)(wave * 64);              // 16-byte chunks of an 8 KB half
 #pragma unroll
         for (int t = 0; t < 2; ++t)
-            dma16(__builtin_amdgcn_readfirstlane(lds_addr(s.ds[t] + chunk * 16)),
-                  (uint32_t)t * kDsBlockBytes + rows + (chunk + (uint32_t)lane) * 16u, r);
+            dma16(__builtin_amdgcn_readfirstlane(lds_addr(s.ds[t] + chunk * 16)), (uint32_t)t * kDsBlockBytes + rows + ds_src, r);
     };
     auto step = [&](int kt) {
         const DsqStage& s = st[kt % kDqStages];
