@@ -339,9 +339,11 @@ def _extra(fn):
 
 def extra_fp32_exact(args, dev, stream, ctx) -> dict:
     """The reference's own precision: the same attention workload in fp32 exact mode (fp32 MFMA), timed like
-    the headline (the clock is already settled), with its parity against the oracle on two heads."""
+    the headline, with its parity against the oracle on two heads. The clock is settled again first: the CPU
+    baseline before it leaves the GPU idle for seconds."""
     a = argparse.Namespace(**{**vars(args), "mode": "fp32"})
     wl = wl_flash_fwd(a, dev, stream, ctx)
+    settle_clock(wl["step"], stream)
     for _ in range(5):
         wl["step"]()
     steps = 20
@@ -361,6 +363,7 @@ def extra_prefill(args, dev, stream, ctx) -> dict:
 
     a = argparse.Namespace(**{**vars(args), "T": 2048, "mode": "bf16"})
     wl = wl_model_fwd(a, dev, stream, ctx)
+    settle_clock(wl["step"], stream)
     for _ in range(3):
         wl["step"]()
     steps = 10
