@@ -601,24 +601,15 @@ __device__ __forceinline__ void dq_ds_block(const FlashBwdArgs& a, int qb_own, i
     const int i16 = lane & 15, G = lane >> 4;
     const uint32_t ds_addr = (uint32_t)(qt * kDsHalfBytes + (4 * hh + (i16 >> 2)) * kDsRowBytes +
                                         (((4 * qh + 2 * (G & 1) + (i16 & 1)) ^ (2 * (i16 >> 2))) << 4) + 8 * ((i16 & 3) >> 1));
-    auto read_ds = [&](const uint8_t* ds, int c) {  // keys 16*c + {4*hh .. +3, 8 + 4*hh .. +3}: the B operand
-        const shortx4 lo = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_shortx4*)(ds + ds_addr + 16 * c * kDsRowBytes));
-        const shortx4 hi =
-            __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_shortx4*)(ds + ds_addr + (16 * c + 8) * kDsRowBytes));
-        return __builtin_bit_cast(bf16x8, (shortx8){lo[0], lo[1], lo[2], lo[3], hi[0], hi[1], hi[2], hi[3]});
-    };
-    auto read_kt = [&](const uint8_t* tile, int c, int d) {  // K^T chunk: keys of 16-key chunk c, dims 32*(2*dsel + d) ..
-        const int rows = (c >> 1) * 8192 + (c & 1) * 4096;
-        const shortx4 lo = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_shortx4*)(tile + taddr[0][d] + rows));
-        const shortx4 hi = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_shortx4*)(tile + taddr[1][d] + rows + 2048));
-        return __builtin_bit_cast(bf16x8, (shortx8){lo[0], lo[1], lo[2], lo[3], hi[0], hi[1], hi[2], hi[3]});
-    };
 
     floatx16 dq[2] = {zero16(), zero16()};
     const int k_end = a.causal ? min(qb_own * kBlk + kBlk, T) : T;
     const int n_tiles = (k_end + kTile - 1) / kTile;
     const int qt0 = 2 * qb_own;  // the block's first 64-query tile
     const int n_qt = min(2, lay.nqt - qt0);
+    // the tiles this wave multiplies: 0 .. n_use-1 (no query of the wave, or every key of a later tile
+    // after its queries under causality, leaves the rest to the other waves)
+    const int n_use = qw >= T ? 0 : (a.causal ? min(n_tiles, (qw + 31) / kTile + 1) : n_tiles);
 
     // tile kt -> stage kt % 5: four DMA instructions per wave, also for kt past the range (an empty buffer
     // then: nothing is read, the stage is not used), so that the count of requests in flight is fixed
@@ -630,57 +621,85 @@ __device__ __forceinline__ void dq_ds_block(const FlashBwdArgs& a, int qb_own, i
         const int k8 = (lane & 7) ^ (2 * (rl & 3));
         ds_src = (uint32_t)(((((wave >> 2) * 8 + 2 * (wave & 3) + (rl >> 2)) * 32 + (k8 >> 1) * 8 + (rl & 3) * 2 + (k8 & 1)) * 16));
     }
-    auto dma = [&](int kt) {
-        DsqStage& s = st[kt % kDqStages];
+    const uint32_t lds0 = lds_addr(&st[0]);  // stage s starts at lds0 + s * sizeof(DsqStage)
+    auto dma = [&](int kt, int stage) {
+        const uint32_t sb = lds0 + (uint32_t)stage * (uint32_t)sizeof(DsqStage);
         const bool live = kt < n_tiles;
         const int k0 = live ? kt * kTile : 0;
         const __amdgpu_buffer_rsrc_t rk = make_rsrc(Kg + (int64_t)k0 * a.ld_qkv, live ? (uint32_t)(T - k0) * (uint32_t)a.ld_qkv * 2u : 0u);
-        const uint32_t lk = __builtin_amdgcn_readfirstlane(lds_addr(s.k + wave * 1024));
+        const uint32_t lk = sb + (uint32_t)offsetof(DsqStage, k) + (uint32_t)wave * 1024u;
         dma16(lk, voff[0], rk);
         dma16(lk + 8192, voff[1], rk);
         const int kb = k0 / kBlk;
         const uint8_t* blk = ds_head + (uint64_t)(lay.block_offset(kb) + (qt0 - lay.first_tile(kb))) * kDsBlockBytes;
         const __amdgpu_buffer_rsrc_t r = make_rsrc(blk, live ? (uint32_t)n_qt * kDsBlockBytes : 0u);
         const uint32_t rows = (uint32_t)(kt & 1) * kDsHalfBytes;  // this tile's rows of the key block
-        const uint32_t chunk = (uint32_t)(wave * 64);              // 16-byte chunks of an 8 KB half
+        const uint32_t ld = sb + (uint32_t)offsetof(DsqStage, ds) + (uint32_t)wave * 1024u;  // 16-byte chunks wave*64 ..
 #pragma unroll
-        for (int t = 0; t < 2; ++t)
-            dma16(__builtin_amdgcn_readfirstlane(lds_addr(s.ds[t] + chunk * 16)), (uint32_t)t * kDsBlockBytes + rows + ds_src, r);
+        for (int t = 0; t < 2; ++t) dma16(ld + (uint32_t)t * kDsHalfBytes, (uint32_t)t * kDsBlockBytes + rows + ds_src, r);
     };
-    auto step = [&](int kt) {
-        const DsqStage& s = st[kt % kDqStages];
-        const int k0 = kt * kTile;
-        if (qw >= T || (a.causal && k0 > qw + 31)) return;  // no query of the wave, or every key after them
+    // one tile's product from stage `stage`: the stage's base is added to this lane's five read offsets once,
+    // and the reads' remaining offsets are constants (immediate offsets of the LDS reads)
+    auto step = [&](int kt, int stage) {
+        const uint32_t sb = lds0 + (uint32_t)stage * (uint32_t)sizeof(DsqStage);
+        uint32_t kbase[2][2];
+#pragma unroll
+        for (int r = 0; r < 2; ++r)
+#pragma unroll
+            for (int d = 0; d < 2; ++d) kbase[r][d] = taddr[r][d] + sb + (uint32_t)offsetof(DsqStage, k);
+        const uint32_t dbase = ds_addr + sb + (uint32_t)offsetof(DsqStage, ds);
+        auto tr = [](uint32_t x) { return __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_shortx4*)(uintptr_t)x); };
+        auto read_ds = [&](int c) {  // keys 16*c + {4*hh .. +3, 8 + 4*hh .. +3}: the B operand
+            const shortx4 lo = tr(dbase + 16 * c * kDsRowBytes);
+            const shortx4 hi = tr(dbase + (16 * c + 8) * kDsRowBytes);
+            return __builtin_bit_cast(bf16x8, (shortx8){lo[0], lo[1], lo[2], lo[3], hi[0], hi[1], hi[2], hi[3]});
+        };
+        auto read_kt = [&](int c, int d) {  // K^T chunk: keys of 16-key chunk c, dims 32*(2*dsel + d) ..
+            const uint32_t rows = (c >> 1) * 8192 + (c & 1) * 4096;
+            const shortx4 lo = tr(kbase[0][d] + rows);
+            const shortx4 hi = tr(kbase[1][d] + rows + 2048);
+            return __builtin_bit_cast(bf16x8, (shortx8){lo[0], lo[1], lo[2], lo[3], hi[0], hi[1], hi[2], hi[3]});
+        };
         // the second 32 keys are all after the wave's queries under causality: their dS was not stored
-        const bool second = !a.causal || k0 + 32 <= qw + 31;
+        const bool second = !a.causal || kt * kTile + 32 <= qw + 31;
         bf16x8 dsf[4];
 #pragma unroll
-        for (int c = 0; c < 4; ++c) dsf[c] = read_ds(s.ds[0], c);
+        for (int c = 0; c < 4; ++c) dsf[c] = read_ds(c);
         if (!second) {
             dsf[2] = __builtin_bit_cast(bf16x8, make_uint4(0, 0, 0, 0));
             dsf[3] = dsf[2];
         }
         bf16x8 ring[4];
-        ring[0] = read_kt(s.k, 0, 0);
-        ring[1] = read_kt(s.k, 0, 1);
-        ring[2] = read_kt(s.k, 1, 0);
+        ring[0] = read_kt(0, 0);
+        ring[1] = read_kt(0, 1);
+        ring[2] = read_kt(1, 0);
         static_for<8>([&](auto J) {
             constexpr int j = decltype(J)::value;  // chunk j / 2, dim block 2*dsel + j % 2
-            if constexpr (j + 3 < 8) ring[(j + 3) & 3] = read_kt(s.k, (j + 3) >> 1, (j + 3) & 1);
+            if constexpr (j + 3 < 8) ring[(j + 3) & 3] = read_kt((j + 3) >> 1, (j + 3) & 1);
             dq[j & 1] = mfma(ring[j & 3], dsf[j >> 1], dq[j & 1]);
             DT_BUNDLE_END;
         });
     };
 
-    dma(0);
-    dma(1);
-    dma(2);
-    dma(3);
+    dma(0, 0);
+    dma(1, 1);
+    dma(2, 2);
+    dma(3, 3);
     ring_barrier();  // tile 0 has landed
-    for (int kt = 0; kt < n_tiles; ++kt) {
-        dma(kt + 4);  // into the stage of tile kt - 1, which every wave has finished
-        step(kt);
+    // tile kt is in stage s = kt % 5; the request for tile kt + 4 goes to the stage of tile kt - 1, which
+    // every wave has finished. A wave's tiles 0 .. n_use-1 and the rest (requests and barriers only) are
+    // two loops: a product skipped inside one loop made the compiler copy the accumulators every tile.
+    int kt = 0, s = 0;
+    for (; kt < n_use; ++kt) {
+        dma(kt + 4, s == 0 ? kDqStages - 1 : s - 1);
+        step(kt, s);
         ring_barrier();
+        s = s == kDqStages - 1 ? 0 : s + 1;
+    }
+    for (; kt < n_tiles; ++kt) {
+        dma(kt + 4, s == 0 ? kDqStages - 1 : s - 1);
+        ring_barrier();
+        s = s == kDqStages - 1 ? 0 : s + 1;
     }
     asm volatile("s_waitcnt vmcnt(0)" ::: "memory");  // the requests past the range, before the workgroup ends
     if (q < T) {
