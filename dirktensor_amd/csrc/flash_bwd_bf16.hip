@@ -308,9 +308,13 @@ __device__ __forceinline__ void dkdv_block(const FlashBwdArgs& a, int kb_own, in
             if (wave == 0) dma_stats(s.lse2, lse2g, q0, T, lane);
             if (wave == 1) dma_stats(s.delta, deltag, q0, T, lane);
         };
-        auto step = [&](const DkdvStage& s, DkdvStage& nxt, int q0, bool has_next) {
+        // kMask: the tile may hold masked elements; kSkip: the wave may have no query of the tile to take
+        auto step = [&](auto MASK, auto SKIP, const DkdvStage& s, DkdvStage& nxt, int q0, bool has_next)
+                        __attribute__((always_inline)) {
+            constexpr bool kMask = decltype(MASK)::value;
             if (has_next) dma(nxt, q0 + kTile);
-            if (a.causal && q0 + kTile - 1 < kw) return;  // every query of the tile precedes the wave's keys
+            if constexpr (decltype(SKIP)::value)
+                if (a.causal && q0 + kTile - 1 < kw) return;  // every query of the tile precedes the wave's keys
             // (the dQ pass never reads the dS of such a tile and wave: all of it is masked)
             // with dS stored, keys past T are masked too (their dS would otherwise be exp2(-lse2) (-delta))
             const bool need_mask = (a.causal && q0 < kw + 31) || (kEmitDs && kw + 31 >= T);
@@ -355,7 +359,7 @@ __device__ __forceinline__ void dkdv_block(const FlashBwdArgs& a, int kb_own, in
             };
             auto elem = [&](int qb, int i) {  // P = exp2(S c - lse2), dS = P (dP - delta)
                 float pv = __builtin_amdgcn_exp2f(sc[qb][i] * c - Lr[qb][i]);
-                pv = dmask[qb] > 8 * (i >> 2) + (i & 3) ? 0.0f : pv;
+                if constexpr (kMask) pv = dmask[qb] > 8 * (i >> 2) + (i & 3) ? 0.0f : pv;
                 p[qb][i] = pv;
                 ds[qb][i] = pv * (dp[qb][i] - Dr[qb][i]);
             };
@@ -400,16 +404,31 @@ __device__ __forceinline__ void dkdv_block(const FlashBwdArgs& a, int kb_own, in
             });
         };
 
+        using True_ = std::true_type;
+        using False_ = std::false_type;
         dma(st0, q_begin);
         stage_barrier();
-        for (int it = 0; it < n_steps; it += 2) {
-            const int q0 = q_begin + it * kTile;
-            step(st0, st1, q0, it + 1 < n_steps);
-            stage_barrier();
-            if (it + 1 >= n_steps) break;
-            step(st1, st0, q0 + kTile, it + 2 < n_steps);
+        // Tiles 0 and 1 hold the diagonal (causal masks; under causality waves 2-3 have no query of tile 0).
+        // From tile 2 on nothing is masked but, with dS stored, the keys past T, a condition fixed per wave:
+        // the loop is compiled without the selects when it is false (the same values: dmask is INT_MIN).
+        step(True_{}, True_{}, st0, st1, q_begin, 1 < n_steps);
+        stage_barrier();
+        if (n_steps > 1) {
+            step(True_{}, False_{}, st1, st0, q_begin + kTile, 2 < n_steps);
             stage_barrier();
         }
+        auto rest = [&](auto MASK) __attribute__((always_inline)) {
+            for (int it = 2; it < n_steps; it += 2) {
+                const int q0 = q_begin + it * kTile;
+                step(MASK, False_{}, st0, st1, q0, it + 1 < n_steps);
+                stage_barrier();
+                if (it + 1 >= n_steps) break;
+                step(MASK, False_{}, st1, st0, q0 + kTile, it + 2 < n_steps);
+                stage_barrier();
+            }
+        };
+        if (kEmitDs && kw + 31 >= T) rest(True_{});
+        else rest(False_{});
         if (key < T) {
             store_rows(dKg, key, a.ld_grad, hh, dk, a.scale);  // dS carries the reference's scale (:293)
             store_rows(dVg, key, a.ld_grad, hh, dv, 1.0f);
