@@ -486,9 +486,12 @@ __device__ __forceinline__ void dq_block(const FlashBwdArgs& a, int qb_own, int 
             dma_tile(s.k, Kg, k0, T, a.ld_qkv, voff, wave);
             dma_tile(s.v, Vg, k0, T, a.ld_qkv, voff, wave);
         };
-        auto step = [&](const DqStage& s, DqStage& nxt, int k0, bool has_next) {
+        // kGen: the tile may hold masked keys, or none the wave's queries see
+        auto step = [&](auto GEN, const DqStage& s, DqStage& nxt, int k0, bool has_next) __attribute__((always_inline)) {
+            constexpr bool kGen = decltype(GEN)::value;
             if (has_next) dma(nxt, k0 + kTile);
-            if (a.causal && k0 > qw + 31) return;  // every key of the tile follows the wave's queries
+            if constexpr (kGen)
+                if (a.causal && k0 > qw + 31) return;  // every key of the tile follows the wave's queries
             const bool need_mask = (a.causal && k0 + kTile - 1 > qw) || k0 + kTile > T;
             // masking without branches: element i of key block kb (key k0 + 32*kb + 4*hh + off_i, off_i =
             // 8*(i/4) + i%4 a constant) is masked when off_i > emask[kb], i.e. when key > lim
@@ -510,7 +513,7 @@ __device__ __forceinline__ void dq_block(const FlashBwdArgs& a, int qb_own, int 
             };
             auto elem = [&](int kb, int i) {  // dS^T = P^T (dP^T - delta), P^T = exp2(S^T c - lse2)
                 float pv = __builtin_amdgcn_exp2f(sc[kb][i] * c - lse2);
-                pv = 8 * (i >> 2) + (i & 3) > emask[kb] ? 0.0f : pv;
+                if constexpr (kGen) pv = 8 * (i >> 2) + (i & 3) > emask[kb] ? 0.0f : pv;
                 ds[kb][i] = pv * (dp[kb][i] - delta);
             };
             auto pack = [&](int kb, int u) {
@@ -545,14 +548,31 @@ __device__ __forceinline__ void dq_block(const FlashBwdArgs& a, int qb_own, int 
             });
         };
 
+        // Tiles 0 .. n_plain-1 need no mask (every key at or before the wave's first query and before T); the
+        // rest (the diagonal under causality, the tile past T) take the selects and, past the wave's queries,
+        // nothing. Two loops, so the first is compiled without them (the same values: emask is INT_MAX).
+        const int k_plain = a.causal ? min(qw + 1, T) : T;
+        const int n_plain = min(max(k_plain, 0) / kTile, n_steps);
+        using True_ = std::true_type;
+        using False_ = std::false_type;
         dma(st0, 0);
         stage_barrier();
-        for (int it = 0; it < n_steps; it += 2) {
+        int it = 0;
+        for (; it + 1 < n_plain; it += 2) {
             const int k0 = it * kTile;
-            step(st0, st1, k0, it + 1 < n_steps);
+            step(False_{}, st0, st1, k0, it + 1 < n_steps);
             stage_barrier();
-            if (it + 1 >= n_steps) break;
-            step(st1, st0, k0 + kTile, it + 2 < n_steps);
+            step(False_{}, st1, st0, k0 + kTile, it + 2 < n_steps);
+            stage_barrier();
+        }
+        if (it < n_plain) {  // an odd count: the last plain tile is an even one
+            step(False_{}, st0, st1, it * kTile, it + 1 < n_steps);
+            stage_barrier();
+            ++it;
+        }
+        for (; it < n_steps; ++it) {
+            if (it & 1) step(True_{}, st1, st0, it * kTile, it + 1 < n_steps);
+            else step(True_{}, st0, st1, it * kTile, it + 1 < n_steps);
             stage_barrier();
         }
         if (q < T) store_rows(dQg, q, a.ld_grad, hh, dq, a.scale);
