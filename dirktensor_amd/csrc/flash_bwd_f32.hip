@@ -298,11 +298,13 @@ __device__ __forceinline__ void dkdv_block(const FlashBwdArgs& a, int kb_own, in
             dk[db] = zero16();
         }
         stage_barrier();
-        for (int it = 0; it < n_steps; ++it) {
+        // kMask: the tile may hold masked elements; kSkip: the wave may have no query of the tile to take
+        auto tile = [&](auto MASK, auto SKIP, int it) __attribute__((always_inline)) {
+            constexpr bool kMask = decltype(MASK)::value;
             const int q0 = q_begin + it * kTile;
             const DkdvStage& s = stg[it & 1];
             if (it + 1 < n_steps) fetch(stg[(it + 1) & 1], q0 + kTile);
-            if (!(a.causal && q0 + kTile - 1 < kw)) {
+            if (!(decltype(SKIP)::value && a.causal && q0 + kTile - 1 < kw)) {
                 // (the dQ pass never reads the dS of a skipped tile and wave: all of it is masked); with dS
                 // stored, keys past T are masked too (their dS would otherwise be exp2(-lse2) (-delta))
                 const bool need_mask = (a.causal && q0 < kw + 31) || (kEmitDs && kw + 31 >= T);
@@ -327,7 +329,7 @@ __device__ __forceinline__ void dkdv_block(const FlashBwdArgs& a, int kb_own, in
                     for (int i = 0; i < 16; ++i) {
                         const int qi = 32 * qb + 8 * (i / 4) + 4 * hh + (i % 4);
                         float pv = __builtin_amdgcn_exp2f(sc[qb][i] * c - s.lse2[qi]);
-                        pv = dmask[qb] > 8 * (i / 4) + (i % 4) ? 0.0f : pv;
+                        if constexpr (kMask) pv = dmask[qb] > 8 * (i / 4) + (i % 4) ? 0.0f : pv;
                         sc[qb][i] = pv;
                         dp[qb][i] = pv * (dp[qb][i] - s.delta[qi]);
                     }
@@ -344,6 +346,18 @@ __device__ __forceinline__ void dkdv_block(const FlashBwdArgs& a, int kb_own, in
                 acc_cols(dk, s.q, ln, hh, dp);  // dK^T += Q^T dS
             }
             stage_barrier();  // stage it&1 is free for the tile after next; tile it+1 has landed
+        };
+        // Tiles 0 and 1 hold the diagonal (causal masks; under causality waves 2-3 have no query of tile 0);
+        // from tile 2 on nothing is masked, so that loop is compiled without the selects and the skip (the
+        // same values: dmask is INT_MIN there). The kernel that stores dS keeps one loop: peeled, it spilled.
+        using True_ = std::true_type;
+        using False_ = std::false_type;
+        if constexpr (kEmitDs) {
+            for (int it = 0; it < n_steps; ++it) tile(True_{}, True_{}, it);
+        } else {
+            tile(True_{}, True_{}, 0);
+            if (n_steps > 1) tile(True_{}, False_{}, 1);
+            for (int it = 2; it < n_steps; ++it) tile(False_{}, False_{}, it);
         }
         if (key < T) {
             store_rows(dKg, key, a.ld_grad, hh, dk, a.scale);  // dS carries the reference's scale (:293)
@@ -403,11 +417,13 @@ __device__ __forceinline__ void dq_block(const FlashBwdArgs& a, int qb_own, int 
         for (int db = 0; db < 4; ++db) dq[db] = zero16();
 
         stage_barrier();
-        for (int it = 0; it < n_steps; ++it) {
+        // kGen: the tile may hold masked keys, or none the wave's queries see
+        auto tile = [&](auto GEN, int it) __attribute__((always_inline)) {
+            constexpr bool kGen = decltype(GEN)::value;
             const int k0 = it * kTile;
             const DqStage& s = stg[it & 1];
             if (it + 1 < n_steps) fetch(stg[(it + 1) & 1], k0 + kTile);
-            if (!(a.causal && k0 > qw + 31)) {
+            if (!(kGen && a.causal && k0 > qw + 31)) {
                 const bool need_mask = (a.causal && k0 + kTile - 1 > qw) || k0 + kTile > T;
                 // masking without branches: element i of key block kb (key k0 + 32*kb + 4*hh + off_i, off_i =
                 // 8*(i/4) + i%4) is masked when off_i > emask[kb], i.e. when key > lim
@@ -424,13 +440,21 @@ __device__ __forceinline__ void dq_block(const FlashBwdArgs& a, int qb_own, int 
 #pragma unroll
                     for (int i = 0; i < 16; ++i) {
                         float pv = __builtin_amdgcn_exp2f(sc[kb][i] * c - lse2);
-                        pv = 8 * (i / 4) + (i % 4) > emask[kb] ? 0.0f : pv;
+                        if constexpr (kGen) pv = 8 * (i / 4) + (i % 4) > emask[kb] ? 0.0f : pv;
                         ds[kb][i] = pv * (dp[kb][i] - delta);
                     }
                 acc_cols(dq, s.k, ln, hh, ds);  // dQ^T += K^T dS^T
             }
             stage_barrier();  // stage it&1 is free for the tile after next; tile it+1 has landed
-        }
+        };
+        // Tiles 0 .. n_plain-1 need no mask (every key at or before the wave's first query and before T); the
+        // rest (the diagonal under causality, the tile past T) take the selects and, past the wave's queries,
+        // nothing. Two loops, so the first is compiled without them (the same values: emask is INT_MAX).
+        const int k_plain = a.causal ? min(qw + 1, T) : T;
+        const int n_plain = min(max(k_plain, 0) / kTile, n_steps);
+        int it = 0;
+        for (; it < n_plain; ++it) tile(std::false_type{}, it);
+        for (; it < n_steps; ++it) tile(std::true_type{}, it);
         if (q < T) store_rows(dQg, q, a.ld_grad, hh, dq, a.scale);
     }
 }
@@ -492,13 +516,18 @@ __device__ __forceinline__ void dq_ds_block(const FlashBwdArgs& a, int qb_own, i
 #pragma unroll
     for (int db = 0; db < 4; ++db) dq[db] = zero16();
 
+    // the tiles this wave multiplies: 0 .. n_use-1 (no query of the wave, or every key of a later tile
+    // after its queries under causality, leaves the rest to the other waves); the rest only fetch and wait,
+    // in a loop of their own (a product skipped inside the loop made the compiler copy the accumulators)
+    const int n_use = q - ln >= T ? 0 : (a.causal ? min(n_steps, (qw + 31) / kTile + 1) : n_steps);
     fetch(stg[0], 0);
     stage_barrier();
-    for (int it = 0; it < n_steps; ++it) {
+    int it = 0;
+    for (; it < n_use; ++it) {
         const int k0 = it * kTile;
         const DsqStage& s = stg[it & 1];
         if (it + 1 < n_steps) fetch(stg[(it + 1) & 1], k0 + kTile);
-        if (q - ln < T && !(a.causal && k0 > qw + 31)) {
+        {
             // the second 32 keys are all after the wave's queries under causality: their dS was not stored
             const bool second = !a.causal || k0 + 32 <= qw + 31;
             floatx16 w[2];
@@ -513,6 +542,10 @@ __device__ __forceinline__ void dq_ds_block(const FlashBwdArgs& a, int qb_own, i
             acc_cols(dq, s.k, ln, hh, w);  // dQ^T += K^T dS^T
         }
         stage_barrier();  // stage it&1 is free for the tile after next; tile it+1 has landed
+    }
+    for (; it < n_steps; ++it) {
+        if (it + 1 < n_steps) fetch(stg[(it + 1) & 1], (it + 1) * kTile);
+        stage_barrier();
     }
     if (q < T) store_rows(dQg, q, a.ld_grad, hh, dq, a.scale);
 }
