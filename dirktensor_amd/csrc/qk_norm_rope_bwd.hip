@@ -15,11 +15,13 @@
 // x is in the same dtype (the bf16 layer path keeps its pre-norm projections as
 // the bf16 output of the QKV GEMM).
 //
-// dw is reduced deterministically: a workgroup handles kRows rows and writes
-// one partial row of column sums; launch_colsum adds the partials, in a fixed
-// order, into the gradient (the reference's `+=`, RMSNorm.cpp:31).
+// dw is reduced deterministically: a workgroup handles a fixed number of rows
+// (norm_rope_bwd_rows: up to kMaxRows, fewer for short inputs, so that the
+// grid still has two workgroups per CU) and writes one partial row of column
+// sums; launch_colsum adds the partials, in a fixed order, into the gradient
+// (the reference's `+=`, RMSNorm.cpp:31).
 //
-// One workgroup of 256 threads per kRows rows of q (blockIdx.y == 0) or k (== 1);
+// One workgroup of 256 threads per row block of q (blockIdx.y == 0) or k (== 1);
 // thread t owns dims [4*(t%16), +4) and [4*(t%16)+64, +4) of heads t/16,
 // t/16 + 16, ..., so both halves of each rotate-half pair sit in one thread.
 // HBM bound: per row it reads g, x (twice, the second time mostly from L2)
@@ -33,7 +35,7 @@ namespace {
 typedef __bf16 bf16x2 __attribute__((ext_vector_type(2)));
 typedef float floatx2 __attribute__((ext_vector_type(2)));
 
-constexpr int kRows = 16;
+constexpr int kMaxRows = 16;
 
 __device__ __forceinline__ uint32_t pack_bf16x2(float lo, float hi) {
     bf16x2 r = __builtin_convertvector((floatx2){lo, hi}, bf16x2);
@@ -76,15 +78,15 @@ __device__ __forceinline__ void rope_back(const float4& a, const float4& b, cons
 }
 
 template <bool kBF16>
-__global__ __launch_bounds__(256) void qk_norm_rope_bwd_kernel(NormRopeBwdArgs a) {
-    __shared__ float red[kRows][4];
+__global__ __launch_bounds__(256) void qk_norm_rope_bwd_kernel(NormRopeBwdArgs a, int rpb) {
+    __shared__ float red[kMaxRows][4];
     const int which = blockIdx.y;
-    const int r0 = blockIdx.x * kRows;
+    const int r0 = blockIdx.x * rpb;
     const int tid = threadIdx.x;
     const int head = tid >> 4;
     const int d0 = 4 * (tid & 15);
     const int C = a.H * 128;
-    const int nr = min(kRows, a.rows - r0);
+    const int nr = min(rpb, a.rows - r0);
 
     void* g = which == 0 ? a.dq : a.dk;
     const void* x = which == 0 ? a.q_x : a.k_x;
@@ -196,14 +198,25 @@ unsigned grid_for(int64_t n) {
 
 }  // namespace
 
-int norm_rope_bwd_blocks(int rows) { return (rows + kRows - 1) / kRows; }
+// rows per workgroup: kMaxRows, or the power of two that still gives the q and k grids 512 workgroups
+// together (two per CU); a function of the row count only, so the summation order is fixed per shape
+static int norm_rope_bwd_rows(int rows) {
+    int r = 1;
+    while (2 * r <= kMaxRows && 2 * r * 256 <= rows) r *= 2;
+    return r;
+}
+int norm_rope_bwd_blocks(int rows) {
+    const int r = norm_rope_bwd_rows(rows);
+    return (rows + r - 1) / r;
+}
 
 int launch_qk_norm_rope_bwd(const NormRopeBwdArgs& a, int bf16, float* grad_q_w, float* grad_k_w,
                             hipStream_t stream, bool accumulate) {
     const int nblk = norm_rope_bwd_blocks(a.rows);
+    const int rpb = norm_rope_bwd_rows(a.rows);
     dim3 grid(nblk, 2);
-    if (bf16) hipLaunchKernelGGL(qk_norm_rope_bwd_kernel<true>, grid, dim3(256), 0, stream, a);
-    else hipLaunchKernelGGL(qk_norm_rope_bwd_kernel<false>, grid, dim3(256), 0, stream, a);
+    if (bf16) hipLaunchKernelGGL(qk_norm_rope_bwd_kernel<true>, grid, dim3(256), 0, stream, a, rpb);
+    else hipLaunchKernelGGL(qk_norm_rope_bwd_kernel<false>, grid, dim3(256), 0, stream, a, rpb);
     DT_HIP_TRY(hipGetLastError());
     const int C = a.H * 128;  // partial: [q, k][nblk][C]
     DT_TRY(launch_colsum(a.partial, nblk, C, grad_q_w, stream, accumulate));
