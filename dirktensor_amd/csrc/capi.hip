@@ -918,7 +918,16 @@ int dt_attn_layer_destroy(dt_attn_layer* L) {
 
 int dt_attn_layer_fwd(dt_attn_layer* L, const float* x, float* out, int B, int T, const int32_t* seq_lens,
                       int dtype, int mem, int save_for_backward, void* stream) {
+    return attn_layer_fwd(L, x, out, B, T, seq_lens, dtype, mem, save_for_backward, stream, false);
+}
+
+}  // extern "C"
+
+int attn_layer_fwd(dt_attn_layer* L, const float* x, float* out, int B, int T, const int32_t* seq_lens, int dtype,
+                   int mem, int save_for_backward, void* stream, bool x16_ready) {
     clear_error();
+    if (x16_ready && (dtype != DT_BF16 || mem != DT_MEM_DEVICE))
+        return set_error(DT_ERR_INVALID_ARG, "a bf16 copy of x is taken in bf16 mode with device memory only");
     if (!x || !out) return set_error(DT_ERR_INVALID_ARG, "x and out must be non-NULL");
     if (B < 1 || T < 1) return set_error(DT_ERR_INVALID_ARG, "B=%d, T=%d must be >= 1", B, T);
     if (T > DT_MAX_SEQ_LEN) return set_error(DT_ERR_INVALID_ARG, "T=%d exceeds max_seq_len %d", T, DT_MAX_SEQ_LEN);
@@ -943,18 +952,21 @@ int dt_attn_layer_fwd(dt_attn_layer* L, const float* x, float* out, int B, int T
     const float* xd = x;
     float* od = out;
     L->saved_T = 0;  // a failed or inference forward leaves nothing to differentiate
-    if (save_for_backward) {
-        // the reference keeps its own copy of the input (m_act_input_2d, OlmoAttention.cpp:64)
+    if (save_for_backward && dtype != DT_BF16) {
+        // the reference keeps its own copy of the input (m_act_input_2d, OlmoAttention.cpp:64); in bf16 mode that
+        // copy is the bf16 x the projections read (x16 below), the only form of x the backward reads there
         DT_TRY(L->x32.ensure(act * 4));
         DT_HIP_TRY(hipMemcpyAsync(L->x32.ptr, x, act * 4, mem == DT_MEM_HOST ? hipMemcpyHostToDevice
                                                                               : hipMemcpyDeviceToDevice, s));
         xd = static_cast<const float*>(L->x32.ptr);
-        DT_TRY(L->rms.ensure((size_t)2 * rows * 4));
-        DT_TRY(L->stats.ensure((size_t)2 * rows * H * 4));
     } else if (mem == DT_MEM_HOST) {
         DT_TRY(ctx->stage[0].ensure(act * 4));
         DT_HIP_TRY(hipMemcpyAsync(ctx->stage[0].ptr, x, act * 4, hipMemcpyHostToDevice, s));
         xd = static_cast<const float*>(ctx->stage[0].ptr);
+    }
+    if (save_for_backward) {
+        DT_TRY(L->rms.ensure((size_t)2 * rows * 4));
+        DT_TRY(L->stats.ensure((size_t)2 * rows * H * 4));
     }
     if (mem == DT_MEM_HOST) {
         DT_TRY(ctx->stage[1].ensure(act * 4));
@@ -1018,7 +1030,7 @@ int dt_attn_layer_fwd(dt_attn_layer* L, const float* x, float* out, int B, int T
         uint16_t* pre16 = static_cast<uint16_t*>(L->qkv_pre.ptr);
         uint16_t* qkv16 = static_cast<uint16_t*>(L->qkv16.ptr);
         uint16_t* attn16 = static_cast<uint16_t*>(L->attn.ptr);
-        DT_TRY(launch_f32_to_bf16(xd, x16, (int64_t)act, s));
+        if (!x16_ready) DT_TRY(launch_f32_to_bf16(xd, x16, (int64_t)act, s));
         if (fused) {
             // x [Wq;Wk;Wv]^T, q/k norm and RoPE in one kernel (OlmoAttention.cpp:63-88); the pre-norm q|k rows
             // (bf16) only when the norms' backward will read them
@@ -1051,8 +1063,6 @@ int dt_attn_layer_fwd(dt_attn_layer* L, const float* x, float* out, int B, int T
     }
     return DT_OK;
 }
-
-}  // extern "C"
 
 int attn_layer_settle_grads(dt_attn_layer* L, hipStream_t s) {
     if (!L->grad_zero_pending || !L->g_qkv) return DT_OK;
@@ -1097,7 +1107,6 @@ int attn_layer_ensure_grads(dt_attn_layer* L, hipStream_t s) {
     return rc;
 }
 
-extern "C" {
 
 // `writing` is set once the first gradient buffer is about to be written
 static int attn_layer_bwd(dt_attn_layer* L, const float* d_out, float* d_x, int B, int T, int mem, void* stream,
@@ -1187,6 +1196,8 @@ static int attn_layer_bwd(dt_attn_layer* L, const float* d_out, float* d_x, int 
     }
     return DT_OK;
 }
+
+extern "C" {
 
 int dt_attn_layer_bwd(dt_attn_layer* L, const float* d_out, float* d_x, int B, int T, int mem, void* stream) {
     bool writing = false;

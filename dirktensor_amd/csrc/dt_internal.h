@@ -265,6 +265,11 @@ struct dt_attn_layer {
     float* g_kn = nullptr;
 };
 
+// dt_attn_layer_fwd with one more input: x16_ready (bf16 mode, device memory) says that L->x16 already holds
+// the B*T*d_model rows of x rounded to bf16 (the model's previous block writes them there with its last norm),
+// so the layer does not round x itself
+int attn_layer_fwd(dt_attn_layer* L, const float* x, float* out, int B, int T, const int32_t* seq_lens, int dtype,
+                   int mem, int save_for_backward, void* stream, bool x16_ready);
 // zero-initialised attention layer (weights set afterwards), and its gradient buffers (allocated zeroed)
 int attn_layer_alloc(dt_ctx* ctx, int d_model, int n_heads, dt_attn_layer** out);
 int attn_layer_ensure_grads(dt_attn_layer* L, hipStream_t s);  // all four buffers, or none on failure

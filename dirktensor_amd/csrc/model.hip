@@ -475,8 +475,10 @@ int dt_model_fwd(dt_model* M, const int32_t* tokens, int B, int T, float* logits
         float* y_pf = save_for_backward ? static_cast<float*>(S.y_pf.ptr) : nullptr;
         float* rms_pa = save_for_backward ? static_cast<float*>(S.rms_pa.ptr) : nullptr;
         float* rms_pf = save_for_backward ? static_cast<float*>(S.rms_pf.ptr) : nullptr;
-        // attention and h = x + N(attn(x))
-        DT_TRY(dt_attn_layer_fwd(Ly.attn, x, a, B, T, nullptr, dtype, DT_MEM_DEVICE, save_for_backward, stream));
+        // attention and h = x + N(attn(x)); in bf16 mode from the second block on, the previous block's last norm
+        // has already written x rounded to bf16 into this layer's x16
+        DT_TRY(attn_layer_fwd(Ly.attn, x, a, B, T, nullptr, dtype, DT_MEM_DEVICE, save_for_backward, stream,
+                              bf && li > 0));
         DT_TRY(launch_rmsnorm_rows(a, Ly.w_pa, x, h, h16, y_pa, rms_pa, (int)rows, dm, kEps, s));
         // MLP (OlmoMlp.cpp:26-63): [gate | up] = h [Wgate; Wup]^T, act = silu(gate) * up, m = act Wdown^T
         // (in bf16 mode the N = 16384 gate|up product is written as bf16: it is only read by SwiGLU)
@@ -487,8 +489,14 @@ int dt_model_fwd(dt_model* M, const int32_t* tokens, int B, int T, float* logits
         DT_TRY(gemm_rm(ctx, s, false, true, (int)rows, dm, hid, S.act.ptr, hid,
                        bf ? static_cast<const void*>(Ly.w_down16) : static_cast<const void*>(Ly.w_down), hid, 0.0f, mo,
                        dm, bf));
-        // x_next = h + N(m)
-        DT_TRY(launch_rmsnorm_rows(mo, Ly.w_pf, h, xn, nullptr, y_pf, rms_pf, (int)rows, dm, kEps, s));
+        // x_next = h + N(m), in bf16 mode also as bf16 into the next layer's x16 (the input its projections read)
+        uint16_t* xn16 = nullptr;
+        if (bf && li + 1 < M->n_layers) {
+            dt_attn_layer* next = M->L[li + 1].attn;
+            DT_TRY(next->x16.ensure(act * 2));
+            xn16 = static_cast<uint16_t*>(next->x16.ptr);
+        }
+        DT_TRY(launch_rmsnorm_rows(mo, Ly.w_pf, h, xn, xn16, y_pf, rms_pf, (int)rows, dm, kEps, s));
         std::swap(x, xn);
     }
     // final norm and LM head (OlmoModel.cpp:44-47, OlmoLmHead.cpp:11-28)
