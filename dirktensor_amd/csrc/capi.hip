@@ -1109,8 +1109,8 @@ int attn_layer_ensure_grads(dt_attn_layer* L, hipStream_t s) {
 
 
 // `writing` is set once the first gradient buffer is about to be written
-static int attn_layer_bwd(dt_attn_layer* L, const float* d_out, float* d_x, int B, int T, int mem, void* stream,
-                          bool& writing) {
+static int attn_layer_bwd(dt_attn_layer* L, const float* d_out, const uint16_t* d_out16, float* d_x, int B, int T,
+                          int mem, void* stream, bool& writing) {
     clear_error();
     if (!d_out || !d_x) return set_error(DT_ERR_INVALID_ARG, "d_out and d_x must be non-NULL");
     if (mem != DT_MEM_DEVICE && mem != DT_MEM_HOST) return set_error(DT_ERR_INVALID_ARG, "unknown mem %d", mem);
@@ -1161,8 +1161,12 @@ static int attn_layer_bwd(dt_attn_layer* L, const float* d_out, float* d_x, int 
     const void *g_in = gd, *wo = L->w_o, *attn = L->attn.ptr;
     if (bf) {
         DT_TRY(L->d16.ensure(act * 2));
-        DT_TRY(launch_f32_to_bf16(gd, static_cast<uint16_t*>(L->d16.ptr), (int64_t)act, s));
-        g_in = L->d16.ptr;
+        if (d_out16 && mem == DT_MEM_DEVICE) {
+            g_in = d_out16;
+        } else {
+            DT_TRY(launch_f32_to_bf16(gd, static_cast<uint16_t*>(L->d16.ptr), (int64_t)act, s));
+            g_in = L->d16.ptr;
+        }
         wo = L->w_o16;
     }
     writing = true;
@@ -1197,11 +1201,19 @@ static int attn_layer_bwd(dt_attn_layer* L, const float* d_out, float* d_x, int 
     return DT_OK;
 }
 
+int attn_layer_bwd_dev(dt_attn_layer* L, const float* d_out, const uint16_t* d_out16, float* d_x, int B, int T,
+                       void* stream) {
+    bool writing = false;
+    const int rc = attn_layer_bwd(L, d_out, d_out16, d_x, B, T, DT_MEM_DEVICE, stream, writing);
+    if (rc != DT_OK && writing && L->grad_zero_pending) (void)attn_layer_settle_grads(L, static_cast<hipStream_t>(stream));
+    return rc;
+}
+
 extern "C" {
 
 int dt_attn_layer_bwd(dt_attn_layer* L, const float* d_out, float* d_x, int B, int T, int mem, void* stream) {
     bool writing = false;
-    const int rc = attn_layer_bwd(L, d_out, d_x, B, T, mem, stream, writing);
+    const int rc = attn_layer_bwd(L, d_out, nullptr, d_x, B, T, mem, stream, writing);
     // a backward that failed after zero_grad, once it had begun writing gradients, may have written some of them:
     // clear them all, so that they read as the zero_grad left them (the error stays the one reported)
     if (rc != DT_OK && writing && L->grad_zero_pending) (void)attn_layer_settle_grads(L, static_cast<hipStream_t>(stream));

@@ -270,6 +270,10 @@ struct dt_attn_layer {
 // so the layer does not round x itself
 int attn_layer_fwd(dt_attn_layer* L, const float* x, float* out, int B, int T, const int32_t* seq_lens, int dtype,
                    int mem, int save_for_backward, void* stream, bool x16_ready);
+// dt_attn_layer_bwd (device memory) with one more input: d_out16 (bf16 mode, nullable) holds d_out rounded to bf16
+// (the model's norm backward writes it beside d_out), so the layer does not round d_out itself
+int attn_layer_bwd_dev(dt_attn_layer* L, const float* d_out, const uint16_t* d_out16, float* d_x, int B, int T,
+                       void* stream);
 // zero-initialised attention layer (weights set afterwards), and its gradient buffers (allocated zeroed)
 int attn_layer_alloc(dt_ctx* ctx, int d_model, int n_heads, dt_attn_layer** out);
 int attn_layer_ensure_grads(dt_attn_layer* L, hipStream_t s);  // all four buffers, or none on failure
@@ -288,9 +292,10 @@ int launch_swiglu(const void* gu, void* act, int rows, int hid, int bf16, hipStr
 int launch_ce_loss(const float* logits, const int32_t* target, float* term, float* grad, float* loss, int rows, int V,
                    int count, hipStream_t s);
 int rmsnorm_bwd_blocks(int rows);
+// dx16 (nullable): dx rounded to bf16 as well; dx may then be NULL (only the bf16 rows are written)
 int launch_rmsnorm_bwd(const float* dy, const float* y, const float* rms, const float* w, const float* dx_add,
                        float* dx, float* partial, float* grad_w, int rows, int dm, hipStream_t s,
-                       bool accumulate = true);
+                       bool accumulate = true, uint16_t* dx16 = nullptr);
 int launch_swiglu_bwd(const float* d_act, const void* gu, void* d_gu, int rows, int hid, int bf16, hipStream_t s);
 int launch_embed_bwd(const float* dx, const int32_t* uniq, const int32_t* start, const int32_t* pos, int n_uniq,
                      float* g_embed, int dm, hipStream_t s);

@@ -590,14 +590,14 @@ static int model_bwd(dt_model* M, const float* d_logits, int mem, void* stream, 
     // blocks in reverse (OlmoBlock.cpp:23-30)
     for (int li = M->n_layers - 1; li >= 0; --li) {
         ModelLayer& Ly = M->L[li];
-        // d_m = N_pf.backward(d_x)
+        // d_m = N_pf.backward(d_x) (in bf16 mode only as bf16: the two GEMMs below are its only readers)
         DT_TRY(launch_rmsnorm_bwd(dx, static_cast<const float*>(Ly.y_pf.ptr), static_cast<const float*>(Ly.rms_pf.ptr),
-                                  Ly.w_pf, nullptr, dmo, partial, Ly.g_pf, rows, dm, s, !fresh));
+                                  Ly.w_pf, nullptr, bf ? nullptr : dmo, partial, Ly.g_pf, rows, dm, s, !fresh,
+                                  bf ? d16 : nullptr));
         // MLP backward: dWdown += d_m^T act; d_act = d_m Wdown; d_gu = swiglu'; dW_gu += d_gu^T h;
         // d_h = d_gu W_gu + d_x (the residual, OlmoBlock.cpp:28; GEMM with beta = 1 into a copy of d_x)
         DT_HIP_TRY(hipMemcpyAsync(dh, dx, act * 4, hipMemcpyDeviceToDevice, s));
         if (bf) {
-            DT_TRY(launch_f32_to_bf16(dmo, d16, (int64_t)act, s));
             DT_TRY(gemm_rm(ctx, s, true, false, dm, hid, rows, d16, dm, Ly.act.ptr, hid, gb, Ly.g_down, hid, true));
             DT_TRY(gemm_rm(ctx, s, false, false, rows, hid, dm, d16, dm, Ly.w_down16, hid, 0.0f, d_act, hid, true));
         } else {
@@ -609,10 +609,11 @@ static int model_bwd(dt_model* M, const float* d_logits, int mem, void* stream, 
         const void* wgu = bf ? static_cast<const void*>(Ly.w_gu16) : static_cast<const void*>(Ly.w_gu);
         DT_TRY(gemm_rm(ctx, s, true, false, 2 * hid, dm, rows, M->d_gu.ptr, 2 * hid, hin, dm, gb, Ly.g_gu, dm, bf));
         DT_TRY(gemm_rm(ctx, s, false, false, rows, dm, 2 * hid, M->d_gu.ptr, 2 * hid, wgu, dm, 1.0f, dh, dm, bf));
-        // d_a = N_pa.backward(d_h); d_x = attn.backward(d_a) + d_h (OlmoBlock.cpp:29-32)
+        // d_a = N_pa.backward(d_h); d_x = attn.backward(d_a) + d_h (OlmoBlock.cpp:29-32); in bf16 mode d_a also as
+        // bf16, the form the layer's output-projection GEMMs read (d16 is free again: the GEMMs above have read it)
         DT_TRY(launch_rmsnorm_bwd(dh, static_cast<const float*>(Ly.y_pa.ptr), static_cast<const float*>(Ly.rms_pa.ptr),
-                                  Ly.w_pa, nullptr, da, partial, Ly.g_pa, rows, dm, s, !fresh));
-        DT_TRY(dt_attn_layer_bwd(Ly.attn, da, dxa, B, T, DT_MEM_DEVICE, stream));
+                                  Ly.w_pa, nullptr, da, partial, Ly.g_pa, rows, dm, s, !fresh, bf ? d16 : nullptr));
+        DT_TRY(attn_layer_bwd_dev(Ly.attn, da, bf ? d16 : nullptr, dxa, B, T, stream));
         DT_TRY(launch_add(dxa, dh, dx, (int64_t)act, s));
     }
     M->grad_zero_pending = false;  // every model-level gradient buffer but the embedding's has been written

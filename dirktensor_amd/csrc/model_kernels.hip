@@ -241,7 +241,7 @@ __global__ __launch_bounds__(256) void ce_reduce_kernel(const float* term, int64
 constexpr int kRowsPerBlock = 4;  // 512 workgroups for 2048 rows
 __global__ __launch_bounds__(256) void rmsnorm_bwd_rows_kernel(const float* dy, const float* y, const float* rms,
                                                                const float* w, const float* dx_add, float* dx,
-                                                               float* partial, int64_t rows, int dm) {
+                                                               uint16_t* dx16, float* partial, int64_t rows, int dm) {
     __shared__ float red[4];
     __shared__ float cs[kRowsPerBlock];
     const int64_t r0 = (int64_t)blockIdx.x * kRowsPerBlock;
@@ -273,7 +273,13 @@ __global__ __launch_bounds__(256) void rmsnorm_bwd_rows_kernel(const float* dy, 
                 const float4 e = *reinterpret_cast<const float4*>(dx_add + row * dm + i);
                 o = make_float4(o.x + e.x, o.y + e.y, o.z + e.z, o.w + e.w);
             }
-            *reinterpret_cast<float4*>(dx + row * dm + i) = o;
+            if (dx) *reinterpret_cast<float4*>(dx + row * dm + i) = o;
+            if (dx16) {  // the same values rounded to bf16, as f32_to_bf16 rounds them
+                uint2 b;
+                b.x = pack_bf16x2(o.x, o.y);
+                b.y = pack_bf16x2(o.z, o.w);
+                *reinterpret_cast<uint2*>(dx16 + row * dm + i) = b;
+            }
             p = make_float4(p.x + g.x * n.x, p.y + g.y * n.y, p.z + g.z * n.z, p.w + g.w * n.w);
         }
         *reinterpret_cast<float4*>(partial + (int64_t)blockIdx.x * dm + i) = p;
@@ -437,9 +443,10 @@ int launch_ce_loss(const float* logits, const int32_t* target, float* term, floa
 int rmsnorm_bwd_blocks(int rows) { return (rows + kRowsPerBlock - 1) / kRowsPerBlock; }
 
 int launch_rmsnorm_bwd(const float* dy, const float* y, const float* rms, const float* w, const float* dx_add,
-                       float* dx, float* partial, float* grad_w, int rows, int dm, hipStream_t s, bool accumulate) {
+                       float* dx, float* partial, float* grad_w, int rows, int dm, hipStream_t s, bool accumulate,
+                       uint16_t* dx16) {
     const int nblk = rmsnorm_bwd_blocks(rows);
-    hipLaunchKernelGGL(rmsnorm_bwd_rows_kernel, dim3(nblk), dim3(256), 0, s, dy, y, rms, w, dx_add, dx, partial,
+    hipLaunchKernelGGL(rmsnorm_bwd_rows_kernel, dim3(nblk), dim3(256), 0, s, dy, y, rms, w, dx_add, dx, dx16, partial,
                        (int64_t)rows, dm);
     DT_HIP_TRY(hipGetLastError());
     return launch_colsum(partial, nblk, dm, grad_w, s, accumulate);
