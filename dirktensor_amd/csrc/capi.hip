@@ -1171,13 +1171,16 @@ static int attn_layer_bwd(dt_attn_layer* L, const float* d_out, const uint16_t* 
     }
     writing = true;
     DT_TRY(gemm_rm(ctx, s, true, false, dm, dm, rows, g_in, dm, attn, dm, gb, L->g_o, dm, bf));
-    DT_TRY(gemm_rm(ctx, s, false, false, rows, dm, dm, g_in, dm, wo, dm, 0.0f, d_attn, dm, bf));
-    // step 2 (:219-232): the attention core's backward from the saved m and l
     const void* d_o = d_attn;
-    if (bf) {  // the d16 copy of d_out has been consumed by the two GEMMs above (stream order)
-        DT_TRY(launch_f32_to_bf16(d_attn, static_cast<uint16_t*>(L->d16.ptr), (int64_t)act, s));
-        d_o = L->d16.ptr;
+    if (bf) {  // d_attn leaves the GEMM as bf16 (fp32 accumulation, one rounding): the attention backward is its
+               // only reader (in the first half of d_attn32's bytes)
+        uint16_t* d_attn16 = reinterpret_cast<uint16_t*>(d_attn);
+        DT_TRY(gemm_rm_bf16(ctx, s, false, false, rows, dm, dm, g_in, dm, wo, dm, d_attn16, dm));
+        d_o = d_attn16;
+    } else {
+        DT_TRY(gemm_rm(ctx, s, false, false, rows, dm, dm, g_in, dm, wo, dm, 0.0f, d_attn, dm, false));
     }
+    // step 2 (:219-232): the attention core's backward from the saved m and l
     const char* att = static_cast<const char*>(bf ? L->qkv16.ptr : L->att32.ptr);
     char* dq = static_cast<char*>(dqkv);
     FlashBwdArgs ba{att, att + dm * esz, att + 2 * dm * esz, attn, d_o, st_m, st_l, dq, dq + dm * esz,
