@@ -251,6 +251,9 @@ def main() -> int:
     ap.add_argument("--bwd-dq", choices=["auto", "from_ds", "recompute"], default="auto",
                     help="attention backward: dQ from the dS the dK/dV pass stores, recomputed S and dP, or "
                     "auto (the dS path with more than one 128-row block per CU and pass)")
+    ap.add_argument("--side-stream", type=int, choices=[0, 1], default=1,
+                    help="model backward: weight-gradient GEMMs and norm-weight column sums on a second stream beside "
+                    "the input-gradient chain (1) or everything on one stream (0)")
     ap.add_argument("--copy-mib", type=int, default=0,
                     help="instead of attention, time a plain copy kernel over this many MiB (counter calibration)")
     args = ap.parse_args()
@@ -274,6 +277,7 @@ def main() -> int:
     ctx.set_qkv_path(args.qkv)
     ctx.set_gemm_tune(bool(args.gemm_tune))
     ctx.set_bwd_dq_path(args.bwd_dq)
+    ctx.set_side_stream(bool(args.side_stream))
     wl = WORKLOADS[args.workload](args, dev, stream, ctx)
 
     settle = settle_clock(wl["step"], stream)

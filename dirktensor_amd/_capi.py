@@ -32,6 +32,7 @@ DT_QKV_AUTO = 2
 DT_OPT_GEMM_TUNE = 2
 DT_OPT_BWD_DQ = 3
 DT_OPT_QKV_SPIN_LIMIT = 4
+DT_OPT_SIDE_STREAM = 5
 DT_BWD_DQ_RECOMPUTE = 0
 DT_BWD_DQ_FROM_DS = 1
 DT_BWD_DQ_AUTO = 2

@@ -86,6 +86,12 @@ class Context:
         that check() reports)."""
         C.call("dt_ctx_set_option", self.handle, C.DT_OPT_QKV_SPIN_LIMIT, int(polls))
 
+    def set_side_stream(self, on: bool) -> None:
+        """Model backwards on this context run their weight-gradient GEMMs and norm-weight column sums on a
+        second stream beside the input-gradient chain (True, the default; the same results) or everything on the
+        caller's stream (False)."""
+        C.call("dt_ctx_set_option", self.handle, C.DT_OPT_SIDE_STREAM, int(bool(on)))
+
     def check(self) -> None:
         """Waits for the device, then raises DTError (DT_ERR_HIP) when a fused QKV wait gave up since the last
         check."""

@@ -169,13 +169,66 @@ int qkv_status_check(dt_ctx* ctx) {
 // ---------------- rocBLAS helpers ----------------
 static const char* blas_status_str(rocblas_status st) { return rocblas_status_to_string(st); }
 
-static int ensure_blas(dt_ctx* ctx) {
-    if (ctx->blas) return DT_OK;
-    rocblas_handle h = nullptr;
-    rocblas_status st = rocblas_create_handle(&h);
-    if (st != rocblas_status_success) return set_error(DT_ERR_BLAS, "rocblas_create_handle: %s", blas_status_str(st));
-    ctx->blas = h;
+// the rocBLAS handle of stream s: the side stream has its own, so that no handle-owned workspace is shared by
+// GEMMs that run at the same time
+static int ensure_blas(dt_ctx* ctx, hipStream_t s, rocblas_handle* out) {
+    void*& slot = (ctx->side && s == static_cast<hipStream_t>(ctx->side)) ? ctx->blas_side : ctx->blas;
+    if (!slot) {
+        rocblas_handle h = nullptr;
+        rocblas_status st = rocblas_create_handle(&h);
+        if (st != rocblas_status_success)
+            return set_error(DT_ERR_BLAS, "rocblas_create_handle: %s", blas_status_str(st));
+        slot = h;
+    }
+    *out = static_cast<rocblas_handle>(slot);
+    return rocblas_set_stream(*out, s) == rocblas_status_success ? DT_OK
+                                                                  : set_error(DT_ERR_BLAS, "rocblas_set_stream failed");
+}
+
+// ---------------- the side stream ----------------
+hipStream_t side_stream(dt_ctx* ctx, hipStream_t s) {
+    if (ctx->side_off) return nullptr;
+    hipStreamCaptureStatus cs = hipStreamCaptureStatusNone;
+    if (hipStreamIsCapturing(s, &cs) != hipSuccess) {
+        (void)hipGetLastError();
+        return nullptr;
+    }
+    if (cs != hipStreamCaptureStatusNone) return nullptr;
+    if (!ctx->side) {
+        hipStream_t st = nullptr;
+        if (hipStreamCreateWithFlags(&st, hipStreamNonBlocking) != hipSuccess) {
+            (void)hipGetLastError();
+            return nullptr;
+        }
+        for (int i = 0; i < kSideEvents; ++i) {
+            hipEvent_t e = nullptr;
+            if (hipEventCreateWithFlags(&e, hipEventDisableTiming) != hipSuccess) {
+                (void)hipGetLastError();
+                for (int j = 0; j < i; ++j) (void)hipEventDestroy(static_cast<hipEvent_t>(ctx->ev[j]));
+                for (int j = 0; j < i; ++j) ctx->ev[j] = nullptr;
+                (void)hipStreamDestroy(st);
+                return nullptr;
+            }
+            ctx->ev[i] = e;
+        }
+        ctx->side = st;
+    }
+    return static_cast<hipStream_t>(ctx->side);
+}
+
+int stream_mark(dt_ctx* ctx, hipStream_t producer, int ev) {
+    DT_HIP_TRY(hipEventRecord(static_cast<hipEvent_t>(ctx->ev[ev]), producer));
     return DT_OK;
+}
+
+int stream_wait_slot(dt_ctx* ctx, hipStream_t waiter, int ev) {
+    DT_HIP_TRY(hipStreamWaitEvent(waiter, static_cast<hipEvent_t>(ctx->ev[ev]), 0));
+    return DT_OK;
+}
+
+int stream_after(dt_ctx* ctx, hipStream_t waiter, hipStream_t producer, int ev) {
+    DT_TRY(stream_mark(ctx, producer, ev));
+    return stream_wait_slot(ctx, waiter, ev);
 }
 
 // bf16-input GEMMs go through hipBLASLt with its first heuristic choice (rocBLAS remains for fp32 inputs and
@@ -206,6 +259,11 @@ __global__ void words_fingerprint_kernel(const uint32_t* p, int64_t n, unsigned 
     atomicAdd(out, acc);
 }
 
+// the split-K workspace of GEMMs on stream s (the side stream has its own: GEMMs on the two streams overlap)
+DeviceBuffer& lt_workspace(dt_ctx* ctx, hipStream_t s) {
+    return (ctx->side && s == static_cast<hipStream_t>(ctx->side)) ? ctx->lt_ws_side : ctx->lt_ws;
+}
+
 void lt_free(LtPlan& p) {
     if (p.la) hipblasLtMatrixLayoutDestroy(p.la);
     if (p.lb) hipblasLtMatrixLayoutDestroy(p.lb);
@@ -226,7 +284,8 @@ static int lt_tune(dt_ctx* ctx, hipStream_t s, hipblasLtHandle_t h, LtPlan& p,
                    const hipblasLtMatmulHeuristicResult_t* heur, int n, int M, int ldc, bool c_bf16, const void* A,
                    const void* B, int* rank) {
     *rank = 0;
-    DT_TRY(ctx->lt_ws.ensure(kLtWorkspace));
+    DeviceBuffer& ws = lt_workspace(ctx, s);
+    DT_TRY(ws.ensure(kLtWorkspace));
     // whole 32-bit words covering the ldc * M output elements, the tail padded with zeros
     const size_t out_bytes = (size_t)ldc * M * (c_bf16 ? 2 : 4);
     const size_t words = (out_bytes + 3) / 4;
@@ -246,7 +305,7 @@ static int lt_tune(dt_ctx* ctx, hipStream_t s, hipblasLtHandle_t h, LtPlan& p,
     const float one = 1.0f, zero = 0.0f;
     auto run = [&](const hipblasLtMatmulAlgo_t& algo) {
         return hipblasLtMatmul(h, p.desc, &one, B, p.la, A, p.lb, &zero, scratch, p.lc, scratch, p.lc, &algo,
-                               ctx->lt_ws.ptr, kLtWorkspace, s) == HIPBLAS_STATUS_SUCCESS;
+                               ws.ptr, kLtWorkspace, s) == HIPBLAS_STATUS_SUCCESS;
     };
     const int64_t nw = (int64_t)words;
     const unsigned blocks = (unsigned)std::min<int64_t>((nw + 255) / 256, 4096);
@@ -361,10 +420,11 @@ static int gemm_lt(dt_ctx* ctx, hipStream_t s, bool ta, bool tb, int M, int N, i
         }
         it = lc->plans.emplace(key, p).first;
     }
-    DT_TRY(ctx->lt_ws.ensure(kLtWorkspace));
+    DeviceBuffer& ws = lt_workspace(ctx, s);
+    DT_TRY(ws.ensure(kLtWorkspace));
     const float one = 1.0f;
     const LtPlan& p = it->second;
-    if (hipblasLtMatmul(lc->h, p.desc, &one, B, p.la, A, p.lb, &beta, C, p.lc, C, p.lc, &p.algo, ctx->lt_ws.ptr,
+    if (hipblasLtMatmul(lc->h, p.desc, &one, B, p.la, A, p.lb, &beta, C, p.lc, C, p.lc, &p.algo, ws.ptr,
                         kLtWorkspace, s) != HIPBLAS_STATUS_SUCCESS)
         return set_error(DT_ERR_BLAS, "hipBLASLt GEMM (%d x %d x %d%s) failed", M, N, K, c_bf16 ? ", bf16 out" : "");
     return DT_OK;
@@ -375,9 +435,6 @@ static int gemm_lt(dt_ctx* ctx, hipStream_t s, bool ta, bool tb, int M, int N, i
 // C^T = op(B)^T op(A)^T: B goes first, each transposed exactly when it is transposed here.
 int gemm_rm(dt_ctx* ctx, hipStream_t s, bool ta, bool tb, int M, int N, int K, const void* A, int lda,
                    const void* B, int ldb, float beta, float* C, int ldc, bool bf16_in) {
-    DT_TRY(ensure_blas(ctx));
-    rocblas_handle h = static_cast<rocblas_handle>(ctx->blas);
-    rocblas_set_stream(h, s);
     const float one = 1.0f;
     const rocblas_operation opb = tb ? rocblas_operation_transpose : rocblas_operation_none;
     const rocblas_operation opa = ta ? rocblas_operation_transpose : rocblas_operation_none;
@@ -385,6 +442,8 @@ int gemm_rm(dt_ctx* ctx, hipStream_t s, bool ta, bool tb, int M, int N, int K, c
         const int rc = gemm_lt(ctx, s, ta, tb, M, N, K, A, lda, B, ldb, beta, C, ldc);
         if (rc <= 0) return rc;  // done, or an error; 1: no hipBLASLt algorithm, rocBLAS below
     }
+    rocblas_handle h = nullptr;
+    DT_TRY(ensure_blas(ctx, s, &h));
     rocblas_status st;
     if (!bf16_in) {
         st = rocblas_sgemm(h, opb, opa, N, M, K, &one, static_cast<const float*>(B), ldb, static_cast<const float*>(A),
@@ -403,9 +462,8 @@ int gemm_rm_bf16(dt_ctx* ctx, hipStream_t s, bool ta, bool tb, int M, int N, int
                  const void* B, int ldb, void* C, int ldc) {
     const int rc = gemm_lt(ctx, s, ta, tb, M, N, K, A, lda, B, ldb, 0.0f, C, ldc, true);
     if (rc <= 0) return rc;  // done, or an error; 1: no hipBLASLt algorithm, rocBLAS below
-    DT_TRY(ensure_blas(ctx));
-    rocblas_handle h = static_cast<rocblas_handle>(ctx->blas);
-    rocblas_set_stream(h, s);
+    rocblas_handle h = nullptr;
+    DT_TRY(ensure_blas(ctx, s, &h));
     const float one = 1.0f, zero = 0.0f;
     const rocblas_operation opb = tb ? rocblas_operation_transpose : rocblas_operation_none;
     const rocblas_operation opa = ta ? rocblas_operation_transpose : rocblas_operation_none;
@@ -555,6 +613,11 @@ int dt_ctx_set_option(dt_ctx* ctx, int option, int value) {
         ctx->qkv_spin = value;
         return DT_OK;
     }
+    if (option == DT_OPT_SIDE_STREAM) {
+        if (value != 0 && value != 1) return set_error(DT_ERR_INVALID_ARG, "DT_OPT_SIDE_STREAM takes 0 or 1, not %d", value);
+        ctx->side_off = !value;
+        return DT_OK;
+    }
     if (option == DT_OPT_BWD_DQ) {
         if (value != DT_BWD_DQ_RECOMPUTE && value != DT_BWD_DQ_FROM_DS && value != DT_BWD_DQ_AUTO)
             return set_error(DT_ERR_INVALID_ARG,
@@ -578,7 +641,12 @@ int dt_ctx_destroy(dt_ctx* ctx) {
     ctx->fwd_split_cnt.release();
     ctx->qkv_ss.release();
     ctx->qkv_status.release();
+    if (ctx->side) (void)hipStreamSynchronize(static_cast<hipStream_t>(ctx->side));
     if (ctx->blas) rocblas_destroy_handle(static_cast<rocblas_handle>(ctx->blas));
+    if (ctx->blas_side) rocblas_destroy_handle(static_cast<rocblas_handle>(ctx->blas_side));
+    for (void* e : ctx->ev)
+        if (e) (void)hipEventDestroy(static_cast<hipEvent_t>(e));
+    if (ctx->side) (void)hipStreamDestroy(static_cast<hipStream_t>(ctx->side));
     if (ctx->lt) {
         LtCache* lc = static_cast<LtCache*>(ctx->lt);
         for (auto& kv : lc->plans) lt_free(kv.second);
@@ -586,6 +654,7 @@ int dt_ctx_destroy(dt_ctx* ctx) {
         delete lc;
     }
     ctx->lt_ws.release();
+    ctx->lt_ws_side.release();
     delete ctx;
     return DT_OK;
 }
@@ -1109,8 +1178,11 @@ int attn_layer_ensure_grads(dt_attn_layer* L, hipStream_t s) {
 
 
 // `writing` is set once the first gradient buffer is about to be written
+// side: the stream the weight gradients' last steps run on (null: s): the GEMMs of dWo and dWqkv and the column
+// sums of the q/k norm weights' partial rows. Each starts after the main stream has formed its input (slot
+// kEvFork); slot kEvO marks the end of dWo's GEMM, the last reader of d_out on it. The caller joins it back.
 static int attn_layer_bwd(dt_attn_layer* L, const float* d_out, const uint16_t* d_out16, float* d_x, int B, int T,
-                          int mem, void* stream, bool& writing) {
+                          int mem, void* stream, hipStream_t side, bool& writing) {
     clear_error();
     if (!d_out || !d_x) return set_error(DT_ERR_INVALID_ARG, "d_out and d_x must be non-NULL");
     if (mem != DT_MEM_DEVICE && mem != DT_MEM_HOST) return set_error(DT_ERR_INVALID_ARG, "unknown mem %d", mem);
@@ -1170,7 +1242,9 @@ static int attn_layer_bwd(dt_attn_layer* L, const float* d_out, const uint16_t* 
         wo = L->w_o16;
     }
     writing = true;
-    DT_TRY(gemm_rm(ctx, s, true, false, dm, dm, rows, g_in, dm, attn, dm, gb, L->g_o, dm, bf));
+    if (side) DT_TRY(stream_after(ctx, side, s, kEvFork));
+    DT_TRY(gemm_rm(ctx, side ? side : s, true, false, dm, dm, rows, g_in, dm, attn, dm, gb, L->g_o, dm, bf));
+    if (side) DT_TRY(stream_mark(ctx, side, kEvO));
     const void* d_o = d_attn;
     if (bf) {  // d_attn leaves the GEMM as bf16 (fp32 accumulation, one rounding): the attention backward is its
                // only reader (in the first half of d_attn32's bytes)
@@ -1190,14 +1264,20 @@ static int attn_layer_bwd(dt_attn_layer* L, const float* d_out, const uint16_t* 
     // steps 3-4 (:234-244): RoPE backward and the q/k norms' backward, in place on dq | dk
     NormRopeBwdArgs nb{dq, dq + dm * esz, pre, pre + dm * esz, rms, rms + rows, L->q_norm, L->k_norm,
                        static_cast<float*>(L->partial.ptr), ctx->rope_cos, ctx->rope_sin, rows, T, H, 3 * dm, 3 * dm};
-    DT_TRY(launch_qk_norm_rope_bwd(nb, bf, L->g_qn, L->g_kn, s, !fresh));
+    DT_TRY(launch_qk_norm_rope_bwd(nb, bf, side ? nullptr : L->g_qn, side ? nullptr : L->g_kn, s, !fresh));
+    if (side) {
+        DT_TRY(stream_after(ctx, side, s, kEvFork));
+        DT_TRY(launch_colsum(nb.partial, nblk, dm, L->g_qn, side, !fresh));
+        DT_TRY(launch_colsum(nb.partial + (size_t)nblk * dm, nblk, dm, L->g_kn, side, !fresh));
+    }
     // step 5 (:246-309): [dWq;dWk;dWv] += [dq|dk|dv]^T x and d_x = [dq|dk|dv] [Wq;Wk;Wv]
     const void* xin = bf ? L->x16.ptr : L->x32.ptr;
     const void* wqkv = bf ? static_cast<const void*>(L->w_qkv16) : static_cast<const void*>(L->w_qkv);
-    DT_TRY(gemm_rm(ctx, s, true, false, 3 * dm, dm, rows, dqkv, 3 * dm, xin, dm, gb, L->g_qkv, dm, bf));
+    DT_TRY(gemm_rm(ctx, side ? side : s, true, false, 3 * dm, dm, rows, dqkv, 3 * dm, xin, dm, gb, L->g_qkv, dm, bf));
     L->grad_zero_pending = false;  // every gradient buffer has been written
     DT_TRY(gemm_rm(ctx, s, false, false, rows, dm, 3 * dm, dqkv, 3 * dm, wqkv, dm, 0.0f, dxd, dm, bf));
     if (mem == DT_MEM_HOST) {
+        if (side) DT_TRY(stream_after(ctx, s, side, kEvJoin));
         DT_HIP_TRY(hipMemcpyAsync(d_x, dxd, act * 4, hipMemcpyDeviceToHost, s));
         DT_HIP_TRY(hipStreamSynchronize(s));
     }
@@ -1205,18 +1285,23 @@ static int attn_layer_bwd(dt_attn_layer* L, const float* d_out, const uint16_t* 
 }
 
 int attn_layer_bwd_dev(dt_attn_layer* L, const float* d_out, const uint16_t* d_out16, float* d_x, int B, int T,
-                       void* stream) {
+                       void* stream, hipStream_t side) {
     bool writing = false;
-    const int rc = attn_layer_bwd(L, d_out, d_out16, d_x, B, T, DT_MEM_DEVICE, stream, writing);
-    if (rc != DT_OK && writing && L->grad_zero_pending) (void)attn_layer_settle_grads(L, static_cast<hipStream_t>(stream));
+    const int rc = attn_layer_bwd(L, d_out, d_out16, d_x, B, T, DT_MEM_DEVICE, stream, side, writing);
+    if (rc != DT_OK && writing && L->grad_zero_pending) {
+        if (side) (void)stream_after(L->ctx, static_cast<hipStream_t>(stream), side, kEvJoin);
+        (void)attn_layer_settle_grads(L, static_cast<hipStream_t>(stream));
+    }
     return rc;
 }
 
 extern "C" {
 
 int dt_attn_layer_bwd(dt_attn_layer* L, const float* d_out, float* d_x, int B, int T, int mem, void* stream) {
+    // one stream: a lone layer has no later work for its weight-gradient GEMMs to run beside (on the side stream
+    // they measured slower, T = 512 and 2048); the model backward gives them the next block's
     bool writing = false;
-    const int rc = attn_layer_bwd(L, d_out, nullptr, d_x, B, T, mem, stream, writing);
+    const int rc = attn_layer_bwd(L, d_out, nullptr, d_x, B, T, mem, stream, nullptr, writing);
     // a backward that failed after zero_grad, once it had begun writing gradients, may have written some of them:
     // clear them all, so that they read as the zero_grad left them (the error stays the one reported)
     if (rc != DT_OK && writing && L->grad_zero_pending) (void)attn_layer_settle_grads(L, static_cast<hipStream_t>(stream));

@@ -210,6 +210,21 @@ int check_device_binding(dt_ctx* ctx);
 // after the stream has been synchronised: DT_ERR_HIP (and clears the word) when a fused QKV wait gave up
 int qkv_status_check(dt_ctx* ctx);
 
+// The context's side stream: weight-gradient GEMMs run on it beside the backward's chain of input gradients,
+// which never reads them. Created on first use (non-blocking, default priority; null when that fails or when s
+// is being captured into a graph, and the caller then stays on s). GEMMs on it use their own BLAS handle and
+// workspace.
+hipStream_t side_stream(dt_ctx* ctx, hipStream_t s);
+// Event slots of the context that order the two streams: a fork (side after main), and one per buffer the
+// side stream's GEMMs read and the main stream later overwrites.
+enum SideEvent { kEvFork = 0, kEvJoin, kEvDown, kEvGu, kEvO, kSideEvents };
+// waiter waits for all that producer has enqueued so far (an event recorded in slot ev)
+int stream_after(dt_ctx* ctx, hipStream_t waiter, hipStream_t producer, int ev);
+// waiter waits for the last record of slot ev (a no-op if the slot was never recorded)
+int stream_wait_slot(dt_ctx* ctx, hipStream_t waiter, int ev);
+// records slot ev on producer
+int stream_mark(dt_ctx* ctx, hipStream_t producer, int ev);
+
 }  // namespace dt
 
 // ---- opaque handles ----
@@ -234,6 +249,11 @@ struct dt_ctx {
     int gemm_tune = 1;            // DT_OPT_GEMM_TUNE
     int bwd_dq = DT_BWD_DQ_AUTO;  // DT_OPT_BWD_DQ
     dt::DeviceBuffer bwd_ds;      // bf16 attention backward: dS of one call (the dS path)
+    void* side = nullptr;         // hipStream_t: the side stream (dt::side_stream)
+    void* blas_side = nullptr;    // rocblas_handle for GEMMs on it
+    dt::DeviceBuffer lt_ws_side;  // hipBLASLt workspace of GEMMs on it
+    void* ev[dt::kSideEvents] = {};  // hipEvent_t slots (dt::SideEvent)
+    int side_off = 0;             // DT_OPT_SIDE_STREAM = 0: everything on the caller's stream
 };
 
 // OlmoAttention on the device (OlmoAttention.h:10-42): weights, forward state kept for backward, gradients.
@@ -270,10 +290,12 @@ struct dt_attn_layer {
 // so the layer does not round x itself
 int attn_layer_fwd(dt_attn_layer* L, const float* x, float* out, int B, int T, const int32_t* seq_lens, int dtype,
                    int mem, int save_for_backward, void* stream, bool x16_ready);
-// dt_attn_layer_bwd (device memory) with one more input: d_out16 (bf16 mode, nullable) holds d_out rounded to bf16
-// (the model's norm backward writes it beside d_out), so the layer does not round d_out itself
+// dt_attn_layer_bwd (device memory) with two more inputs: d_out16 (bf16 mode, nullable) holds d_out rounded to
+// bf16 (the model's norm backward writes it beside d_out), so the layer does not round d_out itself; side (nullable)
+// is the context's side stream for the weight-gradient GEMMs, which the caller joins back into its stream (slot
+// kEvO is recorded on it after the last read of d_out and d_out16)
 int attn_layer_bwd_dev(dt_attn_layer* L, const float* d_out, const uint16_t* d_out16, float* d_x, int B, int T,
-                       void* stream);
+                       void* stream, hipStream_t side);
 // zero-initialised attention layer (weights set afterwards), and its gradient buffers (allocated zeroed)
 int attn_layer_alloc(dt_ctx* ctx, int d_model, int n_heads, dt_attn_layer** out);
 int attn_layer_ensure_grads(dt_attn_layer* L, hipStream_t s);  // all four buffers, or none on failure

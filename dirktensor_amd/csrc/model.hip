@@ -76,7 +76,8 @@ struct dt_model {
     float* g_embed = nullptr;
     float* g_final = nullptr;
     float* g_lm = nullptr;
-    DeviceBuffer d16, dx, dh, da, dxa, dm_, d_act, d_gu, partial, csr;
+    // d16: d_logits as bf16; g16a / g16b: the bf16 gradient rows of a block's two norms (bf16 mode)
+    DeviceBuffer d16, g16a, g16b, dx, dh, da, dxa, dm_, d_act, d_gu, partial, csr;
 };
 
 namespace {
@@ -313,7 +314,7 @@ int dt_model_destroy(dt_model* M) {
         for (DeviceBuffer* b : {&Ly.a, &Ly.y_pa, &Ly.rms_pa, &Ly.h, &Ly.h16, &Ly.gu, &Ly.act, &Ly.m, &Ly.y_pf, &Ly.rms_pf})
             b->release();
     }
-    for (DeviceBuffer* b : {&M->tok, &M->x, &M->x2, &M->yf, &M->yf16, &M->rmsf, &M->logits, &M->d16, &M->dx, &M->dh,
+    for (DeviceBuffer* b : {&M->tok, &M->x, &M->x2, &M->yf, &M->yf16, &M->rmsf, &M->logits, &M->d16, &M->g16a, &M->g16b, &M->dx, &M->dh,
                             &M->da, &M->dxa, &M->dm_, &M->d_act, &M->d_gu, &M->partial, &M->csr,
                             &M->embed_rows_dev})
         b->release();
@@ -531,7 +532,12 @@ int dt_model_fwd(dt_model* M, const int32_t* tokens, int B, int T, float* logits
 }
 
 // `writing` is set once the first gradient buffer is about to be written
-static int model_bwd(dt_model* M, const float* d_logits, int mem, void* stream, bool& writing) {
+// The weight-gradient GEMMs (dW of the LM head, the MLP's down and gate/up matrices, and inside each attention
+// layer dWo and dWqkv) run on the context's side stream when it has one, beside the chain of input gradients on s,
+// which never reads them. Each starts after s has formed its input (slot kEvFork). s waits for the side stream only
+// before it overwrites a buffer a pending side GEMM reads: the MLP's norm-gradient rows (slot kEvDown), d_gu
+// (kEvGu) and the attention layer's d_out rows (kEvO), each one block later; and at the end (kEvJoin).
+static int model_bwd(dt_model* M, const float* d_logits, int mem, void* stream, hipStream_t side, bool& writing) {
     clear_error();
     if (!M || !d_logits) return set_error(DT_ERR_INVALID_ARG, "model and d_logits must be non-NULL");
     if (mem != DT_MEM_DEVICE && mem != DT_MEM_HOST) return set_error(DT_ERR_INVALID_ARG, "unknown mem %d", mem);
@@ -562,60 +568,96 @@ static int model_bwd(dt_model* M, const float* d_logits, int mem, void* stream, 
     DT_TRY(M->dm_.ensure(act * 4));
     DT_TRY(M->d_act.ensure((size_t)rows * hid * 4));
     DT_TRY(M->d_gu.ensure((size_t)rows * 2 * hid * (bf ? 2 : 4)));
-    DT_TRY(M->partial.ensure((size_t)rmsnorm_bwd_blocks(rows) * dm * 4));
-    DT_TRY(M->d16.ensure(std::max((size_t)rows * V, act) * 2));
+    const int nblk = rmsnorm_bwd_blocks(rows);
+    DT_TRY(M->partial.ensure((size_t)3 * nblk * dm * 4));  // the final norm's, then N_pf's and N_pa's
+    if (bf) {
+        DT_TRY(M->d16.ensure((size_t)rows * V * 2));
+        DT_TRY(M->g16a.ensure(act * 2));
+        DT_TRY(M->g16b.ensure(act * 2));
+    }
     float* dx = static_cast<float*>(M->dx.ptr);
     float* dh = static_cast<float*>(M->dh.ptr);
     float* da = static_cast<float*>(M->da.ptr);
     float* dxa = static_cast<float*>(M->dxa.ptr);
     float* dmo = static_cast<float*>(M->dm_.ptr);
     float* d_act = static_cast<float*>(M->d_act.ptr);
-    float* partial = static_cast<float*>(M->partial.ptr);
+    float* part_f = static_cast<float*>(M->partial.ptr);
+    float* part_pf = part_f + (size_t)nblk * dm;
+    float* part_pa = part_pf + (size_t)nblk * dm;
     uint16_t* d16 = static_cast<uint16_t*>(M->d16.ptr);
+    uint16_t* g16a = static_cast<uint16_t*>(M->g16a.ptr);
+    uint16_t* g16b = static_cast<uint16_t*>(M->g16b.ptr);
+    hipStream_t sw = side ? side : s;  // the weight-gradient GEMMs' stream
+    auto fork = [&]() { return side ? stream_after(ctx, side, s, kEvFork) : DT_OK; };
+    auto wait_side = [&](int ev) { return side ? stream_wait_slot(ctx, s, ev) : DT_OK; };
+    // a norm weight's gradient: the column sums of the partial rows its backward kernel wrote (on the side stream
+    // when there is one; each norm has its own partial rows, which the side stream has read before the next
+    // kEvDown / kEvO mark)
+    auto norm_grad_w = [&](float* g) { return side ? nullptr : g; };
+    auto norm_colsum = [&](const float* part, float* g) {
+        if (!side) return DT_OK;
+        DT_TRY(fork());
+        return launch_colsum(part, nblk, dm, g, side, !fresh);
+    };
 
     // LM head (OlmoLmHead.cpp:30-62): dW += d_logits^T y; d_y = d_logits W
     float* d_yf = da;
     writing = true;
     if (bf) {
         DT_TRY(launch_f32_to_bf16(gl, d16, (int64_t)rows * V, s));
-        DT_TRY(gemm_rm(ctx, s, true, false, V, dm, rows, d16, V, M->yf16.ptr, dm, gb, M->g_lm, dm, true));
+        DT_TRY(fork());
+        DT_TRY(gemm_rm(ctx, sw, true, false, V, dm, rows, d16, V, M->yf16.ptr, dm, gb, M->g_lm, dm, true));
         DT_TRY(gemm_rm(ctx, s, false, false, rows, dm, V, d16, V, M->lm_head16, dm, 0.0f, d_yf, dm, true));
     } else {
-        DT_TRY(gemm_rm(ctx, s, true, false, V, dm, rows, gl, V, M->yf.ptr, dm, gb, M->g_lm, dm, false));
+        DT_TRY(fork());
+        DT_TRY(gemm_rm(ctx, sw, true, false, V, dm, rows, gl, V, M->yf.ptr, dm, gb, M->g_lm, dm, false));
         DT_TRY(gemm_rm(ctx, s, false, false, rows, dm, V, gl, V, M->lm_head, dm, 0.0f, d_yf, dm, false));
     }
     // final norm (OlmoModel.cpp:52): RMSNorm::backward from the saved output y and rms
     DT_TRY(launch_rmsnorm_bwd(d_yf, static_cast<const float*>(M->yf.ptr), static_cast<const float*>(M->rmsf.ptr),
-                              M->final_norm, nullptr, dx, partial, M->g_final, rows, dm, s, !fresh));
+                              M->final_norm, nullptr, dx, part_f, norm_grad_w(M->g_final), rows, dm, s, !fresh));
+    DT_TRY(norm_colsum(part_f, M->g_final));
     // blocks in reverse (OlmoBlock.cpp:23-30)
     for (int li = M->n_layers - 1; li >= 0; --li) {
         ModelLayer& Ly = M->L[li];
-        // d_m = N_pf.backward(d_x) (in bf16 mode only as bf16: the two GEMMs below are its only readers)
+        // d_m = N_pf.backward(d_x) (in bf16 mode only as bf16: the two GEMMs below are its only readers), over the
+        // rows the previous block's dWdown GEMM read
+        DT_TRY(wait_side(kEvDown));
         DT_TRY(launch_rmsnorm_bwd(dx, static_cast<const float*>(Ly.y_pf.ptr), static_cast<const float*>(Ly.rms_pf.ptr),
-                                  Ly.w_pf, nullptr, bf ? nullptr : dmo, partial, Ly.g_pf, rows, dm, s, !fresh,
-                                  bf ? d16 : nullptr));
+                                  Ly.w_pf, nullptr, bf ? nullptr : dmo, part_pf, norm_grad_w(Ly.g_pf), rows, dm, s,
+                                  !fresh, bf ? g16a : nullptr));
         // MLP backward: dWdown += d_m^T act; d_act = d_m Wdown; d_gu = swiglu'; dW_gu += d_gu^T h;
         // d_h = d_gu W_gu + d_x (the residual, OlmoBlock.cpp:28; GEMM with beta = 1 into a copy of d_x)
         DT_HIP_TRY(hipMemcpyAsync(dh, dx, act * 4, hipMemcpyDeviceToDevice, s));
+        DT_TRY(norm_colsum(part_pf, Ly.g_pf));  // (forks the side stream for the GEMM below as well)
         if (bf) {
-            DT_TRY(gemm_rm(ctx, s, true, false, dm, hid, rows, d16, dm, Ly.act.ptr, hid, gb, Ly.g_down, hid, true));
-            DT_TRY(gemm_rm(ctx, s, false, false, rows, hid, dm, d16, dm, Ly.w_down16, hid, 0.0f, d_act, hid, true));
+            DT_TRY(gemm_rm(ctx, sw, true, false, dm, hid, rows, g16a, dm, Ly.act.ptr, hid, gb, Ly.g_down, hid, true));
+            if (side) DT_TRY(stream_mark(ctx, side, kEvDown));
+            DT_TRY(gemm_rm(ctx, s, false, false, rows, hid, dm, g16a, dm, Ly.w_down16, hid, 0.0f, d_act, hid, true));
         } else {
-            DT_TRY(gemm_rm(ctx, s, true, false, dm, hid, rows, dmo, dm, Ly.act.ptr, hid, gb, Ly.g_down, hid, false));
+            DT_TRY(gemm_rm(ctx, sw, true, false, dm, hid, rows, dmo, dm, Ly.act.ptr, hid, gb, Ly.g_down, hid, false));
+            if (side) DT_TRY(stream_mark(ctx, side, kEvDown));
             DT_TRY(gemm_rm(ctx, s, false, false, rows, hid, dm, dmo, dm, Ly.w_down, hid, 0.0f, d_act, hid, false));
         }
+        DT_TRY(wait_side(kEvGu));  // the previous block's dW_gu GEMM has read d_gu
         DT_TRY(launch_swiglu_bwd(d_act, Ly.gu.ptr, M->d_gu.ptr, rows, hid, bf, s));
         const void* hin = bf ? Ly.h16.ptr : Ly.h.ptr;
         const void* wgu = bf ? static_cast<const void*>(Ly.w_gu16) : static_cast<const void*>(Ly.w_gu);
-        DT_TRY(gemm_rm(ctx, s, true, false, 2 * hid, dm, rows, M->d_gu.ptr, 2 * hid, hin, dm, gb, Ly.g_gu, dm, bf));
+        DT_TRY(fork());
+        DT_TRY(gemm_rm(ctx, sw, true, false, 2 * hid, dm, rows, M->d_gu.ptr, 2 * hid, hin, dm, gb, Ly.g_gu, dm, bf));
+        if (side) DT_TRY(stream_mark(ctx, side, kEvGu));
         DT_TRY(gemm_rm(ctx, s, false, false, rows, dm, 2 * hid, M->d_gu.ptr, 2 * hid, wgu, dm, 1.0f, dh, dm, bf));
         // d_a = N_pa.backward(d_h); d_x = attn.backward(d_a) + d_h (OlmoBlock.cpp:29-32); in bf16 mode d_a also as
-        // bf16, the form the layer's output-projection GEMMs read (d16 is free again: the GEMMs above have read it)
+        // bf16, the form the layer's output-projection GEMMs read, over the rows the previous block's dWo GEMM read
+        DT_TRY(wait_side(kEvO));
         DT_TRY(launch_rmsnorm_bwd(dh, static_cast<const float*>(Ly.y_pa.ptr), static_cast<const float*>(Ly.rms_pa.ptr),
-                                  Ly.w_pa, nullptr, da, partial, Ly.g_pa, rows, dm, s, !fresh, bf ? d16 : nullptr));
-        DT_TRY(attn_layer_bwd_dev(Ly.attn, da, bf ? d16 : nullptr, dxa, B, T, stream));
+                                  Ly.w_pa, nullptr, da, part_pa, norm_grad_w(Ly.g_pa), rows, dm, s, !fresh,
+                                  bf ? g16b : nullptr));
+        DT_TRY(norm_colsum(part_pa, Ly.g_pa));
+        DT_TRY(attn_layer_bwd_dev(Ly.attn, da, bf ? g16b : nullptr, dxa, B, T, stream, side));
         DT_TRY(launch_add(dxa, dh, dx, (int64_t)act, s));
     }
+    if (side) DT_TRY(stream_after(ctx, s, side, kEvJoin));
     M->grad_zero_pending = false;  // every model-level gradient buffer but the embedding's has been written
     // embedding (OlmoModel.cpp:57-66): per distinct token, its positions in order (CSR built here)
     std::vector<int32_t> order(rows);
@@ -661,7 +703,12 @@ static int model_bwd(dt_model* M, const float* d_logits, int mem, void* stream, 
 int dt_model_bwd(dt_model* M, const float* d_logits, int mem, void* stream) {
     bool writing = false;
     const bool was_pending = M && M->grad_zero_pending;
-    const int rc = model_bwd(M, d_logits, mem, stream, writing);
+    hipStream_t s = static_cast<hipStream_t>(stream);
+    hipStream_t side = (M && check_device_binding(M->ctx) == DT_OK) ? side_stream(M->ctx, s) : nullptr;
+    clear_error();
+    const int rc = model_bwd(M, d_logits, mem, stream, side, writing);
+    // on an error the caller's stream still takes over what the side stream holds of this call
+    if (rc != DT_OK && side) (void)stream_after(M->ctx, s, side, kEvJoin);
     // a backward that failed after zero_grad, once it had begun writing gradients, may have written some of them:
     // clear them all (the layers' too), so that they read as the zero_grad left them (the error stays the one
     // reported)

@@ -449,6 +449,7 @@ int launch_rmsnorm_bwd(const float* dy, const float* y, const float* rms, const 
     hipLaunchKernelGGL(rmsnorm_bwd_rows_kernel, dim3(nblk), dim3(256), 0, s, dy, y, rms, w, dx_add, dx, dx16, partial,
                        (int64_t)rows, dm);
     DT_HIP_TRY(hipGetLastError());
+    if (!grad_w) return DT_OK;  // the caller sums the partial rows itself
     return launch_colsum(partial, nblk, dm, grad_w, s, accumulate);
 }
 

@@ -218,6 +218,7 @@ int launch_qk_norm_rope_bwd(const NormRopeBwdArgs& a, int bf16, float* grad_q_w,
     if (bf16) hipLaunchKernelGGL(qk_norm_rope_bwd_kernel<true>, grid, dim3(256), 0, stream, a, rpb);
     else hipLaunchKernelGGL(qk_norm_rope_bwd_kernel<false>, grid, dim3(256), 0, stream, a, rpb);
     DT_HIP_TRY(hipGetLastError());
+    if (!grad_q_w && !grad_k_w) return DT_OK;  // the caller sums the partial rows itself
     const int C = a.H * 128;  // partial: [q, k][nblk][C]
     DT_TRY(launch_colsum(a.partial, nblk, C, grad_q_w, stream, accumulate));
     return launch_colsum(a.partial + (int64_t)nblk * C, nblk, C, grad_k_w, stream, accumulate);

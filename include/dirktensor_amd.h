@@ -142,12 +142,24 @@ int dt_ctx_destroy(dt_ctx* ctx);
  *                     (and any synchronous DT_MEM_HOST layer or model forward)
  *                     reports as DT_ERR_HIP. 0 makes every wait give up at
  *                     once (for testing that report).
+ *   DT_OPT_SIDE_STREAM 1 (default): the model backward (dt_model_bwd) runs
+ *                     its weight gradients' GEMMs and norm-weight column sums
+ *                     on a second stream of the context, beside the chain of
+ *                     input gradients on the caller's stream, ordered by
+ *                     events; the call's work on both streams is enqueued
+ *                     behind what the caller's stream holds, and the caller's
+ *                     stream waits for all of it before the call returns
+ *                     (results are the same bits as on one stream). Skipped
+ *                     while the caller's stream is capturing a graph. 0: one
+ *                     stream. (dt_attn_layer_bwd always runs on the caller's
+ *                     stream.)
  * Returns DT_ERR_INVALID_ARG for an unknown option or value.
  */
 #define DT_OPT_QKV_FUSED 1
 #define DT_OPT_GEMM_TUNE 2
 #define DT_OPT_BWD_DQ 3
 #define DT_OPT_QKV_SPIN_LIMIT 4
+#define DT_OPT_SIDE_STREAM 5
 #define DT_QKV_GEMM 0
 #define DT_QKV_FUSED 1
 #define DT_QKV_AUTO 2

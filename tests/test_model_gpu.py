@@ -250,6 +250,34 @@ def test_backward_long_k_products(gpu):
 
 
 @pytest.mark.parametrize("mode", ["fp32", "bf16"])
+def test_side_stream_same_bits(gpu, params, mode):
+    """The weight-gradient GEMMs on the context's side stream (the default) give the same bits as everything on
+    the caller's stream (DT_OPT_SIDE_STREAM = 0): every gradient after two accumulating backward passes, and
+    every parameter after the step that follows."""
+    from dirktensor_amd import Context
+
+    B, T = 2, 64
+    tok = synth.model_tokens(B, T, VOCAB, seed=6501)
+    G = torch.from_numpy(synth.normal(6502, (B, T, VOCAB), 0.0, 1e-3)).to(gpu)
+    runs = []
+    for side in (True, False):
+        ctx = Context(0)
+        ctx.set_side_stream(side)
+        m = OlmoModel.from_params(params, ctx=ctx)
+        for _ in range(2):
+            m.forward(tok, mode=mode)
+            m.backward(G)
+        grads = {k: m.grad(k) for k in params}
+        m.step(1e-3)
+        runs.append((grads, {k: m.param(k) for k in params}))
+        m.close()
+        ctx.close()
+    for k in params:
+        assert np.array_equal(runs[0][0][k], runs[1][0][k]), k
+        assert np.array_equal(runs[0][1][k], runs[1][1][k]), k
+
+
+@pytest.mark.parametrize("mode", ["fp32", "bf16"])
 def test_model_load_from_npy_folder(gpu, params, model, mode, tmp_path_factory):
     """OlmoModel(folder) (dt_model_load, OlmoModel.cpp:12-23) reads the reference's .npy files: its logits are
     bit-identical to those of the same parameters set one by one through dt_model_set_param, and every parameter
