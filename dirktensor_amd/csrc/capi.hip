@@ -1267,8 +1267,7 @@ static int attn_layer_bwd(dt_attn_layer* L, const float* d_out, const uint16_t* 
     DT_TRY(launch_qk_norm_rope_bwd(nb, bf, side ? nullptr : L->g_qn, side ? nullptr : L->g_kn, s, !fresh));
     if (side) {
         DT_TRY(stream_after(ctx, side, s, kEvFork));
-        DT_TRY(launch_colsum(nb.partial, nblk, dm, L->g_qn, side, !fresh));
-        DT_TRY(launch_colsum(nb.partial + (size_t)nblk * dm, nblk, dm, L->g_kn, side, !fresh));
+        DT_TRY(launch_colsum(nb.partial, nblk, dm, L->g_qn, side, !fresh, L->g_kn));
     }
     // step 5 (:246-309): [dWq;dWk;dWv] += [dq|dk|dv]^T x and d_x = [dq|dk|dv] [Wq;Wk;Wv]
     const void* xin = bf ? L->x16.ptr : L->x32.ptr;
@@ -1281,6 +1280,19 @@ static int attn_layer_bwd(dt_attn_layer* L, const float* d_out, const uint16_t* 
         DT_HIP_TRY(hipMemcpyAsync(d_x, dxd, act * 4, hipMemcpyDeviceToHost, s));
         DT_HIP_TRY(hipStreamSynchronize(s));
     }
+    return DT_OK;
+}
+
+int attn_layer_step_mats(dt_attn_layer* L, float lr, hipStream_t s) {
+    DT_TRY(attn_layer_ensure_grads(L, s));
+    DT_TRY(attn_layer_settle_grads(L, s));
+    const int64_t dm = L->d_model;
+    // the bf16 copies (once the bf16 mode has made them) are rewritten from the updated weights in the
+    // same pass, so they are current afterwards
+    const bool copies = L->w_qkv16 && L->w_o16;
+    DT_TRY(launch_sgd(L->w_qkv, L->g_qkv, lr, 3 * dm * dm, s, copies ? L->w_qkv16 : nullptr));  // OlmoAttention.cpp:315-317
+    DT_TRY(launch_sgd(L->w_o, L->g_o, lr, dm * dm, s, copies ? L->w_o16 : nullptr));            // :318
+    L->w16_stale = !copies;
     return DT_OK;
 }
 
@@ -1314,18 +1326,12 @@ int dt_attn_layer_step(dt_attn_layer* L, float lr, void* stream) {
     if (!std::isfinite(lr)) return set_error(DT_ERR_INVALID_ARG, "lr must be finite");
     DT_TRY(check_device_binding(L->ctx));
     hipStream_t s = static_cast<hipStream_t>(stream);
-    DT_TRY(attn_layer_ensure_grads(L, s));
-    DT_TRY(attn_layer_settle_grads(L, s));
-    const int64_t dm = L->d_model;
-    // the bf16 copies (once the bf16 mode has made them) are rewritten from the updated weights in the
-    // same pass, so they are current afterwards
-    const bool copies = L->w_qkv16 && L->w_o16;
-    DT_TRY(launch_sgd(L->w_qkv, L->g_qkv, lr, 3 * dm * dm, s, copies ? L->w_qkv16 : nullptr));  // OlmoAttention.cpp:315-317
-    DT_TRY(launch_sgd(L->w_o, L->g_o, lr, dm * dm, s, copies ? L->w_o16 : nullptr));            // :318
-    DT_TRY(launch_sgd(L->q_norm, L->g_qn, lr, dm, s));  // :319, RMSNorm.cpp:38-40
-    DT_TRY(launch_sgd(L->k_norm, L->g_kn, lr, dm, s));  // :320
-    L->w16_stale = !copies;
-    return DT_OK;
+    DT_TRY(attn_layer_step_mats(L, lr, s));
+    // :319-320, RMSNorm.cpp:38-40: both norm weights in one launch
+    float* w[2] = {L->q_norm, L->k_norm};
+    const float* g[2] = {L->g_qn, L->g_kn};
+    const int n[2] = {L->d_model, L->d_model};
+    return launch_sgd_vecs(w, g, n, 2, lr, s);
 }
 
 int dt_attn_layer_zero_grad(dt_attn_layer* L, void* stream) {

@@ -185,9 +185,14 @@ int launch_qk_norm_rope_bwd(const NormRopeBwdArgs& a, int bf16, float* grad_q_w,
                             bool accumulate = true);
 // out[c] += sum_b partial[b][c] (b = 0 .. nblk-1; out[c] = 0 + the sum when accumulate is false), deterministic
 // order
-int launch_colsum(const float* partial, int nblk, int ncols, float* out, hipStream_t s, bool accumulate = true);
+// out[c] (+)= sum over the nblk partial rows of column c, in a fixed order; with out1, a second such sum over the
+// nblk rows that follow, into out1, in the same launch
+int launch_colsum(const float* partial, int nblk, int ncols, float* out, hipStream_t s, bool accumulate = true,
+                  float* out1 = nullptr);
 // w -= lr * g; w16 (nullable): the bf16 copy of w, refreshed in the same pass
 int launch_sgd(float* w, const float* g, float lr, int64_t n, hipStream_t stream, uint16_t* w16 = nullptr);
+// the same update of count short vectors (the norm weights) in one launch, one workgroup per vector
+int launch_sgd_vecs(float* const* w, const float* const* g, const int* n, int count, float lr, hipStream_t stream);
 int launch_fill_zero(float* p, int64_t n, hipStream_t stream);
 int launch_f32_to_bf16(const float* in, uint16_t* out, int64_t n, hipStream_t stream);
 
@@ -297,6 +302,8 @@ int attn_layer_fwd(dt_attn_layer* L, const float* x, float* out, int B, int T, c
 int attn_layer_bwd_dev(dt_attn_layer* L, const float* d_out, const uint16_t* d_out16, float* d_x, int B, int T,
                        void* stream, hipStream_t side);
 // zero-initialised attention layer (weights set afterwards), and its gradient buffers (allocated zeroed)
+// dt_attn_layer_step's updates of Wqkv and Wo (and their bf16 copies), without the two norm weights
+int attn_layer_step_mats(dt_attn_layer* L, float lr, hipStream_t s);
 int attn_layer_alloc(dt_ctx* ctx, int d_model, int n_heads, dt_attn_layer** out);
 int attn_layer_ensure_grads(dt_attn_layer* L, hipStream_t s);  // all four buffers, or none on failure
 bool attn_layer_grads_complete(const dt_attn_layer* L);

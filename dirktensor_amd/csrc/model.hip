@@ -741,14 +741,26 @@ int dt_model_step(dt_model* M, float lr, void* stream) {
     else
         DT_TRY(launch_embed_rows(M->embed, M->g_embed, static_cast<const int32_t*>(M->embed_rows_dev.ptr),
                                  (int)M->embed_rows.size(), (int)dm, lr, false, s));
+    // the norm weights (q_norm, k_norm and both block norms of every block, the final norm) are gathered into
+    // one launch; each is a single workgroup's work
+    std::vector<float*> vw;
+    std::vector<const float*> vg;
+    auto vec = [&](float* w, const float* g) {
+        vw.push_back(w);
+        vg.push_back(g);
+    };
     for (ModelLayer& Ly : M->L) {
-        DT_TRY(dt_attn_layer_step(Ly.attn, lr, stream));  // OlmoBlock.cpp:32-37
-        DT_TRY(launch_sgd(Ly.w_pa, Ly.g_pa, lr, dm, s));
+        DT_TRY(attn_layer_step_mats(Ly.attn, lr, s));  // OlmoBlock.cpp:32-37
+        vec(Ly.attn->q_norm, Ly.attn->g_qn);
+        vec(Ly.attn->k_norm, Ly.attn->g_kn);
+        vec(Ly.w_pa, Ly.g_pa);
         DT_TRY(launch_sgd(Ly.w_gu, Ly.g_gu, lr, 2 * hid * dm, s, copies ? Ly.w_gu16 : nullptr));
         DT_TRY(launch_sgd(Ly.w_down, Ly.g_down, lr, dm * hid, s, copies ? Ly.w_down16 : nullptr));
-        DT_TRY(launch_sgd(Ly.w_pf, Ly.g_pf, lr, dm, s));
+        vec(Ly.w_pf, Ly.g_pf);
     }
-    DT_TRY(launch_sgd(M->final_norm, M->g_final, lr, dm, s));
+    vec(M->final_norm, M->g_final);
+    const std::vector<int> vn(vw.size(), (int)dm);
+    DT_TRY(launch_sgd_vecs(vw.data(), vg.data(), vn.data(), (int)vw.size(), lr, s));
     DT_TRY(launch_sgd(M->lm_head, M->g_lm, lr, V * dm, s, copies ? M->lm_head16 : nullptr));
     M->w16_stale = !copies;
     return DT_OK;

@@ -290,8 +290,13 @@ __global__ __launch_bounds__(256) void rmsnorm_bwd_rows_kernel(const float* dy, 
 // out[c] += sum over b of partial[b][c], in a fixed order: a workgroup takes 64 columns; thread group g (of
 // 4) sums rows g, g+4, g+8, ... in increasing order, then the four sums are added g = 0..3. Deterministic,
 // and 4 x 64 lanes keep many rows in flight instead of one serial chain per column.
-__global__ __launch_bounds__(256) void colsum_kernel(const float* partial, int nblk, int ncols, float* out, int accumulate) {
+// Two such sums in one launch when out1 is given: blockIdx.y = 1 takes the partial rows that follow the first
+// nblk and writes out1.
+__global__ __launch_bounds__(256) void colsum_kernel(const float* partial, int nblk, int ncols, float* out0,
+                                                     float* out1, int accumulate) {
     __shared__ float part[4][64];
+    float* out = blockIdx.y ? out1 : out0;
+    partial += (int64_t)blockIdx.y * nblk * ncols;
     const int cl = threadIdx.x & 63, g = threadIdx.x >> 6;
     const int c = blockIdx.x * 64 + cl;
     float s = 0.0f;
@@ -453,9 +458,10 @@ int launch_rmsnorm_bwd(const float* dy, const float* y, const float* rms, const 
     return launch_colsum(partial, nblk, dm, grad_w, s, accumulate);
 }
 
-int launch_colsum(const float* partial, int nblk, int ncols, float* out, hipStream_t s, bool accumulate) {
-    hipLaunchKernelGGL(colsum_kernel, dim3((ncols + 63) / 64), dim3(256), 0, s, partial, nblk, ncols, out,
-                       accumulate ? 1 : 0);
+int launch_colsum(const float* partial, int nblk, int ncols, float* out, hipStream_t s, bool accumulate,
+                  float* out1) {
+    hipLaunchKernelGGL(colsum_kernel, dim3((ncols + 63) / 64, out1 ? 2 : 1), dim3(256), 0, s, partial, nblk, ncols, out,
+                       out1, accumulate ? 1 : 0);
     DT_HIP_TRY(hipGetLastError());
     return DT_OK;
 }

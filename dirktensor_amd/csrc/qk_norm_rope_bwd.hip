@@ -27,6 +27,8 @@
 // HBM bound: per row it reads g, x (twice, the second time mostly from L2)
 // and writes dx.
 
+#include <algorithm>
+
 #include "dt_internal.h"
 
 namespace dt {
@@ -187,6 +189,24 @@ __global__ __launch_bounds__(256) void sgd4_kernel(float4* w, const float4* g, f
     }
 }
 
+// sgd_kernel's update over several short vectors, workgroup b taking vector b
+constexpr int kMaxSgdVecs = 96;
+struct SgdVecs {
+    float* w[kMaxSgdVecs];
+    const float* g[kMaxSgdVecs];
+    int n[kMaxSgdVecs];
+};
+__global__ __launch_bounds__(256) void sgd_vecs_kernel(SgdVecs v, float lr) {
+#pragma clang fp contract(off)
+    float* w = v.w[blockIdx.x];
+    const float* g = v.g[blockIdx.x];
+    const int n = v.n[blockIdx.x];
+    for (int i = threadIdx.x; i < n; i += 256) {
+        const float step = lr * g[i];
+        w[i] = w[i] - step;
+    }
+}
+
 __global__ __launch_bounds__(256) void fill_zero_kernel(float* p, int64_t n) {
     for (int64_t i = (int64_t)blockIdx.x * 256 + threadIdx.x; i < n; i += (int64_t)gridDim.x * 256) p[i] = 0.0f;
 }
@@ -220,8 +240,7 @@ int launch_qk_norm_rope_bwd(const NormRopeBwdArgs& a, int bf16, float* grad_q_w,
     DT_HIP_TRY(hipGetLastError());
     if (!grad_q_w && !grad_k_w) return DT_OK;  // the caller sums the partial rows itself
     const int C = a.H * 128;  // partial: [q, k][nblk][C]
-    DT_TRY(launch_colsum(a.partial, nblk, C, grad_q_w, stream, accumulate));
-    return launch_colsum(a.partial + (int64_t)nblk * C, nblk, C, grad_k_w, stream, accumulate);
+    return launch_colsum(a.partial, nblk, C, grad_q_w, stream, accumulate, grad_k_w);
 }
 
 int launch_sgd(float* w, const float* g, float lr, int64_t n, hipStream_t stream, uint16_t* w16) {
@@ -235,6 +254,21 @@ int launch_sgd(float* w, const float* g, float lr, int64_t n, hipStream_t stream
         if (w16) return launch_f32_to_bf16(w, w16, n, stream);
     }
     DT_HIP_TRY(hipGetLastError());
+    return DT_OK;
+}
+
+int launch_sgd_vecs(float* const* w, const float* const* g, const int* n, int count, float lr, hipStream_t stream) {
+    for (int b0 = 0; b0 < count; b0 += kMaxSgdVecs) {
+        SgdVecs v{};
+        const int c = std::min(count - b0, kMaxSgdVecs);
+        for (int i = 0; i < c; ++i) {
+            v.w[i] = w[b0 + i];
+            v.g[i] = g[b0 + i];
+            v.n[i] = n[b0 + i];
+        }
+        hipLaunchKernelGGL(sgd_vecs_kernel, dim3(c), dim3(256), 0, stream, v, lr);
+        DT_HIP_TRY(hipGetLastError());
+    }
     return DT_OK;
 }
 

@@ -169,4 +169,3 @@ def test_layer_backward_ds_path(gpu, weights, mode, B, T):
     errs.update({k: rel_err(grads[k], ref_g[k]) for k in KEYS})
     print(f"dS path {mode} B={B} T={T}: " + " ".join(f"{k} {v:.2e}" for k, v in errs.items()))
     assert max(errs.values()) <= (TOL_FP32 if mode == "fp32" else TOL_BF16), errs
-
