@@ -221,6 +221,74 @@ __global__ __launch_bounds__(256) void ce_rows_kernel(const float* logits, const
     }
 }
 
+// The same row with the whole row held in registers (kChunks float4 per thread, 1024 threads, so V / 4 <= 1024 *
+// kChunks; V % 4 == 0, 16-byte aligned rows): the row is read from memory once instead of twice. The row's
+// maximum is formed first and the sum of exponentials then taken relative to it.
+template <int kChunks>
+__global__ __launch_bounds__(1024) void ce_rows_reg_kernel(const float* logits, const int32_t* target, float* term,
+                                                           float* grad, int V, float inv_count) {
+    __shared__ float red[16];
+    const int tid = threadIdx.x, lane = tid & 63, wv = tid >> 6;
+    const int64_t row = blockIdx.x;
+    const int tgt = target[row];
+    const float* l = logits + row * V;
+    float* g = grad ? grad + row * V : nullptr;
+    const int V4 = V / 4;
+    if (tgt < 0) {
+        if (tid == 0) term[row] = 0.0f;
+        if (g)
+            for (int i = tid; i < V4; i += 1024)
+                reinterpret_cast<float4*>(g)[i] = make_float4(0.0f * inv_count, 0.0f * inv_count, 0.0f * inv_count,
+                                                              0.0f * inv_count);
+        return;
+    }
+    const float l_tgt = tid == 0 ? l[tgt] : 0.0f;  // before the barriers: the gradient may overwrite it
+    constexpr float kNegInf = -__builtin_huge_valf();
+    float4 x[kChunks];
+    float m = kNegInf;
+#pragma unroll
+    for (int c = 0; c < kChunks; ++c) {
+        const int i = c * 1024 + tid;
+        x[c] = i < V4 ? reinterpret_cast<const float4*>(l)[i] : make_float4(kNegInf, kNegInf, kNegInf, kNegInf);
+        m = fmaxf(m, fmaxf(fmaxf(x[c].x, x[c].y), fmaxf(x[c].z, x[c].w)));
+    }
+#pragma unroll
+    for (int off = 32; off >= 1; off >>= 1) m = fmaxf(m, __shfl_xor(m, off, 64));
+    if (lane == 0) red[wv] = m;
+    __syncthreads();
+    float mx = red[0];
+    for (int k = 1; k < 16; ++k) mx = fmaxf(mx, red[k]);
+    __syncthreads();  // red is reused below
+    float s = 0.0f;
+#pragma unroll
+    for (int c = 0; c < kChunks; ++c)
+        s += (expf(x[c].x - mx) + expf(x[c].y - mx)) + (expf(x[c].z - mx) + expf(x[c].w - mx));
+#pragma unroll
+    for (int off = 32; off >= 1; off >>= 1) s += __shfl_xor(s, off, 64);
+    if (lane == 0) red[wv] = s;
+    __syncthreads();
+    float se = 0.0f;
+    for (int k = 0; k < 16; ++k) se += red[k];
+    if (tid == 0) term[row] = logf(se) - (l_tgt - mx);
+    if (g) {
+        const float inv = 1.0f / se;
+#pragma unroll
+        for (int c = 0; c < kChunks; ++c) {
+            const int i = c * 1024 + tid;
+            if (i < V4) {
+                float p[4] = {expf(x[c].x - mx) * inv, expf(x[c].y - mx) * inv, expf(x[c].z - mx) * inv,
+                              expf(x[c].w - mx) * inv};
+#pragma unroll
+                for (int e = 0; e < 4; ++e)
+                    if (4 * i + e == tgt) p[e] -= 1.0f;
+                reinterpret_cast<float4*>(g)[i] =
+                    make_float4(p[0] * inv_count, p[1] * inv_count, p[2] * inv_count, p[3] * inv_count);
+            }
+        }
+    }
+}
+constexpr int kCeChunks = 25;  // rows of up to 102400 logits in registers
+
 // loss = sum of the terms (fixed order, fp64) / count, one workgroup
 __global__ __launch_bounds__(256) void ce_reduce_kernel(const float* term, int64_t rows, float inv_count, float* loss) {
     __shared__ double red[256];
@@ -437,7 +505,10 @@ int launch_ce_loss(const float* logits, const int32_t* target, float* term, floa
                    int count, hipStream_t s) {
     const float inv = count > 0 ? 1.0f / (float)count : __builtin_nanf("");  // 0 / 0 as in the reference
     const bool vec = V % 4 == 0 && ((uintptr_t)logits | (uintptr_t)grad) % 16 == 0;
-    if (vec) hipLaunchKernelGGL(ce_rows_kernel<true>, dim3(rows), dim3(256), 0, s, logits, target, term, grad, V, inv);
+    if (vec && V / 4 <= 1024 * kCeChunks)
+        hipLaunchKernelGGL(ce_rows_reg_kernel<kCeChunks>, dim3(rows), dim3(1024), 0, s, logits, target, term, grad, V,
+                           inv);
+    else if (vec) hipLaunchKernelGGL(ce_rows_kernel<true>, dim3(rows), dim3(256), 0, s, logits, target, term, grad, V, inv);
     else hipLaunchKernelGGL(ce_rows_kernel<false>, dim3(rows), dim3(256), 0, s, logits, target, term, grad, V, inv);
     DT_HIP_TRY(hipGetLastError());
     hipLaunchKernelGGL(ce_reduce_kernel, dim3(1), dim3(256), 0, s, term, (int64_t)rows, inv, loss);

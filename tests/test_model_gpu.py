@@ -52,9 +52,10 @@ def test_params_round_trip(gpu, params, model):
         assert np.array_equal(model.param(name), params[name]), name
 
 
-@pytest.mark.parametrize("on_device,V", [(True, 1000), (False, 1000), (True, 999)])  # 999: the scalar row path
+# 1000: rows held in registers; 999: the scalar row path; 102404: rows too long for registers, two float4 passes
+@pytest.mark.parametrize("on_device,V", [(True, 1000), (False, 1000), (True, 999), (True, 102404)])
 def test_ce_loss_and_gradient(gpu, on_device, V):
-    B, T = 3, 70
+    B, T = (3, 70) if V < 10000 else (3, 9)
     logits = synth.normal(6201, (B, T, V), 0.0, 3.0)
     tok = synth.model_tokens(B, T, V, seed=6202)
     tok[1, 40:] = PAD  # right padding (main.cpp:46-57)
@@ -62,12 +63,14 @@ def test_ce_loss_and_gradient(gpu, on_device, V):
     ref_loss, ref_g = oracle.ce_loss(logits, tok, PAD, with_grad=True)
     src = torch.from_numpy(logits).to(gpu) if on_device else logits
     loss, g = ce_loss(src, tok, PAD, with_grad=True)
-    assert abs(loss - ref_loss) <= 1e-5 * abs(ref_loss)
-    assert rel_err(to_np(g), ref_g) <= 1e-5
+    # (the two-pass path's per-thread sums run over 400 terms: fp32 rounding of sum exp reaches ~3e-5 there)
+    tol = 1e-5 if V < 10000 else 1e-4
+    assert abs(loss - ref_loss) <= tol * abs(ref_loss)
+    assert rel_err(to_np(g), ref_g) <= tol
     assert ce_loss(src, tok, PAD) == loss
 
 
-@pytest.mark.parametrize("V", [1000, 999])
+@pytest.mark.parametrize("V", [1000, 999, 102404])
 def test_ce_loss_gradient_in_place(gpu, V):
     """d_logits == logits, as main.cpp reuses probs for the gradient (main.cpp:62-80): same loss and gradient
     as with separate buffers."""
@@ -83,8 +86,9 @@ def test_ce_loss_gradient_in_place(gpu, V):
     tok32 = np.ascontiguousarray(tok, np.int32)
     _capi.call("dt_ce_loss", default_context(0).handle, buf.data_ptr(), tok32.ctypes.data, B, T, V, PAD,
                loss.ctypes.data, buf.data_ptr(), _capi.DT_MEM_DEVICE, torch.cuda.current_stream().cuda_stream)
-    assert abs(float(loss[0]) - ref_loss) <= 1e-5 * abs(ref_loss)
-    assert rel_err(to_np(buf), ref_g) <= 1e-5
+    tol = 1e-5 if V < 10000 else 1e-4  # as in test_ce_loss_and_gradient
+    assert abs(float(loss[0]) - ref_loss) <= tol * abs(ref_loss)
+    assert rel_err(to_np(buf), ref_g) <= tol
 
 
 def test_ce_loss_without_targets_is_nan(gpu):
