@@ -45,6 +45,47 @@ __global__ __launch_bounds__(256) void embed_gather_kernel(const int32_t* tok, c
     for (int i = threadIdx.x; i < dm / 4; i += 256) dst[i] = src[i];
 }
 
+// The same for rows of dm = 1024 * kChunks: the row stays in registers (kChunks float4 per thread) between the
+// sum of squares and the output pass instead of being read a second time.
+template <int kChunks>
+__global__ __launch_bounds__(256) void rmsnorm_rows_reg_kernel(const float* a, const float* w, const float* res,
+                                                               float* out, uint16_t* out16, float* y_save,
+                                                               float* rms_save, int dm, float eps) {
+    __shared__ float red[4];
+    const int64_t row = blockIdx.x;
+    const float* ar = a + row * dm;
+    float4 v[kChunks];
+    float ss = 0.0f;
+#pragma unroll
+    for (int c = 0; c < kChunks; ++c) {
+        v[c] = *reinterpret_cast<const float4*>(ar + 4 * threadIdx.x + 1024 * c);
+        ss += v[c].x * v[c].x + v[c].y * v[c].y + v[c].z * v[c].z + v[c].w * v[c].w;
+    }
+    ss = block_sum(ss, red);
+    const float rms = sqrtf(ss / (float)dm + eps);
+    if (rms_save && threadIdx.x == 0) rms_save[row] = rms;
+#pragma unroll
+    for (int c = 0; c < kChunks; ++c) {
+        const int i = 4 * threadIdx.x + 1024 * c;
+        const float4 wv = *reinterpret_cast<const float4*>(w + i);
+        const float4 y = make_float4((v[c].x / rms) * wv.x, (v[c].y / rms) * wv.y, (v[c].z / rms) * wv.z,
+                                     (v[c].w / rms) * wv.w);
+        if (y_save) *reinterpret_cast<float4*>(y_save + row * dm + i) = y;
+        float4 o = y;
+        if (res) {
+            const float4 r = *reinterpret_cast<const float4*>(res + row * dm + i);
+            o = make_float4(r.x + y.x, r.y + y.y, r.z + y.z, r.w + y.w);
+        }
+        *reinterpret_cast<float4*>(out + row * dm + i) = o;
+        if (out16) {
+            uint2 p;
+            p.x = pack_bf16x2(o.x, o.y);
+            p.y = pack_bf16x2(o.z, o.w);
+            *reinterpret_cast<uint2*>(out16 + row * dm + i) = p;
+        }
+    }
+}
+
 // out = res + (a / rms) * w (res may be null); y_save = (a / rms) * w, rms_save = rms (either may be null);
 // out16 (nullable) receives a bf16 copy of out
 __global__ __launch_bounds__(256) void rmsnorm_rows_kernel(const float* a, const float* w, const float* res, float* out,
@@ -484,8 +525,12 @@ int launch_embed_gather(const int32_t* tok, const float* E, float* x, int rows, 
 
 int launch_rmsnorm_rows(const float* a, const float* w, const float* res, float* out, uint16_t* out16, float* y_save,
                         float* rms_save, int rows, int dm, float eps, hipStream_t s) {
-    hipLaunchKernelGGL(rmsnorm_rows_kernel, dim3(rows), dim3(256), 0, s, a, w, res, out, out16, y_save, rms_save, dm,
-                       eps);
+    if (dm == 2048)
+        hipLaunchKernelGGL(rmsnorm_rows_reg_kernel<2>, dim3(rows), dim3(256), 0, s, a, w, res, out, out16, y_save,
+                           rms_save, dm, eps);
+    else
+        hipLaunchKernelGGL(rmsnorm_rows_kernel, dim3(rows), dim3(256), 0, s, a, w, res, out, out16, y_save, rms_save,
+                           dm, eps);
     DT_HIP_TRY(hipGetLastError());
     return DT_OK;
 }
