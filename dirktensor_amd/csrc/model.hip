@@ -600,18 +600,21 @@ static int model_bwd(dt_model* M, const float* d_logits, int mem, void* stream, 
         return launch_colsum(part, nblk, dm, g, side, !fresh);
     };
 
-    // LM head (OlmoLmHead.cpp:30-62): dW += d_logits^T y; d_y = d_logits W
+    // LM head (OlmoLmHead.cpp:30-62): d_y = d_logits W; dW += d_logits^T y. The side stream starts dW only once d_y
+    // is formed, so the chain's largest product runs alone and dW runs beside the first blocks' backward (the
+    // other weight gradients start with their blocks' input-gradient products; placed after them they measured
+    // slower)
     float* d_yf = da;
     writing = true;
     if (bf) {
         DT_TRY(launch_f32_to_bf16(gl, d16, (int64_t)rows * V, s));
+        DT_TRY(gemm_rm(ctx, s, false, false, rows, dm, V, d16, V, M->lm_head16, dm, 0.0f, d_yf, dm, true));
         DT_TRY(fork());
         DT_TRY(gemm_rm(ctx, sw, true, false, V, dm, rows, d16, V, M->yf16.ptr, dm, gb, M->g_lm, dm, true));
-        DT_TRY(gemm_rm(ctx, s, false, false, rows, dm, V, d16, V, M->lm_head16, dm, 0.0f, d_yf, dm, true));
     } else {
+        DT_TRY(gemm_rm(ctx, s, false, false, rows, dm, V, gl, V, M->lm_head, dm, 0.0f, d_yf, dm, false));
         DT_TRY(fork());
         DT_TRY(gemm_rm(ctx, sw, true, false, V, dm, rows, gl, V, M->yf.ptr, dm, gb, M->g_lm, dm, false));
-        DT_TRY(gemm_rm(ctx, s, false, false, rows, dm, V, gl, V, M->lm_head, dm, 0.0f, d_yf, dm, false));
     }
     // final norm (OlmoModel.cpp:52): RMSNorm::backward from the saved output y and rms
     DT_TRY(launch_rmsnorm_bwd(d_yf, static_cast<const float*>(M->yf.ptr), static_cast<const float*>(M->rmsf.ptr),
